@@ -1,0 +1,184 @@
+/* SPDX-License-Identifier: Apache-2.0
+ *
+ * kvq_hip.h -- C ABI of libkvq_hip.so, the MI355X (gfx950) kernels of the
+ * quantized-KV hot path.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer owned by the caller (the Python layer
+ *     allocates through torch); the library never allocates.  Workspaces are
+ *     passed in and their sizes are given by the *_workspace_bytes helpers.
+ *   - Sizes are int64_t, geometry is int; dtype and index-width arguments use
+ *     the enums below.  `stream` is a hipStream_t passed as void*.
+ *   - Return 0 on success; KVQ_ERR_* (< 0) for rejected arguments; a positive
+ *     hipError_t if the launch failed.  Nothing is launched when an argument
+ *     is rejected.
+ *   - Calls are asynchronous on `stream` and reentrant (no global mutable
+ *     state).
+ *
+ * Reference paths are relative to /root/reference with
+ * pkg/ = src/vllm_ascend_quantized_kv_cache/; each entry point names the
+ * reference interface it replaces.
+ */
+#ifndef KVQ_HIP_H_
+#define KVQ_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  KVQ_DTYPE_F32 = 0,
+  KVQ_DTYPE_F16 = 1,
+  KVQ_DTYPE_BF16 = 2,
+};
+
+enum {
+  KVQ_INDEX_I32 = 0,
+  KVQ_INDEX_I64 = 1,
+};
+
+enum {
+  KVQ_OK = 0,
+  KVQ_ERR_INVALID = -1,     /* bad pointer, dtype or size */
+  KVQ_ERR_GEOMETRY = -2,    /* geometry the kernels do not support */
+};
+
+/* ABI version: bumped whenever a signature below changes. */
+int kvq_abi_version(void);
+
+/* ---- KIVI INT4 ---------------------------------------------------------- */
+
+/* Key pack: token groups of `group_size` tokens -> k_quant [NB,KVH,D,Bs/8]
+ * int32 words (lane = block offset % 8), k_scale/k_mn [NB,KVH,D,Bs/G] fp32.
+ * Replaces kivi_pack_key_cache (pkg/ops/triton/kivi_pack.py:287-348) and its
+ * kernel (:134-226).
+ * Token t of the batch reads source row r = src_index ? src_index[t] : t from
+ * src_a (rows [0, n_a)) or src_b (rows >= n_a, index r - n_a); rows are
+ * [KVH, D] contiguous of `src_dtype`.  num_tokens % group_size == 0; each
+ * group's slots must be contiguous, group aligned and inside one block (the
+ * caller validates); a group whose first slot is negative is skipped. */
+int kvq_kivi_pack_key(const void* src_a, int64_t n_a, const void* src_b,
+                      const int64_t* src_index, int src_dtype,
+                      const void* slot_mapping, int slot_index_type, int64_t num_tokens,
+                      int num_kv_heads, int head_size, int group_size, int block_size,
+                      int32_t* k_quant, float* k_scale, float* k_mn, void* stream);
+
+/* Value pack: per (token, head, head-dim group) -> v_quant [NB,Bs,KVH,D/8]
+ * int32 (lane = dim % 8), v_scale/v_mn [NB,Bs,KVH,D/G] fp32.  Tokens with a
+ * negative slot are skipped.  Source rows as for kvq_kivi_pack_key.
+ * Replaces kivi_pack_value_cache (pkg/ops/triton/kivi_pack.py:229-284) and its
+ * kernel (:61-131). */
+int kvq_kivi_pack_value(const void* src_a, int64_t n_a, const void* src_b,
+                        const int64_t* src_index, int src_dtype,
+                        const void* slot_mapping, int slot_index_type, int64_t num_tokens,
+                        int num_kv_heads, int head_size, int group_size, int block_size,
+                        int32_t* v_quant, float* v_scale, float* v_mn, void* stream);
+
+/* Paged gather-dequant to dense TND with an optional residual-tail overlay.
+ * out_k/out_v are [cu_seqlens[batch], KVH, D] of `out_dtype`; request b owns
+ * rows [cu_seqlens[b], cu_seqlens[b+1]).  Negative block ids read block 0 and
+ * are masked by the sequence length.  Dequant is q*scale then +mn (two fp32
+ * roundings) then a round-to-nearest-even cast.
+ * Overlay (ring_k != NULL): ring_meta is int32 [batch, 5] =
+ *   {ring_row, k_first_lane, k_tail, v_first_lane, v_tail};
+ * the last k_tail rows of request b come from ring_k[ring_row, (k_first_lane
+ * + i) % ring_len] (i = 0..k_tail-1), likewise for values; ring tensors are
+ * [rows, ring_len, KVH, D] of `ring_dtype`.
+ * Replaces kivi_dequant_gather_cache (pkg/ops/kivi_gather.py:36-156) plus the
+ * overlay loop of _gather_dequant_kivi_paged_cache
+ * (pkg/methods/kivi_int4/attention_backend.py:849-935). */
+int kvq_kivi_gather_dequant(const int32_t* k_quant, const float* k_scale, const float* k_mn,
+                            const int32_t* v_quant, const float* v_scale, const float* v_mn,
+                            int64_t num_blocks, int block_size, int num_kv_heads,
+                            int head_size, int group_size,
+                            const void* block_table, int block_index_type, int64_t max_blocks,
+                            const int64_t* cu_seqlens, int64_t batch,
+                            const int32_t* ring_meta, const void* ring_k, const void* ring_v,
+                            int ring_dtype, int ring_len,
+                            void* out_k, void* out_v, int out_dtype, void* stream);
+
+/* Fused KIVI INT4 decode attention: one query token per request attends to
+ * its int4 history (dequantized in registers) and its full-precision residual
+ * window, split over a work list and merged with a log-sum-exp combine.
+ *   query/out   [batch, num_heads, D] of `q_dtype`
+ *   seq_meta    int32 [batch, 8] = {seq_len, k_hist, v_hist, ring_row,
+ *               k_first_lane, v_first_lane, first_work, num_work}
+ *               positions < k_hist (v_hist) read int4 keys (values); the
+ *               others read ring lane (first_lane + p - hist) % ring_len
+ *   work        int32 [num_work, 4] = {request, pos_begin, pos_end, kind}
+ *               kind 0: both sides int4 over the whole range (MFMA path);
+ *               kind 1: any mix of sources (generic path)
+ *   workspace   >= kvq_kivi_decode_workspace_bytes(num_work, num_heads, D)
+ *   block_table int32 [batch, max_blocks]
+ * Replaces the decode branch: _forward_kivi_paged_decode_attention
+ * (pkg/methods/kivi_int4/attention_backend.py:1193-1230), i.e. the gather of
+ * :849-935 followed by npu_fused_infer_attention_score (TND, sparse_mode 0). */
+int64_t kvq_kivi_decode_workspace_bytes(int64_t num_work, int num_heads, int head_size);
+int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batch, int num_heads,
+                         int num_kv_heads, int head_size, float scale,
+                         const int32_t* k_quant, const float* k_scale, const float* k_mn,
+                         const int32_t* v_quant, const float* v_scale, const float* v_mn,
+                         int64_t num_blocks, int block_size, int group_size,
+                         const int32_t* block_table, int64_t max_blocks,
+                         const int32_t* seq_meta, const int32_t* work, int64_t num_work,
+                         const void* ring_k, const void* ring_v, int ring_dtype, int ring_len,
+                         void* workspace, void* out, void* stream);
+
+/* ---- INT8 dynamic per-channel ------------------------------------------- */
+
+/* First-K/V scales in the activation dtype: amax over tokens per (head, dim),
+ * clamp_min(1e-12), inv = (1/amax)*127, aq = 1/inv, every step rounded to
+ * `dtype` as torch evaluates `127.0 / k_max` (reciprocal then multiply).
+ * key/value [num_tokens, KVH*D]; k_inv/v_inv/k_aq/v_aq [KVH*D] of `dtype`;
+ * amax_ws: uint32 [2*KVH*D] workspace (zeroed by this call).
+ * Replaces _prepare_int8_scales (pkg/methods/int8_dynamic/attention_backend.py:130-150)
+ * == Int8DynamicSemantics.calc_scales (pkg/methods/int8_dynamic/semantics.py:49-70). */
+int kvq_int8_calc_scales(const void* key, const void* value, int dtype, int64_t num_tokens,
+                         int64_t channels, uint32_t* amax_ws, void* k_inv, void* v_inv,
+                         void* k_aq, void* v_aq, void* stream);
+
+/* Quantize clamp(round_half_even(x*inv), -128, 127) (product rounded to
+ * `dtype`) and scatter by slot into key_cache/value_cache [NB,Bs,KVH,D] int8.
+ * Negative slots are padding and skipped.
+ * Replaces _quantize_kv_to_runtime_int8 (attention_backend.py:152-171) plus the
+ * host reshape_and_cache it feeds (attention_backend.py:86-88). */
+int kvq_int8_quant_scatter(const void* key, const void* value, int dtype,
+                           const void* k_inv, const void* v_inv,
+                           const void* slot_mapping, int slot_index_type, int64_t num_tokens,
+                           int64_t channels, int8_t* key_cache, int8_t* value_cache,
+                           int64_t num_blocks, int block_size, void* stream);
+
+/* Paged int8 -> dense TND in the activation dtype: (x - 0) * aq, rounded to
+ * `dtype`.  Rows of request b are [cu_seqlens[b], cu_seqlens[b+1]).
+ * Replaces _dequant_int8_paged_kv_to_dense (attention_backend.py:370-404). */
+int kvq_int8_dequant_gather(const int8_t* key_cache, const int8_t* value_cache,
+                            int64_t num_blocks, int block_size, int num_kv_heads, int head_size,
+                            const void* k_aq, const void* v_aq, int dtype,
+                            const int32_t* block_table, int64_t max_blocks,
+                            const int64_t* cu_seqlens, int64_t batch,
+                            void* out_k, void* out_v, void* stream);
+
+/* Fused INT8 decode attention with per-channel antiquant (offset 0):
+ * K = int8 * k_aq[h, d], V = int8 * v_aq[h, d].
+ *   query/out [batch, num_heads, D] of `dtype`; k_aq/v_aq [KVH*D] of `dtype`
+ *   seq_meta int32 [batch, 4] = {seq_len, first_work, num_work, unused}
+ *   work     int32 [num_work, 4] = {request, pos_begin, pos_end, kind}
+ * Replaces _forward_int8_decode (attention_backend.py:173-205):
+ * npu_fused_infer_attention_score BNSD with key/value_antiquant_scale. */
+int64_t kvq_int8_decode_workspace_bytes(int64_t num_work, int num_heads, int head_size);
+int kvq_int8_decode_attn(const void* query, int dtype, int64_t batch, int num_heads,
+                         int num_kv_heads, int head_size, float scale,
+                         const int8_t* key_cache, const int8_t* value_cache,
+                         int64_t num_blocks, int block_size,
+                         const void* k_aq, const void* v_aq,
+                         const int32_t* block_table, int64_t max_blocks,
+                         const int32_t* seq_meta, const int32_t* work, int64_t num_work,
+                         void* workspace, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVQ_HIP_H_ */

@@ -1,0 +1,202 @@
+# SPDX-License-Identifier: Apache-2.0
+"""GPU parity of the KIVI INT4 HIP kernels against the CPU oracle.
+
+Codes, scales and mins must be bit-exact; gathered K/V bit-exact after the
+round-to-nearest-even cast; fused decode attention within atol/rtol 1e-2 of
+the oracle's dequant followed by fp32 SDPA.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import kvq_oracle as ref
+from tests._util import empty_kivi_caches, make_kv, shuffled_table, slots_for, to_dev
+
+pytestmark = pytest.mark.gpu
+
+# (head_size, kv_heads, group_size, block_size) -- the reference's geometry sweep
+GEOMS = [(32, 2, 8, 16), (64, 4, 16, 32), (128, 8, 128, 128), (128, 4, 32, 64), (256, 2, 64, 64),
+         (256, 1, 128, 128), (128, 8, 64, 128)]
+
+
+def _packs(dev, d, kvh, g, bs, dtype, seed, n_groups=5):
+    from vllm_ascend_quantized_kv_cache.ops.kivi_pack import (
+        kivi_pack_key_cache,
+        kivi_pack_value_cache,
+    )
+
+    nb = n_groups * g // bs + 3
+    t = n_groups * g
+    key, value = make_kv(t, kvh, d, dtype=dtype, seed=seed)
+    # groups land in shuffled blocks, group-aligned inside each block
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(seed))
+    gpb = bs // g
+    slots = []
+    for gi in range(n_groups):
+        blk = int(perm[gi // gpb])
+        off = (gi % gpb) * g
+        slots.extend(range(blk * bs + off, blk * bs + off + g))
+    slots = torch.tensor(slots, dtype=torch.int64)
+    vslots = slots.clone()
+    vslots[3] = -1  # value padding token must be skipped
+    cpu = empty_kivi_caches(nb, bs, kvh, d, g, fill=7)
+    gpu = to_dev(cpu, dev)
+    ref.pack_key_cache(key, slots, cpu[0], cpu[1], cpu[2], g)
+    ref.pack_value_cache(value, vslots, cpu[3], cpu[4], cpu[5], g)
+    kivi_pack_key_cache(key.to(dev), slots.to(dev), gpu[0], gpu[1], gpu[2], g)
+    kivi_pack_value_cache(value.to(dev), vslots.to(torch.int32).to(dev), gpu[3], gpu[4], gpu[5], g)
+    return cpu, gpu
+
+
+@pytest.mark.parametrize("d,kvh,g,bs", GEOMS)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_pack_bit_exact(gpu_device, d, kvh, g, bs, dtype):
+    cpu, gpu = _packs(gpu_device, d, kvh, g, bs, dtype, seed=d + g + bs)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("kq", "ks", "km", "vq", "vs", "vm"), cpu, gpu):
+        b = b.cpu()
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"{name} differs"
+
+
+def test_pack_config1_bit_exact(gpu_device):
+    """896 packed tokens, 8 heads, D=G=Bs=128."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_pack import (
+        kivi_pack_key_cache,
+        kivi_pack_value_cache,
+    )
+
+    d, kvh, g, bs, nb = 128, 8, 128, 128, 8
+    key, value = make_kv(1024, kvh, d, seed=0)
+    table = torch.arange(nb, dtype=torch.int32)
+    slots = slots_for(table, range(896), bs)
+    cpu = empty_kivi_caches(nb, bs, kvh, d, g)
+    gpu = to_dev(cpu, gpu_device)
+    ref.pack_key_cache(key[:896], slots, *cpu[:3], g)
+    ref.pack_value_cache(value[:896], slots, *cpu[3:], g)
+    kivi_pack_key_cache(key[:896].to(gpu_device), slots.to(gpu_device), *gpu[:3], g)
+    kivi_pack_value_cache(value[:896].to(gpu_device), slots.to(gpu_device), *gpu[3:], g)
+    torch.cuda.synchronize()
+    for a, b in zip(cpu, gpu):
+        assert torch.equal(a.view(torch.int32), b.cpu().view(torch.int32))
+
+
+@pytest.mark.parametrize("d,kvh,g,bs", GEOMS)
+def test_gather_bit_exact(gpu_device, d, kvh, g, bs):
+    from vllm_ascend_quantized_kv_cache.ops.kivi_gather import kivi_dequant_gather_cache
+
+    cpu, gpu = _packs(gpu_device, d, kvh, g, bs, torch.bfloat16, seed=11 + d, n_groups=8)
+    nb = cpu[0].shape[0]
+    # three ragged requests over a shuffled table; unused columns hold -1
+    maxb = 4
+    table = torch.full((3, maxb), -1, dtype=torch.int32)
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(5))
+    lens = [min(maxb * bs, 3 * bs + 5), bs - 3, 1]
+    used = 0
+    for r, n in enumerate(lens):
+        nblk = -(-n // bs)
+        table[r, :nblk] = perm[used : used + nblk]
+        used += nblk
+    seq = torch.tensor(lens, dtype=torch.int64)
+    for out_dtype in (torch.bfloat16, torch.float32, torch.float16):
+        want_k, want_v = ref.dequant_gather(*cpu, table, seq, out_dtype, g)
+        got_k, got_v = kivi_dequant_gather_cache(
+            *gpu, table.to(gpu_device), seq.to(gpu_device), out_dtype, g
+        )
+        assert torch.equal(want_k, got_k.cpu()), out_dtype
+        assert torch.equal(want_v, got_v.cpu()), out_dtype
+
+
+def _ring_case(dev, d, kvh, g, bs, r_len, lens, seed, ring_dtype=torch.float32):
+    """Packed history for several requests plus residual rings (FIFO, wrapped)."""
+    nb = sum(-(-n // bs) for n in lens) + 2
+    maxb = max(-(-n // bs) for n in lens)
+    table = torch.full((len(lens), maxb), -1, dtype=torch.int32)
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(seed))
+    used = 0
+    for r, n in enumerate(lens):
+        nblk = -(-n // bs)
+        table[r, :nblk] = perm[used : used + nblk]
+        used += nblk
+    cpu = empty_kivi_caches(nb, bs, kvh, d, g)
+    ring_k = torch.zeros(len(lens) + 1, r_len, kvh, d, dtype=ring_dtype)
+    ring_v = torch.zeros_like(ring_k)
+    seqs, windows_k, windows_v, keys, values = [], [], [], [], []
+    gen = torch.Generator().manual_seed(seed + 1)
+    for b, n in enumerate(lens):
+        key, value = make_kv(n, kvh, d, seed=seed * 31 + b)
+        keys.append(key)
+        values.append(value)
+        hk, hv = ref.incremental_split(n, r_len)
+        slots = slots_for(table[b], range(n), bs)
+        if hk:
+            ref.pack_key_cache(key[:hk], slots[:hk], *cpu[:3], g)
+        if hv:
+            ref.pack_value_cache(value[:hv], slots[:hv], *cpu[3:], g)
+        row = len(lens) - b  # rows need not follow request order
+        ks_ = int(torch.randint(0, r_len, (1,), generator=gen))  # ring start
+        vs_ = int(torch.randint(0, r_len, (1,), generator=gen))
+        tk, tv = n - hk, n - hv
+        for i in range(tk):
+            ring_k[row, (ks_ + i) % r_len] = key[hk + i].to(ring_dtype)
+        for i in range(tv):
+            ring_v[row, (vs_ + i) % r_len] = value[hv + i].to(ring_dtype)
+        seqs.append((n, hk, hv, row, ks_, vs_))
+        windows_k.append(key[hk:])
+        windows_v.append(value[hv:])
+    return cpu, table, ring_k, ring_v, seqs, windows_k, windows_v, keys, values
+
+
+@pytest.mark.parametrize("d,kvh,g,bs", GEOMS)
+def test_gather_with_residual_overlay(gpu_device, d, kvh, g, bs):
+    from vllm_ascend_quantized_kv_cache.ops.kivi_gather import gather_dequant_with_residual
+
+    r_len = max(g, 2 * g if g <= 64 else g)
+    lens = [r_len * 3 + 5, r_len // 2, r_len + 1, 2 * r_len]
+    cpu, table, ring_k, ring_v, seqs, wk, wv, _, _ = _ring_case(
+        gpu_device, d, kvh, g, bs, r_len, lens, seed=3
+    )
+    seq_t = torch.tensor(lens)
+    want_k, want_v = ref.dequant_gather(*cpu, table, seq_t, torch.bfloat16, g)
+    want_k = ref.overlay_residual(want_k, lens, wk)
+    want_v = ref.overlay_residual(want_v, lens, wv)
+    meta = torch.tensor(
+        [[row, ks_, n - hk, vs_, n - hv] for (n, hk, hv, row, ks_, vs_) in seqs],
+        dtype=torch.int32,
+    )
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int64)
+    got_k, got_v = gather_dequant_with_residual(
+        to_dev(cpu, gpu_device), table.to(gpu_device), cu.to(gpu_device), sum(lens),
+        torch.bfloat16, g, meta.to(gpu_device), ring_k.to(gpu_device), ring_v.to(gpu_device),
+    )
+    assert torch.equal(want_k, got_k.cpu())
+    assert torch.equal(want_v, got_v.cpu())
+
+
+@pytest.mark.parametrize("d,kvh,g,bs", GEOMS)
+@pytest.mark.parametrize("rep", [1, 5])
+def test_decode_attention_matches_oracle(gpu_device, d, kvh, g, bs, rep):
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import DecodeSeq, kivi_decode_attention
+
+    r_len = 2 * g if g <= 64 else g
+    lens = [r_len * 4 + 7, r_len + 1, 5, 3 * r_len, r_len * 6]
+    cpu, table, ring_k, ring_v, seqs, wk, wv, _, _ = _ring_case(
+        gpu_device, d, kvh, g, bs, r_len, lens, seed=9, ring_dtype=torch.bfloat16
+    )
+    hq = kvh * rep
+    q = torch.randn(len(lens), hq, d, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    scale = d ** -0.5
+    # the reference gather in fp32 (its exact dequant values), then fp32 SDPA;
+    # a bf16 target would add the reference's own intermediate rounding
+    dk, dv = ref.dequant_gather(*cpu, table, torch.tensor(lens), torch.float32, g)
+    dk = ref.overlay_residual(dk, lens, wk)
+    dv = ref.overlay_residual(dv, lens, wv)
+    want = ref.attention(q, dk, dv, [1] * len(lens), lens, scale, causal=True)
+    dseqs = [DecodeSeq(n, hk, hv, row, ks_, vs_) for (n, hk, hv, row, ks_, vs_) in seqs]
+    for split in (None, 64, 256):
+        got = kivi_decode_attention(
+            q.to(gpu_device), to_dev(cpu, gpu_device), table.to(gpu_device), dseqs,
+            ring_k.to(gpu_device), ring_v.to(gpu_device), scale, g, split_tokens=split,
+        )
+        torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)

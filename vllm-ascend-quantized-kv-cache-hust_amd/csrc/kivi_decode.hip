@@ -1,0 +1,280 @@
+// SPDX-License-Identifier: Apache-2.0
+// Fused KIVI INT4 decode attention for MI355X (gfx950): split-K over a work
+// list, log-sum-exp combine.
+//
+// The reference gathers the whole int4 history into a dense bf16 tensor and
+// calls the NPU fused-attention op (pkg/methods/kivi_int4/attention_backend.py:
+// 849-935, 1193-1230).  Here the history is dequantized in registers inside
+// the attention kernel; positions past a side's int4 history read that
+// side's residual ring directly, so nothing dense is ever materialized.
+//
+// Work items (built by the host from the request lengths, no device sync):
+//   kind 0: a range where keys and values both come from int4 pages -- the
+//           MFMA kernel of kivi_decode_mfma.hip;
+//   kind 1: any range (tails where one side is already in the ring, and
+//           geometries the MFMA kernel does not cover) -- the generic kernel
+//           below: one wave per (work item, kv head), the QK dot products
+//           lane-per-position, the PV accumulation lane-per-dim.
+// Each work item leaves (m, l, o[D]) per query head in the workspace (m in
+// the log2 domain); kvq_decode_combine merges a request's items.
+#include "kvq_common.h"
+#include "kvq_decode.h"
+
+namespace {
+
+using namespace kvq;
+
+constexpr int kMaxRep = 16;   // query heads per kv head handled by the generic kernel
+constexpr int kMaxDpl = 4;    // dims per lane (head_size <= 256)
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+template <typename TQ, typename TR>
+__global__ void __launch_bounds__(64)
+kivi_decode_generic_kernel(const TQ* __restrict__ query, int hq, int kvh, int d, float qscale,
+                           const int32_t* __restrict__ kq, const float* __restrict__ ks,
+                           const float* __restrict__ km, const int32_t* __restrict__ vq,
+                           const float* __restrict__ vs, const float* __restrict__ vm, int bs,
+                           int g, const int32_t* __restrict__ block_table, int64_t maxb,
+                           const int32_t* __restrict__ seq_meta,
+                           const int32_t* __restrict__ work, const TR* __restrict__ ring_k,
+                           const TR* __restrict__ ring_v, int ring_len,
+                           float* __restrict__ ws_o, float* __restrict__ ws_ml,
+                           int skip_kind0) {
+  const int wi = blockIdx.x;
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
+  if (skip_kind0 && wk[3] == 0) return;  // the MFMA kernel owns these items
+  const int b = wk[0];
+  const int pb = wk[1];
+  const int pe = wk[2];
+  const int32_t* sm = seq_meta + 8 * static_cast<int64_t>(b);
+  const int khist = sm[1], vhist = sm[2], row = sm[3], kfirst = sm[4], vfirst = sm[5];
+  const int rep = hq / kvh;
+  const int dpl = (d + 63) / 64;
+  const int words = d / 8;
+  const int ng = d / g;
+  const int gpb = bs / g;
+  const int wpd = bs / 8;
+  const int32_t* bt = block_table + static_cast<int64_t>(b) * maxb;
+
+  __shared__ float s_q[kMaxRep * 256];
+  __shared__ float s_p[kMaxRep * 64];
+  for (int i = lane; i < rep * d; i += 64) {
+    const int r = i / d;
+    const int c = i - r * d;
+    s_q[i] = to_f32(query[(static_cast<int64_t>(b) * hq + h * rep + r) * d + c]) * qscale;
+  }
+  __syncthreads();
+
+  float m[kMaxRep], l[kMaxRep], acc[kMaxRep][kMaxDpl];
+#pragma unroll
+  for (int r = 0; r < kMaxRep; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMaxDpl; ++k) acc[r][k] = 0.0f;
+  }
+
+  for (int p0 = pb; p0 < pe; p0 += 64) {
+    const int p = p0 + lane;
+    const bool live = p < pe;
+    float s[kMaxRep];
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r) s[r] = 0.0f;
+    if (live) {
+      if (p < khist) {
+        int64_t blk = bt[p / bs];
+        if (blk < 0) blk = 0;
+        const int off = p % bs;
+        const int64_t base = (blk * kvh + h) * static_cast<int64_t>(d);
+        const uint32_t* wrow = reinterpret_cast<const uint32_t*>(kq) + base * wpd + off / 8;
+        const float* srow = ks + base * gpb + off / g;
+        const float* mrow = km + base * gpb + off / g;
+        const int shift = 4 * (off % 8);
+        for (int c = 0; c < d; ++c) {
+          const float kv = kivi_dequant((wrow[c * wpd] >> shift) & 0xfu, srow[c * gpb], mrow[c * gpb]);
+#pragma unroll
+          for (int r = 0; r < kMaxRep; ++r)
+            if (r < rep) s[r] += s_q[r * d + c] * kv;
+        }
+      } else {
+        const int rl = (kfirst + (p - khist)) % ring_len;
+        const TR* kr = ring_k + ((static_cast<int64_t>(row) * ring_len + rl) * kvh + h) * d;
+        for (int c = 0; c < d; ++c) {
+          const float kv = to_f32(kr[c]);
+#pragma unroll
+          for (int r = 0; r < kMaxRep; ++r)
+            if (r < rep) s[r] += s_q[r * d + c] * kv;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r) {
+      if (r >= rep) continue;
+      const float sr = live ? s[r] : -INFINITY;
+      const float m_new = fmaxf(m[r], wave_max(sr));
+      const float alpha = (m[r] == -INFINITY) ? 0.0f : exp2f(m[r] - m_new);
+      const float pr = live ? exp2f(sr - m_new) : 0.0f;
+      l[r] = l[r] * alpha + wave_sum(pr);
+#pragma unroll
+      for (int k = 0; k < kMaxDpl; ++k) acc[r][k] *= alpha;
+      m[r] = m_new;
+      s_p[r * 64 + lane] = pr;
+    }
+    __syncthreads();
+    const int n = (pe - p0) < 64 ? (pe - p0) : 64;
+    for (int i = 0; i < n; ++i) {
+      const int pp = p0 + i;
+      const bool from_int4 = pp < vhist;
+      int64_t vrow = 0;
+      const TR* vr = nullptr;
+      if (from_int4) {
+        int64_t blk = bt[pp / bs];
+        if (blk < 0) blk = 0;
+        vrow = (blk * bs + pp % bs) * kvh + h;
+      } else {
+        const int rl = (vfirst + (pp - vhist)) % ring_len;
+        vr = ring_v + ((static_cast<int64_t>(row) * ring_len + rl) * kvh + h) * d;
+      }
+#pragma unroll
+      for (int k = 0; k < kMaxDpl; ++k) {
+        const int c = lane + 64 * k;
+        if (k >= dpl || c >= d) continue;
+        float v;
+        if (from_int4) {
+          const uint32_t word = reinterpret_cast<const uint32_t*>(vq)[vrow * words + c / 8];
+          v = kivi_dequant((word >> (4 * (c % 8))) & 0xfu, vs[vrow * ng + c / g], vm[vrow * ng + c / g]);
+        } else {
+          v = to_f32(vr[c]);
+        }
+#pragma unroll
+        for (int r = 0; r < kMaxRep; ++r)
+          if (r < rep) acc[r][k] += s_p[r * 64 + i] * v;
+      }
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int r = 0; r < kMaxRep; ++r) {
+    if (r >= rep) continue;
+    const int64_t hh = static_cast<int64_t>(wi) * hq + h * rep + r;
+    if (lane == 0) {
+      ws_ml[2 * hh] = m[r];
+      ws_ml[2 * hh + 1] = l[r];
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxDpl; ++k) {
+      const int c = lane + 64 * k;
+      if (k < dpl && c < d) ws_o[hh * d + c] = acc[r][k];
+    }
+  }
+}
+
+}  // namespace
+
+namespace kvq {
+
+template <typename TO>
+__global__ void __launch_bounds__(64)
+decode_combine_kernel(int hq, int d, const int32_t* __restrict__ seq_meta, int meta_stride,
+                      int first_col, const float* __restrict__ ws_o,
+                      const float* __restrict__ ws_ml, TO* __restrict__ out) {
+  const int b = blockIdx.x;
+  const int hh = blockIdx.y;
+  const int32_t* sm = seq_meta + static_cast<int64_t>(meta_stride) * b;
+  const int fw = sm[first_col];
+  const int nw = sm[first_col + 1];
+  float mx = -INFINITY;
+  for (int s = 0; s < nw; ++s) mx = fmaxf(mx, ws_ml[2 * (static_cast<int64_t>(fw + s) * hq + hh)]);
+  float wsum = 0.0f;
+  for (int s = 0; s < nw; ++s) {
+    const int64_t idx = static_cast<int64_t>(fw + s) * hq + hh;
+    const float ms = ws_ml[2 * idx];
+    if (ms != -INFINITY) wsum += exp2f(ms - mx) * ws_ml[2 * idx + 1];
+  }
+  const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+  for (int c = threadIdx.x; c < d; c += blockDim.x) {
+    float o = 0.0f;
+    for (int s = 0; s < nw; ++s) {
+      const int64_t idx = static_cast<int64_t>(fw + s) * hq + hh;
+      const float ms = ws_ml[2 * idx];
+      if (ms != -INFINITY) o += exp2f(ms - mx) * ws_o[idx * d + c];
+    }
+    out[(static_cast<int64_t>(b) * hq + hh) * d + c] = from_f32<TO>(o * inv);
+  }
+}
+
+int launch_decode_combine(int dtype, int64_t batch, int hq, int d, const int32_t* seq_meta,
+                          int meta_stride, int first_col, const float* ws_o,
+                          const float* ws_ml, void* out, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(batch), hq);
+  KVQ_DISPATCH_FLOAT(dtype, TO,
+    hipLaunchKernelGGL((decode_combine_kernel<TO>), grid, dim3(64), 0, s, hq, d, seq_meta,
+                       meta_stride, first_col, ws_o, ws_ml, static_cast<TO*>(out)));
+  KVQ_LAUNCH_CHECK();
+  return KVQ_OK;
+}
+
+}  // namespace kvq
+
+extern "C" int64_t kvq_kivi_decode_workspace_bytes(int64_t num_work, int num_heads,
+                                                   int head_size) {
+  return kvq::decode_workspace_bytes(num_work, num_heads, head_size);
+}
+
+extern "C" int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batch, int num_heads,
+                                    int num_kv_heads, int head_size, float scale,
+                                    const int32_t* k_quant, const float* k_scale,
+                                    const float* k_mn, const int32_t* v_quant,
+                                    const float* v_scale, const float* v_mn, int64_t num_blocks,
+                                    int block_size, int group_size, const int32_t* block_table,
+                                    int64_t max_blocks, const int32_t* seq_meta,
+                                    const int32_t* work, int64_t num_work, const void* ring_k,
+                                    const void* ring_v, int ring_dtype, int ring_len,
+                                    void* workspace, void* out, void* stream) {
+  if (batch == 0) return KVQ_OK;
+  if (!query || !k_quant || !k_scale || !k_mn || !v_quant || !v_scale || !v_mn ||
+      !block_table || !seq_meta || !work || !workspace || !out || batch < 0 || num_work <= 0 ||
+      num_blocks <= 0 || ring_len <= 0 || !ring_k || !ring_v)
+    return KVQ_ERR_INVALID;
+  if (num_kv_heads <= 0 || num_heads % num_kv_heads || group_size <= 0 || group_size % 8 ||
+      head_size % 8 || head_size % group_size || block_size % group_size || head_size > 256)
+    return KVQ_ERR_GEOMETRY;
+  if (num_heads / num_kv_heads > kMaxRep) return KVQ_ERR_GEOMETRY;
+  if (num_work > 0x7fffffff || batch > 0x7fffffff || num_heads > 65535) return KVQ_ERR_INVALID;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* ws_o = static_cast<float*>(workspace);
+  float* ws_ml = ws_o + num_work * num_heads * head_size;
+  const float qscale = scale * 1.4426950408889634f;  // fold log2(e): exp2 in the kernels
+
+  bool mfma = false;
+  int rc = kvq::launch_kivi_decode_mfma(query, q_dtype, num_heads, num_kv_heads, head_size,
+                                       qscale, k_quant, k_scale, k_mn, v_quant, v_scale, v_mn,
+                                       block_size, group_size, block_table, max_blocks, seq_meta,
+                                       work, num_work, ws_o, ws_ml, s, &mfma);
+  if (rc != KVQ_OK) return rc;
+  const dim3 grid(static_cast<unsigned>(num_work), num_kv_heads);
+  KVQ_DISPATCH_FLOAT(q_dtype, TQ,
+    KVQ_DISPATCH_FLOAT(ring_dtype, TR,
+      hipLaunchKernelGGL((kivi_decode_generic_kernel<TQ, TR>), grid, dim3(64), 0, s,
+                         static_cast<const TQ*>(query), num_heads, num_kv_heads, head_size,
+                         qscale, k_quant, k_scale, k_mn, v_quant, v_scale, v_mn, block_size,
+                         group_size, block_table, max_blocks, seq_meta, work,
+                         static_cast<const TR*>(ring_k), static_cast<const TR*>(ring_v),
+                         ring_len, ws_o, ws_ml, mfma ? 1 : 0)));
+  KVQ_LAUNCH_CHECK();
+  return kvq::launch_decode_combine(q_dtype, batch, num_heads, head_size, seq_meta, 8, 6, ws_o,
+                                    ws_ml, out, s);
+}

@@ -1,0 +1,257 @@
+// SPDX-License-Identifier: Apache-2.0
+// KIVI INT4 pack kernels for MI355X (gfx950).
+//
+// Key pack  (reference: pkg/ops/triton/kivi_pack.py:134-226)
+//   One workgroup per (token group, kv head).  Thread (tc, dv) owns an 8x8
+//   tile: 8 consecutive tokens x 8 consecutive dims, read as 8 16-byte rows
+//   (16 lanes cover one 256-byte head row, fully coalesced).  Per-dim min/max
+//   over the group's tokens go through LDS; each thread then quantizes its
+//   tile into 8 words (8 tokens of one dim per word) which are staged in LDS
+//   as [dim][chunk] and written back in address order.
+//
+// Value pack (reference: pkg/ops/triton/kivi_pack.py:61-131)
+//   One thread per output word (8 consecutive dims of one token-head row,
+//   a 16-byte load).  The head-dim group's min/max is a butterfly over the
+//   group's G/8 adjacent lanes (DPP/swizzle through __shfl_xor).
+#include "kvq_common.h"
+
+namespace {
+
+using namespace kvq;
+
+template <typename T>
+__device__ __forceinline__ const T* src_row(const T* a, int64_t n_a, const T* b, int64_t row,
+                                             int64_t row_elems) {
+  return row < n_a ? a + row * row_elems : b + (row - n_a) * row_elems;
+}
+
+template <typename T, typename I>
+__global__ void __launch_bounds__(1024)
+kivi_pack_key_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __restrict__ src_b,
+                     const int64_t* __restrict__ src_index, const I* __restrict__ slots,
+                     int kvh, int d, int g, int bs, int32_t* __restrict__ kq,
+                     float* __restrict__ ks, float* __restrict__ km) {
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * g;
+  const int h = blockIdx.y;
+  const int64_t first = ld_index(slots, t0);
+  if (first < 0) return;  // uniform across the workgroup
+  const int64_t blk = first / bs;
+  const int off = static_cast<int>(first - blk * bs);
+  const int nchunk = g / 8;
+  const int ndv = d / 8;
+  const int tiles = nchunk * ndv;
+
+  extern __shared__ float smem[];
+  float* s_mn = smem;                   // [nchunk][d]
+  float* s_mx = s_mn + nchunk * d;      // [nchunk][d]
+  float* s_scale = s_mx + nchunk * d;   // [d]
+  float* s_min = s_scale + d;           // [d]
+  uint32_t* s_words = reinterpret_cast<uint32_t*>(s_min + d);  // [d][nchunk]
+
+  const int tid = threadIdx.x;
+  const bool active = tid < tiles;
+  const int dv = active ? tid % ndv : 0;
+  const int tc = active ? tid / ndv : 0;
+  const int64_t row_elems = static_cast<int64_t>(kvh) * d;
+
+  float x[8][8];
+  if (active) {
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const int64_t t = t0 + tc * 8 + l;
+      const int64_t row = src_index ? src_index[t] : t;
+      load8(src_row(src_a, n_a, src_b, row, row_elems) + h * d + dv * 8, x[l]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float mn = x[0][j], mx = x[0][j];
+#pragma unroll
+      for (int l = 1; l < 8; ++l) {
+        mn = fmin_ordered(mn, x[l][j]);
+        mx = fmax_ordered(mx, x[l][j]);
+      }
+      s_mn[tc * d + dv * 8 + j] = mn;
+      s_mx[tc * d + dv * 8 + j] = mx;
+    }
+  }
+  __syncthreads();
+
+  const int64_t row_base = (blk * kvh + h) * static_cast<int64_t>(d);
+  const int groups_per_block = bs / g;
+  for (int c = tid; c < d; c += blockDim.x) {
+    float mn = s_mn[c], mx = s_mx[c];
+    for (int k = 1; k < nchunk; ++k) {
+      mn = fmin_ordered(mn, s_mn[k * d + c]);
+      mx = fmax_ordered(mx, s_mx[k * d + c]);
+    }
+    const float sc = kivi_group_scale(mn, mx);
+    s_scale[c] = sc;
+    s_min[c] = mn;
+    const int64_t sidx = (row_base + c) * groups_per_block + off / g;
+    ks[sidx] = sc;
+    km[sidx] = mn;
+  }
+  __syncthreads();
+
+  if (active) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = dv * 8 + j;
+      const float sc = s_scale[c];
+      const float mn = s_min[c];
+      uint32_t word = 0;
+#pragma unroll
+      for (int l = 0; l < 8; ++l) word |= kivi_quantize(x[l][j], mn, sc) << (4 * l);
+      s_words[c * nchunk + tc] = word;
+    }
+  }
+  __syncthreads();
+
+  const int words_per_dim = bs / 8;
+  const int total_words = d * nchunk;
+  uint32_t* out = reinterpret_cast<uint32_t*>(kq);
+  for (int i = tid; i < total_words; i += blockDim.x) {
+    const int c = i / nchunk;
+    const int w = i - c * nchunk;
+    out[(row_base + c) * words_per_dim + off / 8 + w] = s_words[i];
+  }
+}
+
+template <typename T, typename I>
+__global__ void __launch_bounds__(256)
+kivi_pack_value_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __restrict__ src_b,
+                       const int64_t* __restrict__ src_index, const I* __restrict__ slots,
+                       int64_t num_tokens, int kvh, int d, int g, int bs,
+                       int32_t* __restrict__ vq, float* __restrict__ vs,
+                       float* __restrict__ vm) {
+  const int words = d / 8;
+  const int gw = g / 8;  // lanes per head-dim group
+  const int64_t total = num_tokens * kvh * words;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const bool valid = gid < total;
+  const int64_t r = valid ? gid / words : 0;
+  const int w = static_cast<int>(gid - r * words);
+  const int64_t t = r / kvh;
+  const int h = static_cast<int>(r - t * kvh);
+  const int64_t row_elems = static_cast<int64_t>(kvh) * d;
+  const int64_t row = valid ? (src_index ? src_index[t] : t) : 0;
+  const T* base = src_row(src_a, n_a, src_b, row, row_elems) + h * d;
+
+  float x[8];
+  float mn = 0.0f, mx = 0.0f;
+  if (valid) {
+    load8(base + w * 8, x);
+    mn = x[0];
+    mx = x[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+      mn = fmin_ordered(mn, x[i]);
+      mx = fmax_ordered(mx, x[i]);
+    }
+  }
+  if ((gw & (gw - 1)) == 0 && gw <= 64) {
+    // groups are gw adjacent, gw-aligned lanes (d % g == 0 keeps rows aligned)
+    for (int o = 1; o < gw; o <<= 1) {
+      mn = fmin_ordered(mn, __shfl_xor(mn, o, 64));
+      mx = fmax_ordered(mx, __shfl_xor(mx, o, 64));
+    }
+  } else if (valid) {
+    // uneven group width: every lane of the group scans the whole group
+    const int g0 = (w / gw) * g;
+    float y[8];
+    load8(base + g0, y);
+    mn = y[0];
+    mx = y[0];
+    for (int k = 0; k < g; k += 8) {
+      load8(base + g0 + k, y);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        mn = fmin_ordered(mn, y[i]);
+        mx = fmax_ordered(mx, y[i]);
+      }
+    }
+  }
+  if (!valid) return;
+  const int64_t slot = ld_index(slots, t);
+  if (slot < 0) return;
+  const float sc = kivi_group_scale(mn, mx);
+  uint32_t word = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) word |= kivi_quantize(x[i], mn, sc) << (4 * i);
+  const int64_t blk = slot / bs;
+  const int64_t off = slot - blk * bs;
+  const int64_t orow = (blk * bs + off) * kvh + h;
+  reinterpret_cast<uint32_t*>(vq)[orow * words + w] = word;
+  if (w % gw == 0) {
+    const int64_t sidx = orow * (d / g) + w / gw;
+    vs[sidx] = sc;
+    vm[sidx] = mn;
+  }
+}
+
+bool kivi_geometry_ok(int kvh, int d, int g, int bs) {
+  return kvh > 0 && d > 0 && g > 0 && bs > 0 && g % 8 == 0 && d % 8 == 0 && d % g == 0 &&
+         bs % g == 0;
+}
+
+}  // namespace
+
+extern "C" int kvq_abi_version(void) { return 1; }
+
+extern "C" int kvq_kivi_pack_key(const void* src_a, int64_t n_a, const void* src_b,
+                                 const int64_t* src_index, int src_dtype,
+                                 const void* slot_mapping, int slot_index_type,
+                                 int64_t num_tokens, int num_kv_heads, int head_size,
+                                 int group_size, int block_size, int32_t* k_quant,
+                                 float* k_scale, float* k_mn, void* stream) {
+  if (num_tokens == 0) return KVQ_OK;
+  if (!src_a || !slot_mapping || !k_quant || !k_scale || !k_mn || num_tokens < 0)
+    return KVQ_ERR_INVALID;
+  if (!kivi_geometry_ok(num_kv_heads, head_size, group_size, block_size))
+    return KVQ_ERR_GEOMETRY;
+  if (num_tokens % group_size) return KVQ_ERR_INVALID;
+  if (!src_index && n_a < num_tokens) return KVQ_ERR_INVALID;
+  const int tiles = (group_size / 8) * (head_size / 8);
+  if (tiles > 1024) return KVQ_ERR_GEOMETRY;
+  const int threads = ((tiles + 63) / 64) * 64;
+  const size_t lds = sizeof(float) * (3 * (group_size / 8) * head_size + 2 * head_size);
+  if (lds > 160 * 1024) return KVQ_ERR_GEOMETRY;
+  const dim3 grid(static_cast<unsigned>(num_tokens / group_size), num_kv_heads);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  KVQ_DISPATCH_FLOAT(src_dtype, T,
+    KVQ_DISPATCH_INDEX(slot_index_type, I,
+      hipLaunchKernelGGL((kivi_pack_key_kernel<T, I>), grid, dim3(threads), lds, s,
+                         static_cast<const T*>(src_a), n_a, static_cast<const T*>(src_b),
+                         src_index, static_cast<const I*>(slot_mapping), num_kv_heads,
+                         head_size, group_size, block_size, k_quant, k_scale, k_mn)));
+  KVQ_LAUNCH_CHECK();
+  return KVQ_OK;
+}
+
+extern "C" int kvq_kivi_pack_value(const void* src_a, int64_t n_a, const void* src_b,
+                                   const int64_t* src_index, int src_dtype,
+                                   const void* slot_mapping, int slot_index_type,
+                                   int64_t num_tokens, int num_kv_heads, int head_size,
+                                   int group_size, int block_size, int32_t* v_quant,
+                                   float* v_scale, float* v_mn, void* stream) {
+  if (num_tokens == 0) return KVQ_OK;
+  if (!src_a || !slot_mapping || !v_quant || !v_scale || !v_mn || num_tokens < 0)
+    return KVQ_ERR_INVALID;
+  if (!kivi_geometry_ok(num_kv_heads, head_size, group_size, block_size))
+    return KVQ_ERR_GEOMETRY;
+  if (!src_index && n_a < num_tokens) return KVQ_ERR_INVALID;
+  const int64_t total = num_tokens * num_kv_heads * (head_size / 8);
+  const int threads = 256;
+  const int64_t blocks = (total + threads - 1) / threads;
+  if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  KVQ_DISPATCH_FLOAT(src_dtype, T,
+    KVQ_DISPATCH_INDEX(slot_index_type, I,
+      hipLaunchKernelGGL((kivi_pack_value_kernel<T, I>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(threads), 0, s, static_cast<const T*>(src_a), n_a,
+                         static_cast<const T*>(src_b), src_index,
+                         static_cast<const I*>(slot_mapping), num_tokens, num_kv_heads,
+                         head_size, group_size, block_size, v_quant, v_scale, v_mn)));
+  KVQ_LAUNCH_CHECK();
+  return KVQ_OK;
+}

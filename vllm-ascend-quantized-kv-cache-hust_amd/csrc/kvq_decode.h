@@ -1,0 +1,39 @@
+// SPDX-License-Identifier: Apache-2.0
+// Internal interfaces shared by the decode-attention translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kvq {
+
+// Workspace: o [num_work, num_heads, D] fp32, then (m, l) [num_work, num_heads, 2].
+inline int64_t decode_workspace_bytes(int64_t num_work, int num_heads, int head_size) {
+  return num_work * num_heads * (static_cast<int64_t>(head_size) + 2) *
+         static_cast<int64_t>(sizeof(float));
+}
+
+// Launch the MFMA kernel for the kind-0 work items when the geometry is one it
+// covers; *launched tells the caller whether kind-0 items still need the
+// generic kernel.
+int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int d, float qscale,
+                            const int32_t* kq, const float* ks, const float* km,
+                            const int32_t* vq, const float* vs, const float* vm, int bs, int g,
+                            const int32_t* block_table, int64_t maxb, const int32_t* seq_meta,
+                            const int32_t* work, int64_t num_work, float* ws_o, float* ws_ml,
+                            hipStream_t s, bool* launched);
+
+// INT8 counterpart: kind-0 items (all positions in int8 pages) on MFMA.
+int launch_int8_decode_mfma(const void* query, int dtype, int hq, int kvh, int d, float qscale,
+                            const int8_t* kc, const int8_t* vc, int bs, const void* k_aq,
+                            const void* v_aq, const int32_t* block_table, int64_t maxb,
+                            const int32_t* work, int64_t num_work, float* ws_o, float* ws_ml,
+                            hipStream_t s, bool* launched);
+
+// Merge each request's work items: out = sum_s 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s.
+// seq_meta row b holds (first_work, num_work) at columns first_col, first_col+1.
+int launch_decode_combine(int dtype, int64_t batch, int hq, int d, const int32_t* seq_meta,
+                          int meta_stride, int first_col, const float* ws_o, const float* ws_ml,
+                          void* out, hipStream_t s);
+
+}  // namespace kvq
