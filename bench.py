@@ -1,0 +1,559 @@
+#!/usr/bin/env python
+# SPDX-License-Identifier: Apache-2.0
+"""Benchmark of the MI355X quantized-KV hot path (one GPU).
+
+Headline line (BASELINE.json metric, configs[2]): one KIVI INT4 decode step
+on Qwen2.5-14B geometry -- 32 sequences with context lengths ~U[2048, 16384],
+40 query / 8 KV heads, head_size 128, group 128, residual 128, block 128,
+shuffled pages.  A step appends one token per sequence to the residual ring,
+evicts the oldest value (and flushes a full key window) into int4 history,
+and runs fused INT4 decode attention.  Plans are built on the host before the
+timed region; the timed region is the device work only.
+
+``value`` = algorithmic bytes of the step / step time (GB/s).  ``roofline``
+covers the fused decode attention (the dominant kernel), timed with HIP
+events on its stream.  ``extra`` carries the other BASELINE configs: INT4
+pack and gather-dequant (config 4), INT8 decode (config 2), long-context INT4
+decode (config 5) and the config 1 round trip.  ``cpu_baseline`` times the
+CPU oracle (the reference algorithm restated in torch) on a bounded sample.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-extras] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "vllm-ascend-quantized-kv-cache-hust_amd"))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+METRIC = "INT4 pack/gather-dequant GB/s (% HBM peak); fused INT4 decode attn µs/layer"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# KIVI state builder (direct packs into the incremental-rule state)
+# ---------------------------------------------------------------------------
+
+
+class KiviState:
+    """Paged int4 history + residual rings for a batch of sequences on the GPU.
+
+    The state is the one the one-token-at-a-time writer leaves behind
+    (``hist_k = ((L-1)//R)*R``, ``hist_v = L - R``); it is built with direct
+    pack launches instead of replaying every token.
+    """
+
+    def __init__(self, torch, dev, lens, *, kvh, d, g, r, bs, spare_steps, seed, key_scales):
+        from vllm_ascend_quantized_kv_cache.methods.kivi_int4.byte_cache import (
+            KiviByteCacheLayout,
+            kivi_caches_from_byte_tensors,
+        )
+        from vllm_ascend_quantized_kv_cache.methods.kivi_int4.residual import KiviResidualRing
+        from vllm_ascend_quantized_kv_cache.ops.kivi_pack import (
+            pack_key_rows,
+            pack_value_rows,
+            ring_write,
+        )
+
+        self.torch = torch
+        self.dev = dev
+        self.lens = list(lens)
+        self.kvh, self.d, self.g, self.r, self.bs = kvh, d, g, r, bs
+        b = len(lens)
+        nblk = [-(-(n + spare_steps) // bs) for n in lens]
+        self.maxb = max(nblk)
+        nb = sum(nblk) + 8
+        self.layout = KiviByteCacheLayout(nb, bs, kvh, d, g)
+        s = self.layout.bytes_per_token_head
+        self.kbuf = torch.zeros((nb, bs, kvh, s), dtype=torch.uint8, device=dev)
+        self.vbuf = torch.zeros_like(self.kbuf)
+        self.caches = kivi_caches_from_byte_tensors(self.kbuf, self.vbuf, self.layout)
+        gen = torch.Generator().manual_seed(seed)
+        perm = torch.randperm(nb, generator=gen)
+        table = torch.zeros((b, self.maxb), dtype=torch.int32)
+        used = 0
+        for i, n in enumerate(nblk):
+            table[i, :n] = perm[used : used + n]
+            used += n
+        self.table_cpu = table
+        self.table = table.to(dev)
+        self.ring = KiviResidualRing(b, r, kvh, d, device=dev, dtype=torch.bfloat16)
+        self.key_scales = key_scales
+        gdev = torch.Generator(device=dev).manual_seed(seed + 1)
+        kq, ks, km, vq, vs, vm = self.caches
+        for i, n in enumerate(lens):
+            key = torch.randn((n, kvh, d), generator=gdev, device=dev) * key_scales
+            key = key.to(torch.bfloat16)
+            value = torch.randn((n, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
+            hk = ((n - 1) // r) * r if n else 0
+            hv = max(0, n - r)
+            slots = self.slots(i, 0, n)
+            if hk:
+                pack_key_rows(key, None, None, slots[:hk], kq, ks, km, g)
+            if hv:
+                pack_value_rows(value, None, None, slots[:hv], vq, vs, vm, g)
+            base = i * r
+            for is_key, h, src in ((True, hk, key), (False, hv, value)):
+                cnt = n - h
+                dst = torch.arange(base, base + cnt, device=dev, dtype=torch.int64)
+                rows = torch.arange(h, n, device=dev, dtype=torch.int64)
+                ring_write(self.ring.tensor(is_key), src, rows, dst)
+                lane_slots = [int(x) for x in self.slot_list(i, h, n)]
+                self.ring.start[is_key][i] = 0
+                self.ring.length[is_key][i] = cnt
+                ls = [-1] * r
+                ls[:cnt] = lane_slots
+                self.ring.lane_slot[is_key][i] = ls
+                self.ring.slot_lane[is_key][i] = {s_: j for j, s_ in enumerate(lane_slots)}
+            del key, value
+        self.ring.written = True
+        torch.cuda.synchronize()
+
+    def slot_list(self, i, p0, p1):
+        row = self.table_cpu[i].tolist()
+        return [row[p // self.bs] * self.bs + p % self.bs for p in range(p0, p1)]
+
+    def slots(self, i, p0, p1):
+        return self.torch.tensor(self.slot_list(i, p0, p1), dtype=self.torch.int64, device=self.dev)
+
+    def decode_seqs(self):
+        from vllm_ascend_quantized_kv_cache.ops.kivi_decode import DecodeSeq
+
+        out = []
+        for i, n in enumerate(self.lens):
+            tk, fk = self.ring.tail(i, n, is_key=True)
+            tv, fv = self.ring.tail(i, n, is_key=False)
+            out.append(DecodeSeq(n, n - tk, n - tv, i, fk, fv))
+        return out
+
+
+def decode_bytes(seqs, *, kvh, d, g, hq, bs, res_elem=2, q_elem=2):
+    """Algorithmic bytes of one fused INT4 decode over ``seqs``."""
+    s = d // 2 + 8 * d // g
+    total = 0
+    for q in seqs:
+        total += (q.k_hist + q.v_hist) * kvh * s
+        total += ((q.seq_len - q.k_hist) + (q.seq_len - q.v_hist)) * kvh * d * res_elem
+        total += 2 * hq * d * q_elem + 4 * math.ceil(q.seq_len / bs)
+    return total
+
+
+# ---------------------------------------------------------------------------
+# headline: KIVI INT4 decode step (config 3)
+# ---------------------------------------------------------------------------
+
+
+def bench_kivi_decode(torch, dev, *, b, hq, kvh, d, g, r, bs, lens, steps, warmup, seed,
+                      want_cpu, split_tokens=None, label="config3"):
+    from vllm_ascend_quantized_kv_cache.methods.kivi_int4.residual import StorePlan
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
+        choose_split_tokens,
+        kivi_decode_attention,
+        plan_decode_work,
+    )
+    from vllm_ascend_quantized_kv_cache.ops.kivi_pack import (
+        pack_key_rows,
+        pack_value_rows,
+        ring_write,
+    )
+
+    gen = torch.Generator().manual_seed(seed)
+    key_scales = torch.exp(torch.randn((kvh, d), generator=gen)).to(dev)
+    t0 = time.time()
+    st = KiviState(torch, dev, lens, kvh=kvh, d=d, g=g, r=r, bs=bs,
+                   spare_steps=steps + warmup + 1, seed=seed, key_scales=key_scales)
+    log(f"{label}: state built in {time.time() - t0:.1f}s "
+        f"({sum(lens)} tokens, {st.kbuf.numel() * 2 / 1e9:.2f} GB int4 pages)")
+    s_bytes = st.layout.bytes_per_token_head
+    kq, ks, km, vq, vs, vm = st.caches
+    gdev = torch.Generator(device=dev).manual_seed(seed + 7)
+    total = steps + warmup
+    new_k = (torch.randn((total, b, kvh, d), generator=gdev, device=dev) * key_scales).to(torch.bfloat16)
+    new_v = torch.randn((total, b, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
+    qs = torch.randn((total, b, hq, d), generator=gdev, device=dev).to(torch.bfloat16)
+    out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=dev)
+    scale = d ** -0.5
+
+    # host planning for every step, outside the timed region
+    plans = []
+    ring = st.ring
+    for step in range(total):
+        plan = StorePlan()
+        for i in range(b):
+            pos = st.lens[i]
+            slot = st.slot_list(i, pos, pos + 1)
+            ring.plan_store(plan, i, slot, [i], is_key=True, block_size=bs, group_size=g)
+            ring.plan_store(plan, i, slot, [i], is_key=False, block_size=bs, group_size=g)
+            st.lens[i] += 1
+        seqs = st.decode_seqs()
+        split = split_tokens or choose_split_tokens(sum(s.seq_len for s in seqs), kvh)
+        meta_np, work_np = plan_decode_work(seqs, split)
+
+        def dev_t(x):
+            return torch.tensor(x, dtype=torch.int64).to(dev)
+
+        p = {
+            "kidx": dev_t(plan.key.pack_src), "kslots": dev_t(plan.key.pack_slots),
+            "vidx": dev_t(plan.value.pack_src), "vslots": dev_t(plan.value.pack_slots),
+            "kdst": dev_t(list(plan.key.ring.keys())), "ksrc": dev_t(list(plan.key.ring.values())),
+            "vdst": dev_t(list(plan.value.ring.keys())), "vsrc": dev_t(list(plan.value.ring.values())),
+            "meta": torch.from_numpy(meta_np).to(dev), "work": torch.from_numpy(work_np).to(dev),
+            "seqs": seqs,
+            "n_pack_k": len(plan.key.pack_slots), "n_pack_v": len(plan.value.pack_slots),
+            "n_ring": len(plan.key.ring) + len(plan.value.ring),
+        }
+        p["decode_bytes"] = decode_bytes(seqs, kvh=kvh, d=d, g=g, hq=hq, bs=bs)
+        p["step_bytes"] = (
+            p["decode_bytes"]
+            + (p["n_pack_k"] + p["n_pack_v"]) * kvh * (2 * d + s_bytes)
+            + p["n_ring"] * kvh * d * 4
+        )
+        plans.append(p)
+    torch.cuda.synchronize()
+    kflat = ring.key.view(-1, kvh, d)
+    vflat = ring.value.view(-1, kvh, d)
+
+    ev = []
+
+    def run_step(i, timed):
+        p = plans[i]
+        if p["n_pack_k"]:
+            pack_key_rows(kflat, new_k[i], p["kidx"], p["kslots"], kq, ks, km, g)
+        if p["n_pack_v"]:
+            pack_value_rows(vflat, new_v[i], p["vidx"], p["vslots"], vq, vs, vm, g)
+        ring_write(ring.key, new_k[i], p["ksrc"], p["kdst"])
+        ring_write(ring.value, new_v[i], p["vsrc"], p["vdst"])
+        if timed:
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+        kivi_decode_attention(qs[i], st.caches, st.table, [], ring.key, ring.value, scale, g,
+                              out=out, plan=(p["meta"], p["work"]))
+        if timed:
+            e1.record()
+            ev.append((e0, e1))
+
+    for i in range(warmup):
+        run_step(i, False)
+    torch.cuda.synchronize()
+    s0 = torch.cuda.Event(enable_timing=True)
+    s1 = torch.cuda.Event(enable_timing=True)
+    s0.record()
+    for i in range(warmup, total):
+        run_step(i, True)
+    s1.record()
+    torch.cuda.synchronize()
+    step_ms = s0.elapsed_time(s1) / steps
+    dec_ms = sum(a.elapsed_time(z) for a, z in ev) / len(ev)
+    timed = plans[warmup:]
+    step_bytes = sum(p["step_bytes"] for p in timed) / steps
+    dec_bytes = sum(p["decode_bytes"] for p in timed) / steps
+    res = {
+        "step_ms": step_ms,
+        "decode_ms": dec_ms,
+        "step_gbs": step_bytes / step_ms / 1e6,
+        "decode_gbs": dec_bytes / dec_ms / 1e6,
+        "decode_bytes": dec_bytes,
+        "step_bytes": step_bytes,
+        "work_items": int(plans[-1]["work"].shape[0]),
+    }
+    if want_cpu:
+        res["cpu"] = cpu_baseline_decode(torch, st, qs[total - 1], plans[-1]["seqs"], hq=hq,
+                                         kvh=kvh, d=d, g=g, bs=bs, scale=scale)
+    del st, plans
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline_decode(torch, st, q, seqs, *, hq, kvh, d, g, bs, scale, sample=2):
+    """Oracle (reference algorithm in torch-CPU) on ``sample`` of the sequences."""
+    from oracle import kvq_oracle as ref
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    caches = tuple(t.cpu() for t in st.caches)
+    idx = list(range(sample))
+    table = st.table_cpu[idx]
+    lens = [seqs[i].seq_len for i in idx]
+    wk, wv = [], []
+    for i in idx:
+        rk = st.ring.key[i].cpu()
+        rv = st.ring.value[i].cpu()
+        wk.append(rk[st.ring.lanes(i, is_key=True)])
+        wv.append(rv[st.ring.lanes(i, is_key=False)])
+    qc = q[idx].cpu()
+
+    def run():
+        dk, dv = ref.dequant_gather(*caches, table, torch.tensor(lens), torch.bfloat16, g)
+        dk = ref.overlay_residual(dk, lens, wk)
+        dv = ref.overlay_residual(dv, lens, wv)
+        return ref.attention(qc, dk, dv, [1] * len(lens), lens, scale, causal=True)
+
+    run()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    nbytes = decode_bytes([seqs[i] for i in idx], kvh=kvh, d=d, g=g, hq=hq, bs=bs)
+    return {
+        "value": round(nbytes / t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"{sample} of {len(seqs)} config-3 sequences ({sum(lens)} tokens): oracle "
+            f"dequant-gather + residual overlay + fp32 SDPA, median of 3, {t * 1e3:.1f} ms"
+        ),
+        "ms": round(t * 1e3, 2),
+    }
+
+
+# ---------------------------------------------------------------------------
+# extras
+# ---------------------------------------------------------------------------
+
+
+def bench_pack_gather(torch, dev, *, reps=10, seed=0):
+    """Config 4 geometry: pack a 2048-token chunk per request, gather 10240 tokens."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_gather import gather_dequant_with_residual
+    from vllm_ascend_quantized_kv_cache.ops.kivi_pack import pack_key_rows, pack_value_rows
+
+    b, kvh, d, g, r, bs = 8, 8, 128, 128, 128, 128
+    lens = [10240] * b
+    gen = torch.Generator().manual_seed(seed)
+    key_scales = torch.exp(torch.randn((kvh, d), generator=gen)).to(dev)
+    st = KiviState(torch, dev, lens, kvh=kvh, d=d, g=g, r=r, bs=bs, spare_steps=1, seed=seed,
+                   key_scales=key_scales)
+    s = st.layout.bytes_per_token_head
+    kq, ks, km, vq, vs, vm = st.caches
+    # pack: the last 2048 positions of every request (whole key groups)
+    chunk = 2048
+    gdev = torch.Generator(device=dev).manual_seed(seed + 3)
+    key = (torch.randn((b * chunk, kvh, d), generator=gdev, device=dev) * key_scales).to(torch.bfloat16)
+    value = torch.randn((b * chunk, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
+    slots = torch.cat([st.slots(i, 8192, 10240) for i in range(b)])
+
+    def pack():
+        pack_key_rows(key, None, None, slots, kq, ks, km, g)
+        pack_value_rows(value, None, None, slots, vq, vs, vm, g)
+
+    pack()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        pack()
+    e1.record()
+    torch.cuda.synchronize()
+    pack_ms = e0.elapsed_time(e1) / reps
+    pack_bytes = b * chunk * kvh * 2 * (2 * d + s)
+
+    # gather: all 10240 tokens of each request, residual tail overlaid
+    seqs = st.decode_seqs()
+    meta = torch.tensor([[q.ring_row, q.k_first, q.seq_len - q.k_hist, q.v_first,
+                          q.seq_len - q.v_hist] for q in seqs], dtype=torch.int32, device=dev)
+    cu_list = [0]
+    for n in lens:
+        cu_list.append(cu_list[-1] + n)
+    cu = torch.tensor(cu_list, dtype=torch.int64, device=dev)
+    total = cu_list[-1]
+
+    def gather():
+        return gather_dequant_with_residual(st.caches, st.table, cu, total, torch.bfloat16, g,
+                                            meta, st.ring.key, st.ring.value)
+
+    gather()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        gather()
+    e1.record()
+    torch.cuda.synchronize()
+    gather_ms = e0.elapsed_time(e1) / reps
+    hist = sum(q.k_hist + q.v_hist for q in seqs)
+    res_t = sum(2 * q.seq_len - q.k_hist - q.v_hist for q in seqs)
+    gather_bytes = hist * kvh * (s + 2 * d) + res_t * kvh * d * 4
+    del st, key, value
+    torch.cuda.empty_cache()
+    return {
+        "pack_ms": pack_ms,
+        "pack_gbs": pack_bytes / pack_ms / 1e6,
+        "gather_ms": gather_ms,
+        "gather_gbs": gather_bytes / gather_ms / 1e6,
+    }
+
+
+def bench_int8_decode(torch, dev, *, reps=20, seed=0):
+    """Config 2: INT8 per-channel decode, 64 x 4096 tokens, Llama-3-8B geometry."""
+    from vllm_ascend_quantized_kv_cache.ops.int8_ops import (
+        int8_calc_scales,
+        int8_decode_attention,
+        int8_quant_scatter,
+        plan_int8_work,
+    )
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import choose_split_tokens
+
+    b, hq, kvh, d, bs, n = 64, 32, 8, 128, 128, 4096
+    nb = b * n // bs
+    gen = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(nb, generator=gen)
+    table = perm.view(b, n // bs).to(torch.int32).to(dev)
+    key_scales = torch.exp(torch.randn((kvh, d), generator=gen)).to(dev)
+    gdev = torch.Generator(device=dev).manual_seed(seed + 5)
+    kc = torch.zeros((nb, bs, kvh, d), dtype=torch.int8, device=dev)
+    vc = torch.zeros_like(kc)
+    k_inv = v_inv = k_aq = v_aq = None
+    pos = torch.arange(n, device=dev)
+    for i in range(b):
+        key = (torch.randn((n, kvh, d), generator=gdev, device=dev) * key_scales).to(torch.bfloat16)
+        value = torch.randn((n, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
+        if k_inv is None:  # scales from the first K/V the layer sees
+            k_inv, v_inv, k_aq, v_aq = int8_calc_scales(key, value)
+        slots = table[i].to(torch.int64)[pos // bs] * bs + pos % bs
+        int8_quant_scatter(key, value, k_inv, v_inv, slots, kc, vc)
+    q = torch.randn((b, hq, d), generator=gdev, device=dev).to(torch.bfloat16)
+    lens = [n] * b
+    meta, work = plan_int8_work(lens, choose_split_tokens(sum(lens), kvh))
+    plan = (torch.from_numpy(meta).to(dev), torch.from_numpy(work).to(dev))
+    out = torch.empty_like(q)
+
+    def run():
+        int8_decode_attention(q, kc, vc, k_aq, v_aq, table, lens, d ** -0.5, out=out, plan=plan)
+
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    nbytes = b * (2 * n * kvh * d + 2 * hq * d * 2 + 4 * (n // bs))
+    del kc, vc
+    torch.cuda.empty_cache()
+    return {"ms": ms, "us_per_layer": ms * 1e3, "gbs": nbytes / ms / 1e6,
+            "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+
+
+# ---------------------------------------------------------------------------
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-config5", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            "bench.py measures one MI355X: this build's hot path runs on a single GPU "
+            "(no collectives); --gpus must be 1.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    b, hq, kvh, d, g, r, bs = 32, 40, 8, 128, 128, 128, 128
+    gen = torch.Generator().manual_seed(0)
+    lens = torch.randint(2048, 16385, (b,), generator=gen).tolist()
+    log(f"config3: {b} seqs, L in [{min(lens)}, {max(lens)}], mean {sum(lens) / b:.0f}")
+    main_res = bench_kivi_decode(
+        torch, dev, b=b, hq=hq, kvh=kvh, d=d, g=g, r=r, bs=bs, lens=lens, steps=args.steps,
+        warmup=args.warmup, seed=0, want_cpu=not args.no_cpu,
+    )
+    log(f"config3: step {main_res['step_ms'] * 1e3:.1f} us, decode {main_res['decode_ms'] * 1e3:.1f} us "
+        f"({main_res['decode_gbs']:.0f} GB/s)")
+
+    extra = {}
+    if not args.no_extras:
+        pg = bench_pack_gather(torch, dev)
+        extra["config4_pack"] = {"ms": round(pg["pack_ms"], 4), "gbs": round(pg["pack_gbs"], 1),
+                                 "frac": round(pg["pack_gbs"] / HBM_PEAK_GBS, 4)}
+        extra["config4_gather"] = {"ms": round(pg["gather_ms"], 4),
+                                   "gbs": round(pg["gather_gbs"], 1),
+                                   "frac": round(pg["gather_gbs"] / HBM_PEAK_GBS, 4)}
+        log(f"config4: pack {pg['pack_gbs']:.0f} GB/s, gather {pg['gather_gbs']:.0f} GB/s")
+        i8 = bench_int8_decode(torch, dev)
+        extra["config2_int8_decode"] = {k: round(v, 4) for k, v in i8.items()}
+        log(f"config2: int8 decode {i8['us_per_layer']:.1f} us ({i8['gbs']:.0f} GB/s)")
+        if not args.no_config5:
+            gen5 = torch.Generator().manual_seed(5)
+            del gen5
+            c5 = bench_kivi_decode(
+                torch, dev, b=256, hq=64, kvh=8, d=128, g=64, r=128, bs=128,
+                lens=[32768] * 256, steps=5, warmup=2, seed=5, want_cpu=False, label="config5",
+            )
+            extra["config5_int4_decode"] = {
+                "us_per_layer": round(c5["decode_ms"] * 1e3, 1),
+                "gbs": round(c5["decode_gbs"], 1),
+                "frac": round(c5["decode_gbs"] / HBM_PEAK_GBS, 4),
+                "step_us": round(c5["step_ms"] * 1e3, 1),
+            }
+            log(f"config5: decode {c5['decode_ms'] * 1e3:.1f} us ({c5['decode_gbs']:.0f} GB/s)")
+
+    line = {
+        "metric": METRIC,
+        "value": round(main_res["step_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_res["step_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 KV, bf16 q/out, fp32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V, log-normal key channel scales, shuffled pages)",
+        "config": {
+            "workload": "BASELINE configs[2]: KIVI INT4 fused decode step, Qwen2.5-14B geometry",
+            "batch": b, "num_heads": hq, "num_kv_heads": kvh, "head_size": d,
+            "group_size": g, "residual_length": r, "block_size": bs,
+            "context": "U[2048,16384] seed 0",
+        },
+        "decode_us_per_layer": round(main_res["decode_ms"] * 1e3, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(main_res["decode_gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(main_res["decode_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "kvq_kivi_decode_attn (fused INT4 decode + combine)",
+            "algorithmic_bytes_per_launch": int(main_res["decode_bytes"]),
+        },
+        "extra": extra,
+    }
+    if "cpu" in main_res:
+        c = dict(main_res["cpu"])
+        c.pop("ms", None)
+        line["cpu_baseline"] = c
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

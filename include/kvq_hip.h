@@ -76,6 +76,16 @@ int kvq_kivi_pack_value(const void* src_a, int64_t n_a, const void* src_b,
                         int num_kv_heads, int head_size, int group_size, int block_size,
                         int32_t* v_quant, float* v_scale, float* v_mn, void* stream);
 
+/* Residual-ring write: ring row dst_rows[i] (a row is KVH*D elements of
+ * `ring_dtype`, the ring viewed as [rows*ring_len, KVH, D]) takes source row
+ * src_rows[i] (identity when NULL) of `src_dtype`, converted with
+ * round-to-nearest-even.  Replaces the per-token lane writes of
+ * _store_kivi_residual_entries (pkg/methods/kivi_int4/attention_backend.py:
+ * 411-462), batched over every token and request of a step. */
+int kvq_kivi_ring_write(const void* src, int src_dtype, const int64_t* src_rows,
+                        const int64_t* dst_rows, int64_t num_rows, int row_elems,
+                        void* ring, int ring_dtype, void* stream);
+
 /* Paged gather-dequant to dense TND with an optional residual-tail overlay.
  * out_k/out_v are [cu_seqlens[batch], KVH, D] of `out_dtype`; request b owns
  * rows [cu_seqlens[b], cu_seqlens[b+1]).  Negative block ids read block 0 and

@@ -189,6 +189,25 @@ kivi_pack_value_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __rest
   }
 }
 
+
+// Residual ring write: row dst_rows[i] of the ring takes source row
+// src_rows[i] (or i), converted to the ring dtype; 8 elements per thread.
+template <typename TS, typename TD>
+__global__ void __launch_bounds__(256)
+ring_write_kernel(const TS* __restrict__ src, const int64_t* __restrict__ src_rows,
+                  const int64_t* __restrict__ dst_rows, int64_t n, int row_elems,
+                  TD* __restrict__ ring) {
+  const int per_row = row_elems / 8;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gid >= n * per_row) return;
+  const int64_t i = gid / per_row;
+  const int c = static_cast<int>(gid - i * per_row) * 8;
+  const int64_t sr = src_rows ? src_rows[i] : i;
+  float x[8];
+  load8(src + sr * row_elems + c, x);
+  store8(ring + dst_rows[i] * row_elems + c, x);
+}
+
 bool kivi_geometry_ok(int kvh, int d, int g, int bs) {
   return kvh > 0 && d > 0 && g > 0 && bs > 0 && g % 8 == 0 && d % 8 == 0 && d % g == 0 &&
          bs % g == 0;
@@ -252,6 +271,25 @@ extern "C" int kvq_kivi_pack_value(const void* src_a, int64_t n_a, const void* s
                          static_cast<const T*>(src_b), src_index,
                          static_cast<const I*>(slot_mapping), num_tokens, num_kv_heads,
                          head_size, group_size, block_size, v_quant, v_scale, v_mn)));
+  KVQ_LAUNCH_CHECK();
+  return KVQ_OK;
+}
+
+extern "C" int kvq_kivi_ring_write(const void* src, int src_dtype, const int64_t* src_rows,
+                                   const int64_t* dst_rows, int64_t num_rows, int row_elems,
+                                   void* ring, int ring_dtype, void* stream) {
+  if (num_rows == 0) return KVQ_OK;
+  if (!src || !dst_rows || !ring || num_rows < 0 || row_elems <= 0 || row_elems % 8)
+    return KVQ_ERR_INVALID;
+  const int64_t total = num_rows * (row_elems / 8);
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  KVQ_DISPATCH_FLOAT(src_dtype, TS,
+    KVQ_DISPATCH_FLOAT(ring_dtype, TD,
+      hipLaunchKernelGGL((ring_write_kernel<TS, TD>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(256), 0, s, static_cast<const TS*>(src), src_rows, dst_rows,
+                         num_rows, row_elems, static_cast<TD*>(ring))));
   KVQ_LAUNCH_CHECK();
   return KVQ_OK;
 }

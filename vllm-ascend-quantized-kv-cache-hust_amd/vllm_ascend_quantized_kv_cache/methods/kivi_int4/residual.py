@@ -1,0 +1,301 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Device-resident KIVI residual windows with a host mirror.
+
+The reference keeps one full-precision ring row per request
+(``[max_num_seqs, R, KVH, D]``) and drives it token by token from Python,
+synchronising with the device for every slot lookup
+(``pkg/methods/kivi_int4/attention_backend.py:181-462``).  Here the ring
+tensors stay on the GPU and the host keeps an exact mirror of which slot
+every lane holds, so the per-token rules can be replayed on the host without
+reading the device:
+
+* a slot already held is overwritten in place;
+* otherwise, while the window is full, keys flush the whole window and values
+  evict the single oldest lane (``:448-455``); then the token is appended.
+
+Replaying a batch of tokens yields a ``StorePlan``: packed-history writes
+(sources are old ring lanes or rows of this step's input) and final ring-lane
+writes.  ``execute`` issues them as at most three launches per side (key
+pack, value pack, ring write), in an order that reads every old lane before
+it is overwritten.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from ...ops.kivi_layout import key_slot_groups_error
+
+
+@dataclass
+class SideWrites:
+    """Device work of one side (keys or values) for one store batch."""
+
+    pack_src: list[int] = field(default_factory=list)  # source row per packed token
+    pack_slots: list[int] = field(default_factory=list)  # history slot per packed token
+    ring: dict[int, int] = field(default_factory=dict)  # ring row -> input row (last wins)
+    lane_src: dict[int, int] = field(default_factory=dict)  # ring row -> current source row
+
+    def empty(self) -> bool:
+        return not self.pack_slots and not self.ring
+
+
+@dataclass
+class StorePlan:
+    """Batched device work; source rows index ``[ring rows ; input rows]``."""
+
+    key: SideWrites = field(default_factory=SideWrites)
+    value: SideWrites = field(default_factory=SideWrites)
+
+    def side(self, is_key: bool) -> SideWrites:
+        return self.key if is_key else self.value
+
+    def empty(self) -> bool:
+        return self.key.empty() and self.value.empty()
+
+
+class KiviResidualRing:
+    """Ring tensors ``[rows, R, KVH, D]`` (keys, values) plus their host mirror."""
+
+    def __init__(
+        self,
+        rows: int,
+        ring_len: int,
+        num_kv_heads: int,
+        head_size: int,
+        *,
+        device,
+        dtype=torch.float32,
+    ) -> None:
+        self.rows = rows
+        self.ring_len = ring_len
+        self.num_kv_heads = num_kv_heads
+        self.head_size = head_size
+        self.device = device
+        self.key = torch.zeros((rows, ring_len, num_kv_heads, head_size), dtype=dtype, device=device)
+        self.value = torch.zeros_like(self.key)
+        self.written = False
+        self.start = {True: [0] * rows, False: [0] * rows}
+        self.length = {True: [0] * rows, False: [0] * rows}
+        self.lane_slot = {True: [[-1] * ring_len for _ in range(rows)],
+                          False: [[-1] * ring_len for _ in range(rows)]}
+        self.slot_lane: dict[bool, list[dict[int, int]]] = {
+            True: [dict() for _ in range(rows)],
+            False: [dict() for _ in range(rows)],
+        }
+
+    # -- dtype ----------------------------------------------------------------
+
+    @property
+    def dtype(self):
+        return self.key.dtype
+
+    def adopt_dtype(self, dtype) -> None:
+        """Match the ring to the activations so pack and overlay stay exact.
+
+        An untouched ring takes the activation dtype; a ring that already
+        holds data and meets a different dtype widens to fp32 (lossless for
+        every 16-bit input).
+        """
+        if dtype == self.key.dtype:
+            return
+        if not self.written:
+            self.key = torch.zeros(self.key.shape, dtype=dtype, device=self.device)
+            self.value = torch.zeros_like(self.key)
+        elif self.key.dtype != torch.float32:
+            self.key = self.key.float()
+            self.value = self.value.float()
+
+    def tensor(self, is_key: bool) -> torch.Tensor:
+        return self.key if is_key else self.value
+
+    # -- host mirror queries -----------------------------------------------
+
+    def lanes(self, row: int, *, is_key: bool) -> list[int]:
+        """Occupied lanes of ``row`` in FIFO order (wrapping past R)."""
+        n = self.length[is_key][row]
+        s = self.start[is_key][row]
+        return [(s + i) % self.ring_len for i in range(n)]
+
+    def window_slots(self, row: int, *, is_key: bool) -> list[int]:
+        ls = self.lane_slot[is_key][row]
+        return [ls[lane] for lane in self.lanes(row, is_key=is_key)]
+
+    def holds(self, row: int, slot: int, *, is_key: bool) -> bool:
+        return slot in self.slot_lane[is_key][row]
+
+    def tail(self, row: int, seq_len: int, *, is_key: bool) -> tuple[int, int]:
+        """``(tail_len, first_lane)`` of the overlay for a sequence of ``seq_len``.
+
+        The last ``min(seq_len, len)`` window entries replace the sequence's
+        last positions (``attention_backend.py:899-923``).
+        """
+        n = self.length[is_key][row]
+        t = min(seq_len, n)
+        first = (self.start[is_key][row] + n - t) % self.ring_len
+        return t, first
+
+    # -- mutation ----------------------------------------------------------
+
+    def reset_row(self, row: int) -> None:
+        for is_key in (True, False):
+            self.start[is_key][row] = 0
+            self.length[is_key][row] = 0
+            self.lane_slot[is_key][row] = [-1] * self.ring_len
+            self.slot_lane[is_key][row] = {}
+
+    def keep_only(self, row: int, keep_slots: set[int], *, is_key: bool) -> list[tuple[int, int]]:
+        """Drop lanes whose slot is not in ``keep_slots``; compact to lane 0.
+
+        Returns the ``(dst_lane, src_lane)`` moves the device copy must perform
+        (the reference rewrites the kept entries from lane 0 on,
+        ``attention_backend.py:328-356``).
+        """
+        lanes = self.lanes(row, is_key=is_key)
+        ls = self.lane_slot[is_key][row]
+        kept = [lane for lane in lanes if ls[lane] in keep_slots]
+        if len(kept) == len(lanes):
+            return []
+        slots = [ls[lane] for lane in kept]
+        self.start[is_key][row] = 0
+        self.length[is_key][row] = len(kept)
+        new_ls = [-1] * self.ring_len
+        for i, s in enumerate(slots):
+            new_ls[i] = s
+        self.lane_slot[is_key][row] = new_ls
+        self.slot_lane[is_key][row] = {s: i for i, s in enumerate(slots)}
+        return [(i, src) for i, src in enumerate(kept) if i != src]
+
+    def plan_store(
+        self,
+        plan: StorePlan,
+        row: int,
+        slots: list[int],
+        input_rows: list[int],
+        *,
+        is_key: bool,
+        block_size: int,
+        group_size: int,
+    ) -> None:
+        """Replay ``_store_kivi_residual_entries`` for one request and side.
+
+        ``input_rows[i]`` is the row (in the step's input) of the token with
+        slot ``slots[i]``.  Updates the mirror and appends the device work to
+        ``plan``; raises before any launch if a key flush would break the
+        pack kernel's aligned-group contract.
+        """
+        side = plan.side(is_key)
+        r = self.ring_len
+        na = self.rows * r
+        base = row * r
+        ls = self.lane_slot[is_key][row]
+        sl = self.slot_lane[is_key][row]
+
+        def source(lane: int) -> int:  # where the lane's current content lives
+            return side.lane_src.get(base + lane, base + lane)
+
+        for slot, irow in zip(slots, input_rows):
+            lane = sl.get(slot)
+            if lane is not None:
+                side.lane_src[base + lane] = na + irow
+                side.ring[base + lane] = irow
+                continue
+            while self.length[is_key][row] >= r:
+                count = r if is_key else 1
+                ev = self.lanes(row, is_key=is_key)[:count]
+                ev_slots = [ls[lane] for lane in ev]
+                if is_key:
+                    err = key_slot_groups_error(ev_slots, block_size=block_size,
+                                                group_size=group_size)
+                    if err is not None:
+                        raise RuntimeError(
+                            "KIVI key flush requires contiguous aligned token groups."
+                        )
+                side.pack_src.extend(source(lane) for lane in ev)
+                side.pack_slots.extend(ev_slots)
+                for lane in ev:
+                    sl.pop(ls[lane], None)
+                    ls[lane] = -1
+                    side.ring.pop(base + lane, None)
+                    side.lane_src.pop(base + lane, None)
+                n = self.length[is_key][row] - count
+                self.length[is_key][row] = n
+                self.start[is_key][row] = (self.start[is_key][row] + count) % r if n else 0
+            tail = (self.start[is_key][row] + self.length[is_key][row]) % r
+            ls[tail] = slot
+            sl[slot] = tail
+            side.lane_src[base + tail] = na + irow
+            side.ring[base + tail] = irow
+            self.length[is_key][row] += 1
+
+    def flush_prefix(self, plan: StorePlan, row: int, count: int, *, is_key: bool,
+                     block_size: int, group_size: int) -> None:
+        """Move the ``count`` oldest entries of a window to int4 history."""
+        n = self.length[is_key][row]
+        count = min(count, n)
+        if count <= 0:
+            return
+        ev = self.lanes(row, is_key=is_key)[:count]
+        ls = self.lane_slot[is_key][row]
+        ev_slots = [ls[lane] for lane in ev]
+        if is_key:
+            err = key_slot_groups_error(ev_slots, block_size=block_size, group_size=group_size)
+            if err is not None or count % group_size:
+                raise RuntimeError("KIVI key flush requires contiguous aligned token groups.")
+        side = plan.side(is_key)
+        base = row * self.ring_len
+        side.pack_src.extend(side.lane_src.get(base + lane, base + lane) for lane in ev)
+        side.pack_slots.extend(ev_slots)
+        for lane in ev:
+            self.slot_lane[is_key][row].pop(ls[lane], None)
+            ls[lane] = -1
+            side.ring.pop(base + lane, None)
+            side.lane_src.pop(base + lane, None)
+        self.length[is_key][row] = n - count
+        self.start[is_key][row] = (self.start[is_key][row] + count) % self.ring_len if n - count else 0
+
+    # -- execution ---------------------------------------------------------
+
+    def execute(
+        self,
+        plan: StorePlan,
+        key_input: torch.Tensor | None,
+        value_input: torch.Tensor | None,
+        *,
+        pack_key,
+        pack_value,
+        ring_write,
+    ) -> None:
+        """Issue a plan: history packs first (they read old lanes), then ring writes.
+
+        ``pack_key/pack_value(src_a, src_b, src_index, slots)`` and
+        ``ring_write(src, src_rows, dst_rows, is_key)`` are the launch hooks;
+        ``src_a`` is the ring viewed as ``[rows*R, KVH, D]``, ``src_b`` the
+        step's input converted to the ring dtype.
+        """
+        dev = self.key.device
+        inputs = {True: key_input, False: value_input}
+        for is_key in (True, False):
+            side = plan.side(is_key)
+            if not side.pack_slots:
+                continue
+            inp = inputs[is_key]
+            if inp is not None and inp.dtype != self.dtype:
+                inp = inp.to(self.dtype)
+            flat = self.tensor(is_key).view(-1, self.num_kv_heads, self.head_size)
+            idx = torch.tensor(side.pack_src, dtype=torch.int64).to(dev, non_blocking=True)
+            slots = torch.tensor(side.pack_slots, dtype=torch.int64).to(dev, non_blocking=True)
+            (pack_key if is_key else pack_value)(flat, inp, idx, slots)
+        for is_key in (True, False):
+            side = plan.side(is_key)
+            if not side.ring:
+                continue
+            dst = torch.tensor(list(side.ring.keys()), dtype=torch.int64).to(dev, non_blocking=True)
+            src = torch.tensor(list(side.ring.values()), dtype=torch.int64).to(dev, non_blocking=True)
+            ring_write(inputs[is_key], src, dst, is_key)
+            self.written = True
+
+
+__all__ = ["KiviResidualRing", "SideWrites", "StorePlan"]

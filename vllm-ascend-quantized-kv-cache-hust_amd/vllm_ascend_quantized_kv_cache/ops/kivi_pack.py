@@ -160,9 +160,30 @@ def kivi_pack_key_cache(
     )
 
 
+def ring_write(
+    ring: torch.Tensor,
+    src: torch.Tensor,
+    src_rows: torch.Tensor | None,
+    dst_rows: torch.Tensor,
+) -> None:
+    """``ring.view(-1, KVH, D)[dst_rows[i]] = src[src_rows[i]]`` (dtype converted)."""
+    n = dst_rows.numel()
+    if n == 0:
+        return
+    _native.require_gpu_tensors("kivi ring write", ring, src, src_rows, dst_rows)
+    row_elems = ring.shape[-1] * ring.shape[-2]
+    rc = _native.lib().kvq_kivi_ring_write(
+        _native.ptr(src.contiguous()), _native.dtype_code(src.dtype), _native.ptr(src_rows),
+        _native.ptr(dst_rows), n, row_elems, _native.ptr(ring), _native.dtype_code(ring.dtype),
+        _native.stream_of(ring),
+    )
+    _native.check(rc, "kvq_kivi_ring_write")
+
+
 __all__ = [
     "kivi_pack_key_cache",
     "kivi_pack_value_cache",
     "pack_key_rows",
     "pack_value_rows",
+    "ring_write",
 ]
