@@ -187,6 +187,14 @@ int kvq_int8_decode_attn(const void* query, int dtype, int64_t batch, int num_he
                          const int32_t* seq_meta, const int32_t* work, int64_t num_work,
                          void* workspace, void* out, void* stream);
 
+/* ---- self-test ---------------------------------------------------------- */
+
+/* One v_mfma_f32_16x16x32_f16 with the operand/result lane mapping the decode
+ * kernels assume: d[16x16] = a[16x32] * b[32x16], row-major fp16 inputs and
+ * fp32 output.  No counterpart in the reference; it lets the test suite pin
+ * the gfx950 matrix-core lane layout directly. */
+int kvq_selftest_mfma_f16(const void* a, const void* b, float* d, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

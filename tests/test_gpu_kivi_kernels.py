@@ -200,3 +200,19 @@ def test_decode_attention_matches_oracle(gpu_device, d, kvh, g, bs, rep):
             ring_k.to(gpu_device), ring_v.to(gpu_device), scale, g, split_tokens=split,
         )
         torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
+
+
+def test_mfma_lane_layout(gpu_device):
+    """The 16x16x32 f16 MFMA lane mapping the decode kernels assume."""
+    from vllm_ascend_quantized_kv_cache.ops import _native
+
+    g = torch.Generator().manual_seed(0)
+    a = torch.randint(-4, 5, (16, 32), generator=g).to(torch.float16)
+    b = torch.randint(-4, 5, (32, 16), generator=g).to(torch.float16)
+    da, db = a.to(gpu_device), b.to(gpu_device)
+    d = torch.empty(16, 16, dtype=torch.float32, device=gpu_device)
+    rc = _native.lib().kvq_selftest_mfma_f16(
+        da.data_ptr(), db.data_ptr(), d.data_ptr(), _native.stream_of(d)
+    )
+    _native.check(rc, "kvq_selftest_mfma_f16")
+    assert torch.equal(d.cpu(), a.float() @ b.float())

@@ -38,6 +38,58 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Stage the K (is_key) or V rows of positions [p0, p0 + n) of one kv head into
+// LDS as fp32 [64][d + 1]: int4 history dequantized exactly, ring rows copied.
+template <typename TR>
+__device__ __forceinline__ void stage_rows(float* __restrict__ dst, bool is_key, int p0, int n,
+                                           int hist, const int32_t* __restrict__ bt, int bs,
+                                           int kvh, int h, int d, int g,
+                                           const uint32_t* __restrict__ q4,
+                                           const float* __restrict__ sc,
+                                           const float* __restrict__ mn,
+                                           const TR* __restrict__ ring, int64_t ring_row0,
+                                           int ring_first, int ring_len, int lane) {
+  const int ndv = d / 8;
+  const int pitch = d + 1;
+  const int gpb = bs / g;
+  const int wpd = bs / 8;
+  // one task = 8 consecutive dims of one position
+  for (int t = lane; t < 64 * ndv; t += 64) {
+    const int pi = t / ndv;
+    const int dv = t - pi * ndv;
+    if (pi >= n) continue;
+    const int p = p0 + pi;
+    float x[8];
+    if (p < hist) {
+      int64_t blk = bt[p / bs];
+      if (blk < 0) blk = 0;
+      const int off = p % bs;
+      if (is_key) {
+        const int64_t base = (blk * kvh + h) * static_cast<int64_t>(d) + dv * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t w = q4[(base + i) * wpd + off / 8];
+          x[i] = kivi_dequant((w >> (4 * (off % 8))) & 0xfu, sc[(base + i) * gpb + off / g],
+                              mn[(base + i) * gpb + off / g]);
+        }
+      } else {
+        const int64_t vrow = (blk * bs + off) * kvh + h;
+        const uint32_t w = q4[vrow * ndv + dv];
+        const int gi = (dv * 8) / g;
+        const float s_ = sc[vrow * (d / g) + gi];
+        const float m_ = mn[vrow * (d / g) + gi];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = kivi_dequant((w >> (4 * i)) & 0xfu, s_, m_);
+      }
+    } else {
+      const int rl = (ring_first + (p - hist)) % ring_len;
+      load8(ring + ((ring_row0 + rl) * kvh + h) * d + dv * 8, x);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[pi * pitch + dv * 8 + i] = x[i];
+  }
+}
+
 template <typename TQ, typename TR>
 __global__ void __launch_bounds__(64)
 kivi_decode_generic_kernel(const TQ* __restrict__ query, int hq, int kvh, int d, float qscale,
@@ -62,20 +114,20 @@ kivi_decode_generic_kernel(const TQ* __restrict__ query, int hq, int kvh, int d,
   const int khist = sm[1], vhist = sm[2], row = sm[3], kfirst = sm[4], vfirst = sm[5];
   const int rep = hq / kvh;
   const int dpl = (d + 63) / 64;
-  const int words = d / 8;
-  const int ng = d / g;
-  const int gpb = bs / g;
-  const int wpd = bs / 8;
+  const int pitch = d + 1;
   const int32_t* bt = block_table + static_cast<int64_t>(b) * maxb;
+  const uint32_t* kqu = reinterpret_cast<const uint32_t*>(kq);
+  const uint32_t* vqu = reinterpret_cast<const uint32_t*>(vq);
 
-  __shared__ float s_q[kMaxRep * 256];
-  __shared__ float s_p[kMaxRep * 64];
+  extern __shared__ float lds_f[];
+  float* s_rows = lds_f;                 // [64][d + 1]
+  float* s_q = s_rows + 64 * pitch;      // [rep][d]
+  float* s_p = s_q + rep * d;            // [rep][64]
   for (int i = lane; i < rep * d; i += 64) {
     const int r = i / d;
     const int c = i - r * d;
     s_q[i] = to_f32(query[(static_cast<int64_t>(b) * hq + h * rep + r) * d + c]) * qscale;
   }
-  __syncthreads();
 
   float m[kMaxRep], l[kMaxRep], acc[kMaxRep][kMaxDpl];
 #pragma unroll
@@ -87,36 +139,21 @@ kivi_decode_generic_kernel(const TQ* __restrict__ query, int hq, int kvh, int d,
   }
 
   for (int p0 = pb; p0 < pe; p0 += 64) {
-    const int p = p0 + lane;
-    const bool live = p < pe;
+    const int n = (pe - p0) < 64 ? (pe - p0) : 64;
+    stage_rows(s_rows, true, p0, n, khist, bt, bs, kvh, h, d, g, kqu, ks, km, ring_k,
+               static_cast<int64_t>(row) * ring_len, kfirst, ring_len, lane);
+    __syncthreads();
+    const bool live = lane < n;
     float s[kMaxRep];
 #pragma unroll
     for (int r = 0; r < kMaxRep; ++r) s[r] = 0.0f;
     if (live) {
-      if (p < khist) {
-        int64_t blk = bt[p / bs];
-        if (blk < 0) blk = 0;
-        const int off = p % bs;
-        const int64_t base = (blk * kvh + h) * static_cast<int64_t>(d);
-        const uint32_t* wrow = reinterpret_cast<const uint32_t*>(kq) + base * wpd + off / 8;
-        const float* srow = ks + base * gpb + off / g;
-        const float* mrow = km + base * gpb + off / g;
-        const int shift = 4 * (off % 8);
-        for (int c = 0; c < d; ++c) {
-          const float kv = kivi_dequant((wrow[c * wpd] >> shift) & 0xfu, srow[c * gpb], mrow[c * gpb]);
+      const float* krow = s_rows + lane * pitch;
+      for (int c = 0; c < d; ++c) {
+        const float kv = krow[c];
 #pragma unroll
-          for (int r = 0; r < kMaxRep; ++r)
-            if (r < rep) s[r] += s_q[r * d + c] * kv;
-        }
-      } else {
-        const int rl = (kfirst + (p - khist)) % ring_len;
-        const TR* kr = ring_k + ((static_cast<int64_t>(row) * ring_len + rl) * kvh + h) * d;
-        for (int c = 0; c < d; ++c) {
-          const float kv = to_f32(kr[c]);
-#pragma unroll
-          for (int r = 0; r < kMaxRep; ++r)
-            if (r < rep) s[r] += s_q[r * d + c] * kv;
-        }
+        for (int r = 0; r < kMaxRep; ++r)
+          if (r < rep) s[r] += s_q[r * d + c] * kv;
       }
     }
 #pragma unroll
@@ -133,31 +170,16 @@ kivi_decode_generic_kernel(const TQ* __restrict__ query, int hq, int kvh, int d,
       s_p[r * 64 + lane] = pr;
     }
     __syncthreads();
-    const int n = (pe - p0) < 64 ? (pe - p0) : 64;
+    stage_rows(s_rows, false, p0, n, vhist, bt, bs, kvh, h, d, g, vqu, vs, vm, ring_v,
+               static_cast<int64_t>(row) * ring_len, vfirst, ring_len, lane);
+    __syncthreads();
     for (int i = 0; i < n; ++i) {
-      const int pp = p0 + i;
-      const bool from_int4 = pp < vhist;
-      int64_t vrow = 0;
-      const TR* vr = nullptr;
-      if (from_int4) {
-        int64_t blk = bt[pp / bs];
-        if (blk < 0) blk = 0;
-        vrow = (blk * bs + pp % bs) * kvh + h;
-      } else {
-        const int rl = (vfirst + (pp - vhist)) % ring_len;
-        vr = ring_v + ((static_cast<int64_t>(row) * ring_len + rl) * kvh + h) * d;
-      }
+      const float* vrow = s_rows + i * pitch;
 #pragma unroll
       for (int k = 0; k < kMaxDpl; ++k) {
         const int c = lane + 64 * k;
         if (k >= dpl || c >= d) continue;
-        float v;
-        if (from_int4) {
-          const uint32_t word = reinterpret_cast<const uint32_t*>(vq)[vrow * words + c / 8];
-          v = kivi_dequant((word >> (4 * (c % 8))) & 0xfu, vs[vrow * ng + c / g], vm[vrow * ng + c / g]);
-        } else {
-          v = to_f32(vr[c]);
-        }
+        const float v = vrow[c];
 #pragma unroll
         for (int r = 0; r < kMaxRep; ++r)
           if (r < rep) acc[r][k] += s_p[r * 64 + i] * v;
@@ -266,9 +288,11 @@ extern "C" int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batc
                                        work, num_work, ws_o, ws_ml, s, &mfma);
   if (rc != KVQ_OK) return rc;
   const dim3 grid(static_cast<unsigned>(num_work), num_kv_heads);
+  const int rep = num_heads / num_kv_heads;
+  const size_t lds = sizeof(float) * (64 * (head_size + 1) + rep * head_size + rep * 64);
   KVQ_DISPATCH_FLOAT(q_dtype, TQ,
     KVQ_DISPATCH_FLOAT(ring_dtype, TR,
-      hipLaunchKernelGGL((kivi_decode_generic_kernel<TQ, TR>), grid, dim3(64), 0, s,
+      hipLaunchKernelGGL((kivi_decode_generic_kernel<TQ, TR>), grid, dim3(64), lds, s,
                          static_cast<const TQ*>(query), num_heads, num_kv_heads, head_size,
                          qscale, k_quant, k_scale, k_mn, v_quant, v_scale, v_mn, block_size,
                          group_size, block_table, max_blocks, seq_meta, work,

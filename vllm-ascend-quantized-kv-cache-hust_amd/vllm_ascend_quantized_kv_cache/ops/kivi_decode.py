@@ -19,6 +19,8 @@ from . import _native
 
 #: positions per work item when the caller does not choose
 DEFAULT_SPLIT_TOKENS = 1024
+#: positions per generic (mixed-source) work item
+TAIL_ITEM_TOKENS = 64
 
 
 @dataclass(frozen=True)
@@ -54,6 +56,9 @@ def plan_decode_work(
     ``split_tokens``); one kind-1 item covers the rest (at most two residual
     windows long).  Every request owns at least one item, contiguous in the list.
     """
+    # kind-0 items start on 128-token boundaries: the MFMA kernel walks
+    # page- and key-group-aligned tiles of up to 128 tokens
+    split_tokens = max(128, -(-int(split_tokens) // 128) * 128)
     meta = np.zeros((len(seqs), 8), dtype=np.int32)
     work: list[tuple[int, int, int, int]] = []
     for b, s in enumerate(seqs):
@@ -64,8 +69,15 @@ def plan_decode_work(
             e = min(end_a, p + split_tokens)
             work.append((b, p, e, 0))
             p = e
-        if end_a < s.seq_len or s.seq_len == 0:
-            work.append((b, end_a, s.seq_len, 1))
+        # the mixed-source tail (at most two residual windows) in 64-position
+        # items, so tails of different requests and heads run side by side
+        p = end_a
+        while p < s.seq_len:
+            e = min(s.seq_len, p + TAIL_ITEM_TOKENS)
+            work.append((b, p, e, 1))
+            p = e
+        if s.seq_len == 0:
+            work.append((b, 0, 0, 1))
         meta[b] = (
             s.seq_len, s.k_hist, s.v_hist, s.ring_row, s.k_first, s.v_first,
             first, len(work) - first,
