@@ -136,6 +136,23 @@ int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batch, int num_
                          const void* ring_k, const void* ring_v, int ring_dtype, int ring_len,
                          void* workspace, void* out, void* stream);
 
+/* ---- dense attention ----------------------------------------------------- */
+
+/* Attention over dense TND tensors: query [cu_q[batch], num_heads, D], key and
+ * value [cu_k[batch], num_kv_heads, D], out like query, all of `dtype`.
+ * Request b's query row i sits at kv position lk_b - lq_b + i; with `causal`
+ * keys past it are masked.  GQA maps query head h to kv head
+ * h / (num_heads / num_kv_heads).  cu_* are int32 [batch + 1]; max_q_len
+ * bounds lq_b.  head_size in {32, 64, 128, 256}.
+ * Replaces npu_fused_infer_attention_score with input_layout "TND"
+ * (pkg/methods/kivi_int4/attention_backend.py:1248-1262, 1320-1334 and the
+ * dense fallback 1341-1392; pkg/methods/int8_dynamic/attention_backend.py:
+ * 282-296, 350-364). */
+int kvq_prefill_attn(const void* query, const void* key, const void* value, int dtype,
+                     const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                     int64_t batch, int64_t max_q_len, int num_heads, int num_kv_heads,
+                     int head_size, float scale, int causal, void* out, void* stream);
+
 /* ---- INT8 dynamic per-channel ------------------------------------------- */
 
 /* First-K/V scales in the activation dtype: amax over tokens per (head, dim),

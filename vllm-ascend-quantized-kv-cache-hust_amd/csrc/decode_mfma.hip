@@ -75,10 +75,10 @@ __device__ __forceinline__ float max_kg(float v) {
   return v;
 }
 
-constexpr int kHeadsPerWg = 2;  // waves (kv heads) per workgroup
+constexpr int kHeadsPerWg = 4;  // waves (kv heads) per workgroup
 
 template <typename TQ, int CPG>
-__global__ void __launch_bounds__(128, 4)
+__global__ void __launch_bounds__(256, 2)
 kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qscale,
                         const uint32_t* __restrict__ kq, const float* __restrict__ ks,
                         const float* __restrict__ km, const uint32_t* __restrict__ vq,

@@ -1,0 +1,867 @@
+# SPDX-License-Identifier: Apache-2.0
+"""KIVI INT4 attention mixin (int4 paged history + full-precision residual window).
+
+Role and behaviour follow ``AscendKiviInt4AttentionBackendMixin`` of the
+reference (``pkg/methods/kivi_int4/attention_backend.py``, cited below as
+``ab.py``): the adapter composes this mixin in front of the host's attention
+implementation, ``forward`` owns the whole INT4 path, and every guard fails
+closed with the reference's messages.  What changes is where the work runs:
+
+* the residual windows live on the GPU (``KiviResidualRing``) with an exact
+  host mirror, so the per-token window rules replay on the host without
+  device reads and each step issues a few batched launches;
+* packing, gather-dequant (with the residual overlay fused in), fused decode
+  attention and dense prefill attention are the MI355X HIP kernels behind the
+  ``_launch_*`` hooks (tests replace the hooks, the validations stay real).
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+
+from .byte_cache import kivi_byte_cache_layout, kivi_caches_from_byte_tensors
+from .geometry import validate_kivi_geometry
+from .residual import KiviResidualRing, StorePlan
+from .semantics import KiviInt4Semantics
+
+
+def _attn_state_name(attn_metadata: Any) -> str:
+    state = getattr(attn_metadata, "attn_state", None)
+    if state is None:
+        return "UNKNOWN"
+    return getattr(state, "name", None) or str(state)
+
+
+def _host_list(x: Any) -> list[int]:
+    if isinstance(x, torch.Tensor):
+        return [int(v) for v in x.tolist()]
+    return [int(v) for v in x]
+
+
+class AscendKiviInt4AttentionBackendMixin:
+    """KIVI INT4 (int4 history + full-precision residual window) attention path."""
+
+    # ------------------------------------------------------------------
+    # state (ab.py:50-133)
+    # ------------------------------------------------------------------
+
+    def _init_kivi_state(self, kv_cache_dtype: str | None, vllm_config: Any = None) -> None:
+        self.enable_kivi = kv_cache_dtype in ("kivi_int4", "kivi")
+        cache_config = getattr(vllm_config, "cache_config", None)
+        group_size = getattr(cache_config, "kivi_group_size", 128)
+        residual_length = getattr(cache_config, "kivi_residual_length", 128)
+        self.kivi_group_size = group_size if isinstance(group_size, int) else 128
+        self.kivi_residual_length = residual_length if isinstance(residual_length, int) else 128
+        if self.enable_kivi:
+            self._validate_kivi_geometry()
+        self.kivi_bits = 4
+        self.k_quant_cache = None
+        self.k_scale_cache = None
+        self.k_mn_cache = None
+        self.v_quant_cache = None
+        self.v_scale_cache = None
+        self.v_mn_cache = None
+        self._kivi_ring: KiviResidualRing | None = None
+        scheduler_config = getattr(vllm_config, "scheduler_config", None)
+        max_num_seqs = getattr(scheduler_config, "max_num_seqs", 128)
+        self.kivi_max_num_seqs = (
+            max_num_seqs if isinstance(max_num_seqs, int) and max_num_seqs > 0 else 128
+        )
+        self.kivi_residual_req_to_row: dict[str, int] = {}
+        self.kivi_residual_row_to_req: list[str | None] = []
+        self.kivi_residual_free_rows: list[int] = []
+
+    def _validate_kivi_geometry(self) -> None:
+        validate_kivi_geometry(
+            head_size=self.head_size,
+            group_size=self.kivi_group_size,
+            residual_length=self.kivi_residual_length,
+        )
+
+    def _kivi_sem(self) -> KiviInt4Semantics:
+        geometry = (self.head_size, self.kivi_group_size, self.kivi_residual_length)
+        memo = getattr(self, "_kivi_sem_memo", None)
+        if memo is not None and memo[0] == geometry:
+            return memo[1]
+        sem = KiviInt4Semantics(self)
+        self._kivi_sem_memo = (geometry, sem)
+        return sem
+
+    def _kivi_caches(self) -> tuple[torch.Tensor, ...]:
+        return (
+            self.k_quant_cache,
+            self.k_scale_cache,
+            self.k_mn_cache,
+            self.v_quant_cache,
+            self.v_scale_cache,
+            self.v_mn_cache,
+        )
+
+    def _check_kivi_cache_bound(self) -> None:
+        if any(t is None for t in self._kivi_caches()):
+            raise RuntimeError("KIVI cache tensors are not bound.")
+
+    def _get_kivi_block_size(self) -> int:
+        self._check_kivi_cache_bound()
+        return self.k_quant_cache.shape[-1] * 8
+
+    # ------------------------------------------------------------------
+    # cache binding (ab.py:135-175)
+    # ------------------------------------------------------------------
+
+    def _bind_kivi_cache(self, kv_cache: Any) -> None:
+        """Bind the paged cache: two host byte buffers (sliced into six views) or six tensors."""
+        if kv_cache is None:
+            return
+        if not isinstance(kv_cache, list | tuple):
+            raise RuntimeError(
+                "KIVI INT4 kv_cache must be a 2-tuple of byte buffers or a "
+                f"6-tuple, got {type(kv_cache)}."
+            )
+        if len(kv_cache) == 0:
+            return
+        if len(kv_cache) == 2:
+            layout = kivi_byte_cache_layout(
+                kv_cache[0],
+                kv_cache[1],
+                num_kv_heads=self.num_kv_heads,
+                head_size=self.head_size,
+                group_size=self.kivi_group_size,
+            )
+            kv_cache = kivi_caches_from_byte_tensors(kv_cache[0], kv_cache[1], layout)
+        if len(kv_cache) != 6:
+            raise RuntimeError(
+                "KIVI INT4 kv_cache must be a 2-tuple of byte buffers or a "
+                "6-tuple: (k_quant, k_scale, k_mn, v_quant, v_scale, v_mn)."
+            )
+        (
+            self.k_quant_cache,
+            self.k_scale_cache,
+            self.k_mn_cache,
+            self.v_quant_cache,
+            self.v_scale_cache,
+            self.v_mn_cache,
+        ) = kv_cache
+        self._ensure_kivi_residual_buffers()
+
+    # ------------------------------------------------------------------
+    # residual rows (ab.py:181-259)
+    # ------------------------------------------------------------------
+
+    def _ensure_kivi_residual_buffers(self) -> KiviResidualRing:
+        if self._kivi_ring is not None:
+            return self._kivi_ring
+        self._check_kivi_cache_bound()
+        rows = self.kivi_max_num_seqs
+        self._kivi_ring = KiviResidualRing(
+            rows,
+            self.kivi_residual_length,
+            self.num_kv_heads,
+            self.head_size,
+            device=self.k_quant_cache.device,
+            dtype=self.k_scale_cache.dtype,
+        )
+        self.kivi_residual_req_to_row = {}
+        self.kivi_residual_row_to_req = [None] * rows
+        self.kivi_residual_free_rows = list(range(rows - 1, -1, -1))
+        return self._kivi_ring
+
+    # the ring tensors and window state under the reference's attribute names
+    @property
+    def kivi_residual_key_cache(self) -> torch.Tensor | None:
+        return None if self._kivi_ring is None else self._kivi_ring.key
+
+    @property
+    def kivi_residual_value_cache(self) -> torch.Tensor | None:
+        return None if self._kivi_ring is None else self._kivi_ring.value
+
+    @property
+    def kivi_residual_key_start(self) -> list[int]:
+        return self._ensure_kivi_residual_buffers().start[True]
+
+    @property
+    def kivi_residual_key_len(self) -> list[int]:
+        return self._ensure_kivi_residual_buffers().length[True]
+
+    @property
+    def kivi_residual_value_start(self) -> list[int]:
+        return self._ensure_kivi_residual_buffers().start[False]
+
+    @property
+    def kivi_residual_value_len(self) -> list[int]:
+        return self._ensure_kivi_residual_buffers().length[False]
+
+    def _get_kivi_req_keys(self, req_ids: list[str] | None, num_reqs: int) -> list[str]:
+        if req_ids is not None and len(req_ids) >= num_reqs:
+            return [str(r) for r in req_ids[:num_reqs]]
+        return [f"__kivi_batch_row_{i}" for i in range(num_reqs)]
+
+    def _get_kivi_residual_row(self, req_key: str, *, create: bool) -> int | None:
+        self._ensure_kivi_residual_buffers()
+        row = self.kivi_residual_req_to_row.get(req_key)
+        if row is not None or not create:
+            return row
+        if not self.kivi_residual_free_rows:
+            raise RuntimeError(
+                "KIVI residual rows are exhausted. "
+                f"max_num_seqs={self.kivi_max_num_seqs}, req_id={req_key}."
+            )
+        row = self.kivi_residual_free_rows.pop()
+        self.kivi_residual_req_to_row[req_key] = row
+        self.kivi_residual_row_to_req[row] = req_key
+        return row
+
+    def _release_kivi_residual_row(self, req_key: str) -> None:
+        row = self.kivi_residual_req_to_row.pop(req_key, None)
+        if row is None:
+            return
+        self.kivi_residual_row_to_req[row] = None
+        self._kivi_ring.reset_row(row)
+        self.kivi_residual_free_rows.append(row)
+
+    def _release_finished_kivi_residual_rows(self, finished_req_keys: set[str]) -> None:
+        for key in finished_req_keys:
+            self._release_kivi_residual_row(key)
+
+    # ------------------------------------------------------------------
+    # window queries (ab.py:286-326, 485-492)
+    # ------------------------------------------------------------------
+
+    def _get_kivi_residual_lanes(self, row_idx: int, *, is_key: bool) -> list[int]:
+        return self._ensure_kivi_residual_buffers().lanes(row_idx, is_key=is_key)
+
+    def _collect_kivi_residual_window(
+        self,
+        req_key: str,
+        *,
+        is_key: bool,
+        target_dtype: Any | None = None,
+        target_device: Any | None = None,
+    ) -> tuple[list[int], torch.Tensor | None]:
+        """``(slots, rows)`` of a request's window in FIFO order."""
+        ring = self._ensure_kivi_residual_buffers()
+        row = self._get_kivi_residual_row(req_key, create=False)
+        if row is None:
+            return [], None
+        lanes = ring.lanes(row, is_key=is_key)
+        if not lanes:
+            return [], None
+        lane_t = torch.tensor(lanes, dtype=torch.long, device=ring.device)
+        rows = ring.tensor(is_key)[row].index_select(0, lane_t)
+        if target_dtype is not None or target_device is not None:
+            rows = rows.to(
+                device=target_device or rows.device, dtype=target_dtype or rows.dtype
+            )
+        return ring.window_slots(row, is_key=is_key), rows
+
+    def _has_kivi_residual_entry(self, slot: int, *, req_key: str, is_key: bool) -> bool:
+        row = self._get_kivi_residual_row(req_key, create=False)
+        if row is None:
+            return False
+        return self._kivi_ring.holds(row, int(slot), is_key=is_key)
+
+    # ------------------------------------------------------------------
+    # window writes (ab.py:377-462, 562-674)
+    # ------------------------------------------------------------------
+
+    def _execute_kivi_plan(self, plan: StorePlan, key: Any, value: Any) -> None:
+        if plan.empty():
+            return
+        self._kivi_ring.execute(
+            plan,
+            key,
+            value,
+            pack_key=self._launch_kivi_key_pack,
+            pack_value=self._launch_kivi_value_pack,
+            ring_write=self._launch_kivi_ring_write,
+        )
+
+    def _adopt_ring_dtype(self, *tensors: Any) -> None:
+        ring = self._ensure_kivi_residual_buffers()
+        for t in tensors:
+            if t is not None:
+                ring.adopt_dtype(t.dtype)
+
+    def _store_kivi_residual_entries(
+        self, values: torch.Tensor, slots: torch.Tensor, *, req_key: str, is_key: bool
+    ) -> None:
+        """Append tokens to a request's window; a full window flushes first.
+
+        In-place overwrite for held slots; keys flush the whole window, values
+        evict their single oldest entry (``ab.py:411-462``).
+        """
+        if values.numel() == 0 or slots.numel() == 0:
+            return
+        self._adopt_ring_dtype(values)
+        row = self._get_kivi_residual_row(req_key, create=True)
+        plan = StorePlan()
+        slot_list = _host_list(slots)
+        self._kivi_ring.plan_store(
+            plan, row, slot_list, list(range(len(slot_list))), is_key=is_key,
+            block_size=self._get_kivi_block_size(), group_size=self.kivi_group_size,
+        )
+        self._execute_kivi_plan(plan, values if is_key else None, None if is_key else values)
+
+    def _flush_kivi_residual_prefix(self, req_key: str, *, is_key: bool, count: int) -> None:
+        row = self._get_kivi_residual_row(req_key, create=False)
+        if row is None:
+            return
+        plan = StorePlan()
+        self._kivi_ring.flush_prefix(
+            plan, row, count, is_key=is_key, block_size=self._get_kivi_block_size(),
+            group_size=self.kivi_group_size,
+        )
+        self._execute_kivi_plan(plan, None, None)
+
+    def _request_spans(self, slot_mapping: Any, actual_seq_qlen: Any
+                       ) -> tuple[list[tuple[int, int]], int]:
+        """``([(start, end)] per request, number of requests)`` from cumulative lengths.
+
+        Same walk as ``ab.py:578-590``: spans stop at the slot mapping's end and
+        empty spans keep their request index.
+        """
+        if isinstance(actual_seq_qlen, torch.Tensor):
+            actual_seq_qlen = actual_seq_qlen.tolist()
+        max_tokens = int(slot_mapping.shape[0])
+        spans, prev = [], 0
+        for q_end in actual_seq_qlen:
+            q_end = min(int(q_end), max_tokens)
+            if prev >= max_tokens:
+                break
+            spans.append((prev, q_end))
+            prev = q_end
+        return spans, len(actual_seq_qlen)
+
+    def _write_kivi_cache(
+        self, key: Any, value: Any, slot_mapping: Any, req_ids: list[str] | None,
+        actual_seq_qlen: list[int] | Any,
+    ) -> None:
+        """Token-by-token residual writes for every request of the step (``ab.py:562-606``)."""
+        if key is None or value is None or slot_mapping is None:
+            return
+        spans, num_reqs = self._request_spans(slot_mapping, actual_seq_qlen)
+        if not spans:
+            return
+        self._check_kivi_cache_bound()
+        self._adopt_ring_dtype(key, value)
+        slots = _host_list(slot_mapping)
+        keys = self._get_kivi_req_keys(req_ids, num_reqs)
+        bs, g = self._get_kivi_block_size(), self.kivi_group_size
+        plan = StorePlan()
+        for i, (start, end) in enumerate(spans):
+            if end <= start:
+                continue
+            rows = [t for t in range(start, end) if slots[t] >= 0]
+            if not rows:
+                continue
+            row = self._get_kivi_residual_row(keys[i], create=True)
+            req_slots = [slots[t] for t in rows]
+            self._kivi_ring.plan_store(plan, row, req_slots, rows, is_key=True,
+                                       block_size=bs, group_size=g)
+            self._kivi_ring.plan_store(plan, row, req_slots, rows, is_key=False,
+                                       block_size=bs, group_size=g)
+        self._execute_kivi_plan(plan, key, value)
+
+    def _write_kivi_prefill_cache(
+        self, key: Any, value: Any, slot_mapping: Any, req_ids: list[str] | None,
+        actual_seq_qlen: list[int] | Any,
+    ) -> None:
+        """Bulk prefill: ``floor(n/R)*R`` tokens straight to history, the rest to the window.
+
+        ``ab.py:608-674``.
+        """
+        if key is None or value is None or slot_mapping is None:
+            return
+        spans, num_reqs = self._request_spans(slot_mapping, actual_seq_qlen)
+        if not spans:
+            return
+        self._check_kivi_cache_bound()
+        slots = _host_list(slot_mapping)
+        keys = self._get_kivi_req_keys(req_ids, num_reqs)
+        r = self.kivi_residual_length
+        bs, g = self._get_kivi_block_size(), self.kivi_group_size
+        ring = self._ensure_kivi_residual_buffers()
+        na = ring.rows * ring.ring_len
+        plan = StorePlan()
+        adopted = False
+        for i, (start, end) in enumerate(spans):
+            if end <= start:
+                continue
+            rows = [t for t in range(start, end) if slots[t] >= 0]
+            if not rows:
+                continue
+            flush = (len(rows) // r) * r
+            if flush:
+                self._check_key_flush(key, [slots[t] for t in rows[:flush]])
+                for side in (plan.key, plan.value):
+                    side.pack_src.extend(na + t for t in rows[:flush])
+                    side.pack_slots.extend(slots[t] for t in rows[:flush])
+            if flush < len(rows):
+                if not adopted:
+                    self._adopt_ring_dtype(key, value)
+                    adopted = True
+                row = self._get_kivi_residual_row(keys[i], create=True)
+                rest = rows[flush:]
+                rest_slots = [slots[t] for t in rest]
+                ring.plan_store(plan, row, rest_slots, rest, is_key=True, block_size=bs,
+                                group_size=g)
+                ring.plan_store(plan, row, rest_slots, rest, is_key=False, block_size=bs,
+                                group_size=g)
+        self._execute_kivi_plan(plan, key, value)
+
+    def _check_key_flush(self, key: Any, slots: list[int]) -> None:
+        """Validation of a key flush before any launch (``ab.py:676-726``)."""
+        if key.shape[-1] != self.head_size:
+            raise RuntimeError(
+                "KIVI INT4 key head_size must match attention head_size "
+                f"({self.head_size}), got {key.shape[-1]}."
+            )
+        if len(slots) % self.kivi_group_size != 0:
+            raise RuntimeError(
+                "KIVI key flush must contain whole token groups, got "
+                f"{len(slots)} tokens for group_size={self.kivi_group_size}."
+            )
+        if self.head_size % 8 != 0:
+            raise RuntimeError(
+                f"KIVI INT4 int32 packing requires head_size ({self.head_size}) "
+                "to be divisible by 8."
+            )
+        if self.kivi_group_size % 8 != 0:
+            raise RuntimeError(
+                "KIVI INT4 key packing requires kivi_group_size "
+                f"({self.kivi_group_size}) to be divisible by 8."
+            )
+        block_size = self._get_kivi_block_size()
+        if block_size % self.kivi_group_size != 0:
+            raise RuntimeError(
+                f"KIVI INT4 key cache requires block_size ({block_size}) to be "
+                f"divisible by kivi_group_size ({self.kivi_group_size})."
+            )
+        if not self._kivi_sem().is_aligned_key_window(slots, block_size):
+            raise RuntimeError("KIVI key flush requires contiguous aligned token groups.")
+
+    def _write_kivi_key_quant_cache(self, key: Any, slot_mapping: Any) -> None:
+        """Pack whole key groups into history after the reference's checks."""
+        self._check_kivi_cache_bound()
+        if key is None or slot_mapping is None:
+            return
+        slots = _host_list(slot_mapping)
+        keep = [i for i, s in enumerate(slots) if s >= 0]
+        if not keep:
+            return
+        if len(keep) != len(slots):
+            idx = torch.tensor(keep, dtype=torch.long, device=key.device)
+            key = key.index_select(0, idx)
+            slots = [slots[i] for i in keep]
+        self._check_key_flush(key, slots)
+        slot_t = torch.tensor(slots, dtype=torch.long).to(self.k_quant_cache.device)
+        self._launch_kivi_key_pack(key.contiguous(), None, None, slot_t)
+
+    def _write_kivi_value_quant_cache(self, value: Any, slot_mapping: Any) -> None:
+        self._check_kivi_cache_bound()
+        if value is None or slot_mapping is None:
+            return
+        slots = _host_list(slot_mapping)
+        keep = [i for i, s in enumerate(slots) if s >= 0]
+        if not keep:
+            return
+        head_size = value.shape[-1]
+        if head_size != self.head_size:
+            raise RuntimeError(
+                "KIVI INT4 value head_size must match attention head_size "
+                f"({self.head_size}), got {head_size}."
+            )
+        if head_size % self.kivi_group_size != 0:
+            raise RuntimeError(
+                f"KIVI INT4 value head_size ({head_size}) must be divisible by "
+                f"kivi_group_size ({self.kivi_group_size})."
+            )
+        if len(keep) != len(slots):
+            idx = torch.tensor(keep, dtype=torch.long, device=value.device)
+            value = value.index_select(0, idx)
+            slots = [slots[i] for i in keep]
+        slot_t = torch.tensor(slots, dtype=torch.long).to(self.v_quant_cache.device)
+        self._launch_kivi_value_pack(value.contiguous(), None, None, slot_t)
+
+    # ------------------------------------------------------------------
+    # launch hooks (HIP kernels; tests replace them)
+    # ------------------------------------------------------------------
+
+    def _launch_kivi_key_pack(self, src_a: Any, src_b: Any, src_index: Any, slots: Any) -> None:
+        from ...ops.kivi_pack import pack_key_rows
+
+        pack_key_rows(src_a, src_b, src_index, slots, self.k_quant_cache, self.k_scale_cache,
+                      self.k_mn_cache, self.kivi_group_size)
+
+    def _launch_kivi_value_pack(self, src_a: Any, src_b: Any, src_index: Any, slots: Any) -> None:
+        from ...ops.kivi_pack import pack_value_rows
+
+        pack_value_rows(src_a, src_b, src_index, slots, self.v_quant_cache, self.v_scale_cache,
+                        self.v_mn_cache, self.kivi_group_size)
+
+    def _launch_kivi_ring_write(self, src: Any, src_rows: Any, dst_rows: Any, is_key: bool) -> None:
+        from ...ops.kivi_pack import ring_write
+
+        ring_write(self._kivi_ring.tensor(is_key), src, src_rows, dst_rows)
+
+    def _launch_kivi_gather(self, block_table: Any, cu_seqlens: Any, total: int,
+                            target_dtype: Any, ring_meta: Any) -> tuple[Any, Any]:
+        from ...ops.kivi_gather import gather_dequant_with_residual
+
+        return gather_dequant_with_residual(
+            self._kivi_caches(), block_table, cu_seqlens, total, target_dtype,
+            self.kivi_group_size, ring_meta, self._kivi_ring.key, self._kivi_ring.value,
+        )
+
+    def _launch_kivi_decode(self, query: Any, block_table: Any, seqs: list, out: Any) -> Any:
+        from ...ops.kivi_decode import kivi_decode_attention
+
+        return kivi_decode_attention(
+            query, self._kivi_caches(), block_table, seqs, self._kivi_ring.key,
+            self._kivi_ring.value, self.scale, self.kivi_group_size, out=out,
+        )
+
+    def _launch_dense_attention(self, query: Any, key: Any, value: Any, q_lens: list[int],
+                                kv_lens: list[int], causal: bool, out: Any) -> Any:
+        from ...ops.attention import prefill_attention
+
+        return prefill_attention(query, key, value, q_lens, kv_lens, self.scale, causal, out=out)
+
+    # ------------------------------------------------------------------
+    # per-step window sync (ab.py:813-836)
+    # ------------------------------------------------------------------
+
+    def _sync_kivi_residual_windows(
+        self, block_table: Any, seq_lens: list[int], req_ids: list[str] | None,
+        finished_req_ids: set[str] | None = None,
+    ) -> None:
+        """Release finished rows and drop window entries a request no longer owns."""
+        keys = self._get_kivi_req_keys(req_ids, len(seq_lens))
+        if finished_req_ids:
+            self._release_finished_kivi_residual_rows({str(r) for r in finished_req_ids})
+        ring = self._ensure_kivi_residual_buffers()
+        bs = self._get_kivi_block_size()
+        table: list[list[int]] | None = None
+        for i, n in enumerate(seq_lens):
+            row = self._get_kivi_residual_row(keys[i], create=False)
+            if row is None:
+                continue
+            if ring.length[True][row] == 0 and ring.length[False][row] == 0:
+                continue
+            if table is None:
+                table = (block_table.to("cpu", torch.long).tolist()
+                         if isinstance(block_table, torch.Tensor)
+                         else [list(r) for r in block_table])
+            cols: dict[int, int] = {}
+            for c, blk in enumerate(table[i] if i < len(table) else []):
+                if int(blk) >= 0 and int(blk) not in cols:
+                    cols[int(blk)] = c
+            n = int(n)
+
+            def live(slot: int) -> bool:
+                c = cols.get(slot // bs)
+                return c is not None and c * bs + slot % bs < n
+
+            for is_key in (True, False):
+                held = ring.window_slots(row, is_key=is_key)
+                keep = {s for s in held if live(s)}
+                if len(keep) != len(held):
+                    self._compact_kivi_window(row, keep, is_key=is_key)
+
+    def _clear_stale_kivi_residual_entries(self, req_key: str, live_slots: set[int], *,
+                                           is_key: bool) -> None:
+        row = self._get_kivi_residual_row(req_key, create=False)
+        if row is None:
+            return
+        self._compact_kivi_window(row, {int(s) for s in live_slots}, is_key=is_key)
+
+    def _compact_kivi_window(self, row: int, keep: set[int], *, is_key: bool) -> None:
+        ring = self._kivi_ring
+        lanes_before = ring.lanes(row, is_key=is_key)
+        slots_before = ring.window_slots(row, is_key=is_key)
+        kept = [ln for ln, s in zip(lanes_before, slots_before) if s in keep]
+        moves = ring.keep_only(row, keep, is_key=is_key)
+        if not moves:
+            return
+        base = row * ring.ring_len
+        flat = ring.tensor(is_key).view(-1, ring.num_kv_heads, ring.head_size)
+        src_rows = torch.tensor([base + ln for ln in kept], dtype=torch.long, device=ring.device)
+        staged = flat.index_select(0, src_rows)  # copy first: sources and targets overlap
+        dst = torch.arange(base, base + len(kept), dtype=torch.long, device=ring.device)
+        self._launch_kivi_ring_write(staged, None, dst, is_key)
+
+    # ------------------------------------------------------------------
+    # gather + overlay (ab.py:849-935)
+    # ------------------------------------------------------------------
+
+    def _ring_meta_rows(self, seq_lens: list[int], req_keys: list[str]) -> list[list[int]]:
+        ring = self._kivi_ring
+        meta = []
+        for i, n in enumerate(seq_lens):
+            row = self._get_kivi_residual_row(req_keys[i], create=False)
+            if row is None:
+                meta.append([0, 0, 0, 0, 0])
+                continue
+            kt, kf = ring.tail(row, int(n), is_key=True)
+            vt, vf = ring.tail(row, int(n), is_key=False)
+            meta.append([row, kf, kt, vf, vt])
+        return meta
+
+    def _gather_dequant_kivi_paged_cache(
+        self, block_table: Any, seq_lens: list[int], target_dtype: Any,
+        req_ids: list[str] | None = None,
+    ) -> tuple[Any, Any]:
+        """Dense TND K/V of every request: int4 history with the residual tail overlaid."""
+        from ...ops.kivi_layout import check_gather_metadata_host
+
+        self._ensure_kivi_residual_buffers()
+        dev = self.k_quant_cache.device
+        lens = [int(n) for n in seq_lens]
+        batch = len(lens)
+        bt = block_table[:batch].to(device=dev, dtype=torch.long).contiguous()
+        check_gather_metadata_host(
+            bt.to("cpu").tolist(), lens, max_blocks=bt.shape[1],
+            num_blocks=self.k_quant_cache.shape[0], block_size=self._get_kivi_block_size(),
+        )
+        keys = self._get_kivi_req_keys(req_ids, batch)
+        meta = torch.tensor(self._ring_meta_rows(lens, keys), dtype=torch.int32).to(dev)
+        cu = [0]
+        for n in lens:
+            cu.append(cu[-1] + n)
+        cu_t = torch.tensor(cu, dtype=torch.int64).to(dev)
+        return self._launch_kivi_gather(bt, cu_t, cu[-1], target_dtype, meta)
+
+    # ------------------------------------------------------------------
+    # attention paths (ab.py:937-1392)
+    # ------------------------------------------------------------------
+
+    def _decode_seqs(self, seq_lens: list[int], req_keys: list[str]) -> list:
+        from ...ops.kivi_decode import DecodeSeq
+
+        ring = self._kivi_ring
+        seqs = []
+        for i, n in enumerate(seq_lens):
+            n = int(n)
+            row = self._get_kivi_residual_row(req_keys[i], create=False)
+            if row is None:
+                seqs.append(DecodeSeq(n, n, n))
+                continue
+            kt, kf = ring.tail(row, n, is_key=True)
+            vt, vf = ring.tail(row, n, is_key=False)
+            seqs.append(DecodeSeq(n, n - kt, n - vt, row, kf, vf))
+        return seqs
+
+    def _is_kivi_chunked_prefill_all_new(self, attn_metadata: Any) -> bool:
+        qlen = attn_metadata.actual_seq_lengths_q
+        for i in range(attn_metadata.num_decodes, len(attn_metadata.seq_lens_list)):
+            q_start = qlen[i - 1] if i > 0 else 0
+            if attn_metadata.seq_lens_list[i] > qlen[i] - q_start:
+                return False
+        return True
+
+    def forward(
+        self,
+        layer: Any,
+        query: torch.Tensor,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        kv_cache: Any,
+        attn_metadata: Any,
+        output: torch.Tensor | None = None,
+        output_scale: torch.Tensor | None = None,
+        output_block_scale: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """INT4 forward entry (``ab.py:972-1004``); bypasses the host cache writer."""
+        assert output is not None, "Output tensor must be provided."
+        if not getattr(self, "enable_kivi", False):
+            raise RuntimeError(
+                "the KIVI INT4 attention impl was instantiated without the "
+                "kivi_int4 cache dtype; check the host get_impl_cls dispatch"
+            )
+        if output_scale is not None or output_block_scale is not None:
+            raise NotImplementedError(
+                "fused output quantization is not yet supported for "
+                "AscendKiviInt4AttentionBackendImpl"
+            )
+        if attn_metadata is None:
+            return output.fill_(0)
+        return self._forward_kivi_attention(query, key, value, attn_metadata, output, kv_cache)
+
+    def _forward_kivi_attention(
+        self, query: Any, key: Any, value: Any, attn_metadata: Any, output: Any,
+        kv_cache: Any = None,
+    ) -> Any:
+        """Dispatch by attention state (``ab.py:1006-1191``)."""
+        self._bind_kivi_cache(kv_cache)
+        finished = getattr(attn_metadata, "finished_req_ids", None)
+        if finished:
+            self._release_finished_kivi_residual_rows({str(r) for r in finished})
+
+        state = _attn_state_name(attn_metadata)
+        qlen = attn_metadata.actual_seq_lengths_q
+        if state == "DecodeOnly":
+            qlen = list(range(1, len(attn_metadata.seq_lens_list) + 1))
+        num_tokens = int(qlen[-1])
+        query = query[:num_tokens]
+        req_ids = getattr(attn_metadata, "req_ids", None)
+
+        def actual(t: Any) -> int:
+            return min(getattr(attn_metadata, "num_actual_tokens", t.shape[0]), t.shape[0])
+
+        if state == "PrefillNoCache":
+            if key is None or value is None:
+                raise RuntimeError("KIVI PrefillNoCache requires dense key/value.")
+            n = actual(key)
+            self._write_kivi_prefill_cache(
+                key[:n], value[:n], attn_metadata.slot_mapping[:n], req_ids,
+                attn_metadata.actual_seq_lengths_q,
+            )
+            return self._forward_kivi_prefill(query, key, value, attn_metadata, output)
+
+        if state == "ChunkedPrefill" and not self._is_kivi_chunked_prefill_all_new(attn_metadata):
+            raise RuntimeError(
+                "KIVI ChunkedPrefill does not support prefill requests with "
+                "historical KV cache. Only decode rows plus all-new prefill "
+                "prompts are supported."
+            )
+
+        seq_lens = attn_metadata.seq_lens_list
+        if state == "DecodeOnly":
+            if key is not None and value is not None and actual(key) > 0:
+                n = actual(key)
+                self._write_kivi_cache(key[:n], value[:n], attn_metadata.slot_mapping[:n],
+                                       req_ids, list(range(1, len(seq_lens) + 1)))
+            self._sync_kivi_residual_windows(attn_metadata.block_tables, seq_lens, req_ids,
+                                             finished)
+            return self._forward_kivi_paged_decode_attention(
+                query, attn_metadata.block_tables, seq_lens, req_ids, output
+            )
+
+        if state == "ChunkedPrefill":
+            if key is not None and value is not None and actual(key) > 0:
+                n = actual(key)
+                slot_mapping = attn_metadata.slot_mapping[:n]
+                nd = min(attn_metadata.num_decode_tokens, n)
+                ndr = attn_metadata.num_decodes
+                if nd > 0:
+                    self._write_kivi_cache(
+                        key[:nd], value[:nd], slot_mapping[:nd],
+                        None if req_ids is None else req_ids[:ndr], list(range(1, ndr + 1)),
+                    )
+                if nd < n:
+                    pq = [int(attn_metadata.actual_seq_lengths_q[i]) - nd
+                          for i in range(ndr, len(attn_metadata.actual_seq_lengths_q))]
+                    self._write_kivi_prefill_cache(
+                        key[nd:n], value[nd:n], slot_mapping[nd:n],
+                        None if req_ids is None else req_ids[ndr:], pq,
+                    )
+            self._sync_kivi_residual_windows(attn_metadata.block_tables, seq_lens, req_ids,
+                                             finished)
+            return self._forward_kivi_chunked_prefill(query, key, value, attn_metadata, output)
+
+        if key is not None and value is not None and actual(key) > 0:
+            n = actual(key)
+            self._write_kivi_cache(key[:n], value[:n], attn_metadata.slot_mapping[:n], req_ids,
+                                   attn_metadata.actual_seq_lengths_q)
+        self._sync_kivi_residual_windows(attn_metadata.block_tables, seq_lens, req_ids,
+                                         finished)
+        dense_k, dense_v = self._gather_dequant_kivi_paged_cache(
+            attn_metadata.block_tables, seq_lens, query.dtype, req_ids
+        )
+        return self._forward_kivi_dense_attention(
+            query, dense_k, dense_v, seq_lens, qlen, attn_metadata.causal, output
+        )
+
+    def _forward_kivi_paged_decode_attention(
+        self, query: Any, block_table: Any, seq_lens: list[int], req_ids: list[str] | None,
+        output: Any,
+    ) -> Any:
+        """One query token per request over int4 history + residual (``ab.py:1193-1230``)."""
+        batch = len(seq_lens)
+        keys = self._get_kivi_req_keys(req_ids, batch)
+        seqs = self._decode_seqs([int(n) for n in seq_lens], keys)
+        q = query[:batch].reshape(batch, self.num_heads, self.head_size)
+        out_view = output[:batch].view(batch, self.num_heads, self.head_size)
+        bt = block_table[:batch].to(device=q.device, dtype=torch.int32).contiguous()
+        got = self._launch_kivi_decode(q.contiguous(), bt, seqs, out_view)
+        if got is not None and got is not out_view:
+            out_view.copy_(got)
+        return output
+
+    def _forward_kivi_prefill(self, query: Any, key: Any, value: Any, attn_metadata: Any,
+                              output: Any) -> Any:
+        """Causal prefill on the raw prompt K/V (``ab.py:1232-1266``)."""
+        lens = KiviInt4Semantics.cu_seqlens_to_seq_lens(attn_metadata.actual_seq_lengths_q)
+        n = sum(lens)
+        out = output[:n].view(n, self.num_heads, self.head_size)
+        got = self._launch_dense_attention(
+            query[:n].reshape(n, self.num_heads, self.head_size), key[:n], value[:n], lens, lens,
+            bool(attn_metadata.causal), out,
+        )
+        if got is not None and got is not out:
+            out.copy_(got)
+        return output
+
+    # reference name of the same path
+    _forward_kivi_prefill_fia = _forward_kivi_prefill
+
+    def _forward_kivi_chunked_prefill(self, query: Any, key: Any, value: Any,
+                                      attn_metadata: Any, output: Any) -> Any:
+        """Decode rows on the paged cache, all-new prompt rows on their own K/V.
+
+        ``ab.py:1268-1339``.
+        """
+        nd = attn_metadata.num_decode_tokens
+        ndr = attn_metadata.num_decodes
+        qlen = attn_metadata.actual_seq_lengths_q
+        num_tokens = int(qlen[-1])
+        req_ids = getattr(attn_metadata, "req_ids", None)
+        if nd > 0:
+            self._forward_kivi_paged_decode_attention(
+                query[:nd], attn_metadata.block_tables[:ndr], attn_metadata.seq_lens_list[:ndr],
+                None if req_ids is None else req_ids[:ndr], output,
+            )
+        if attn_metadata.num_prefills <= 0:
+            return output
+        if key is None or value is None:
+            raise RuntimeError(
+                "KIVI ChunkedPrefill requires dense key/value for all-new prefill prompts."
+            )
+        if not self._is_kivi_chunked_prefill_all_new(attn_metadata):
+            raise RuntimeError(
+                "KIVI ChunkedPrefill prefill-with-history is disabled. Only "
+                "all-new prompt prefills are supported."
+            )
+        lens = [int(qlen[i]) - (int(qlen[i - 1]) if i > 0 else 0) for i in range(ndr, len(qlen))]
+        n = num_tokens - nd
+        out = output[nd:num_tokens].view(n, self.num_heads, self.head_size)
+        got = self._launch_dense_attention(
+            query[nd:num_tokens].reshape(n, self.num_heads, self.head_size),
+            key[nd:num_tokens], value[nd:num_tokens], lens, lens, bool(attn_metadata.causal), out,
+        )
+        if got is not None and got is not out:
+            out.copy_(got)
+        return output
+
+    def _forward_kivi_dense_attention(self, query: Any, key: Any, value: Any,
+                                      seq_lens: list[int], actual_seq_qlen: Any, causal: bool,
+                                      output: Any) -> Any:
+        """Attention of each request's queries over its dense K/V (``ab.py:1341-1392``)."""
+        q_lens = KiviInt4Semantics.cu_seqlens_to_seq_lens(actual_seq_qlen)
+        q_lens = q_lens[: len(seq_lens)]
+        n = sum(q_lens)
+        if n == 0:
+            return output
+        out = output[:n].view(n, self.num_heads, self.head_size)
+        got = self._launch_dense_attention(
+            query[:n].reshape(n, self.num_heads, self.head_size), key, value, q_lens,
+            [int(x) for x in seq_lens], bool(causal), out,
+        )
+        if got is not None and got is not out:
+            out.copy_(got)
+        return output
+
+
+__all__ = ["AscendKiviInt4AttentionBackendMixin"]

@@ -178,3 +178,27 @@ __all__ = [
     "int8_quant_scatter",
     "plan_int8_work",
 ]
+
+
+def int8_quantize(x: torch.Tensor, inv: torch.Tensor) -> torch.Tensor:
+    """Codes of ``x [T, KVH, D]`` through the quantize+scatter kernel (slot t -> row t)."""
+    t = x.shape[0]
+    kvh, d = inv.shape[-2], inv.shape[-1]
+    codes = torch.empty((t, 1, kvh, d), dtype=torch.int8, device=x.device)
+    if t == 0:
+        return codes.view(x.shape)
+    slots = torch.arange(t, dtype=torch.int64, device=x.device)
+    xx = x.reshape(t, kvh, d)
+    int8_quant_scatter(xx, xx, inv, inv, slots, codes, torch.empty_like(codes))
+    return codes.view(x.shape)
+
+
+def int8_dequantize(x: torch.Tensor, inv: torch.Tensor, target_dtype) -> torch.Tensor:
+    """``(x - 0) * (1/inv)`` in ``target_dtype`` through the paged dequant kernel."""
+    t = x.shape[0]
+    kvh, d = inv.shape[-2], inv.shape[-1]
+    aq = (1.0 / inv.to(target_dtype)).reshape(kvh * d)
+    pages = x.reshape(t, 1, kvh, d).contiguous()
+    table = torch.arange(t, dtype=torch.int32, device=x.device).view(1, t)
+    dk, _ = int8_dequant_gather(pages, pages, table, [t], target_dtype, aq, aq)
+    return dk.view(x.shape)
