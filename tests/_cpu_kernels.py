@@ -20,32 +20,24 @@ from oracle import kvq_oracle as ref
 ROOT = Path(__file__).resolve().parents[1]
 
 
-def _rows(src_a, src_b, src_index, n):
-    if src_index is None:
-        return src_a.reshape(-1, *src_a.shape[-2:])[:n]
-    flat_a = src_a.reshape(-1, *src_a.shape[-2:])
-    pool = flat_a if src_b is None else torch.cat([flat_a, src_b.to(flat_a.dtype)], dim=0)
-    return pool[src_index.long()]
-
-
 def install_cpu_kernels(impl) -> dict[str, list]:
     """Replace the KIVI mixin's launch hooks with oracle-backed CPU versions.
 
+    The pack hooks are replaced through their reference signature
+    ``(rows, slots)``, so the mixin's flush path hands them materialized rows.
     Returns call logs keyed by hook name.
     """
     calls: dict[str, list] = {"key_pack": [], "value_pack": [], "ring": [], "gather": [],
                               "decode": [], "dense": []}
 
-    def pack_key(src_a, src_b, src_index, slots):
-        rows = _rows(src_a, src_b, src_index, slots.numel())
-        calls["key_pack"].append((rows.clone(), slots.clone()))
-        ref.pack_key_cache(rows, slots, impl.k_quant_cache, impl.k_scale_cache,
+    def pack_key(key, slots):
+        calls["key_pack"].append((key.clone(), slots.clone()))
+        ref.pack_key_cache(key, slots, impl.k_quant_cache, impl.k_scale_cache,
                            impl.k_mn_cache, impl.kivi_group_size)
 
-    def pack_value(src_a, src_b, src_index, slots):
-        rows = _rows(src_a, src_b, src_index, slots.numel())
-        calls["value_pack"].append((rows.clone(), slots.clone()))
-        ref.pack_value_cache(rows, slots, impl.v_quant_cache, impl.v_scale_cache,
+    def pack_value(value, slots):
+        calls["value_pack"].append((value.clone(), slots.clone()))
+        ref.pack_value_cache(value, slots, impl.v_quant_cache, impl.v_scale_cache,
                              impl.v_mn_cache, impl.kivi_group_size)
 
     def ring_write(src, src_rows, dst_rows, is_key):

@@ -1,0 +1,107 @@
+# SPDX-License-Identifier: Apache-2.0
+"""The C-ABI library: it loads, exports every declared symbol, and the ctypes
+signatures match the header (no GPU; no compute call is made)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "kvq_hip.h"
+PKG = ROOT / "vllm-ascend-quantized-kv-cache-hust_amd" / "vllm_ascend_quantized_kv_cache"
+
+_C_TO_CTYPES = {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float}
+
+
+def _declarations() -> dict[str, tuple[str, list[str]]]:
+    """``name -> (return type, [parameter declarations])`` parsed from the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    decls = {}
+    for m in re.finditer(r"(?m)^(int64_t|int|size_t)\s+(kvq_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p.strip() for p in m.group(3).split(",") if p.strip() and p.strip() != "void"]
+        decls[m.group(2)] = (m.group(1), params)
+    return decls
+
+
+def _ctype_of(param: str):
+    if "*" in param:
+        return ctypes.c_void_p
+    base = param.replace("const", "").split()[0]
+    return _C_TO_CTYPES[base]
+
+
+def test_header_declares_the_c_abi():
+    decls = _declarations()
+    for name in ("kvq_kivi_pack_key", "kvq_kivi_pack_value", "kvq_kivi_gather_dequant",
+                 "kvq_kivi_decode_attn", "kvq_prefill_attn", "kvq_int8_calc_scales",
+                 "kvq_int8_quant_scatter", "kvq_int8_decode_attn"):
+        assert name in decls, name
+
+
+def test_ctypes_signatures_match_header():
+    from vllm_ascend_quantized_kv_cache.ops._native import SIGNATURES
+
+    decls = _declarations()
+    assert set(SIGNATURES) == set(decls)
+    for name, (ret, params) in decls.items():
+        restype, argtypes = SIGNATURES[name]
+        assert restype is _C_TO_CTYPES[ret], name
+        assert [_ctype_of(p) for p in params] == argtypes, name
+
+
+def test_library_exports_every_declared_symbol():
+    from vllm_ascend_quantized_kv_cache.ops import _native
+
+    path = _native.library_path()
+    if not path.exists():
+        pytest.skip("libkvq_hip.so not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(path))
+    missing = [n for n in _declarations() if not hasattr(lib, n)]
+    assert not missing
+    lib.kvq_abi_version.restype = ctypes.c_int
+    assert lib.kvq_abi_version() == 1  # pure host function, touches no device
+
+
+def test_workspace_sizes_are_host_computable():
+    from vllm_ascend_quantized_kv_cache.ops import _native
+
+    if not _native.library_path().exists():
+        pytest.skip("libkvq_hip.so not built")
+    lib = _native.lib()
+    # per work item: num_heads * (D + 2) fp32 (o accumulator, running max, sum)
+    assert lib.kvq_kivi_decode_workspace_bytes(10, 40, 128) == 10 * 40 * 130 * 4
+    assert lib.kvq_int8_decode_workspace_bytes(3, 32, 128) == 3 * 32 * 130 * 4
+
+
+def test_ops_refuse_cpu_tensors_loudly():
+    """The product path has no CPU fallback: host tensors raise before any launch."""
+    import torch
+
+    from vllm_ascend_quantized_kv_cache.ops.attention import prefill_attention
+    from vllm_ascend_quantized_kv_cache.ops.kivi_pack import kivi_pack_value_cache
+
+    v = torch.zeros(8, 1, 8)
+    caches = (torch.zeros(1, 8, 1, 1, dtype=torch.int32), torch.zeros(1, 8, 1, 1),
+              torch.zeros(1, 8, 1, 1))
+    with pytest.raises(RuntimeError, match="no CPU fallback|GPU"):
+        kivi_pack_value_cache(v, torch.arange(8), *caches, 8)
+    q = torch.zeros(4, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU fallback|GPU"):
+        prefill_attention(q, q, q, [4], [4], 0.125, True)
+
+
+def test_product_never_imports_the_oracle():
+    offenders = []
+    for path in PKG.rglob("*.py"):
+        text = path.read_text()
+        if re.search(r"^\s*(from|import)\s+oracle\b", text, flags=re.M) or "kvq_oracle" in text:
+            offenders.append(str(path))
+    for path in (PKG.parent / "csrc").glob("*"):
+        if "kvq_ref" in path.read_text(errors="ignore"):
+            offenders.append(str(path))
+    assert not offenders

@@ -40,6 +40,28 @@ def _host_list(x: Any) -> list[int]:
     return [int(v) for v in x]
 
 
+def _hook_replaced(impl: Any, name: str) -> bool:
+    """True when ``name`` was overridden on the instance or by a subclass."""
+    if name in vars(impl):
+        return True
+    return getattr(type(impl), name) is not getattr(AscendKiviInt4AttentionBackendMixin, name)
+
+
+def _gather_rows(src_a: Any, src_b: Any, src_index: Any) -> Any:
+    """Rows ``src_index`` of ``[src_a ; src_b]`` (both viewed as ``[n, KVH, D]``)."""
+    if src_index is None:
+        return src_a
+    n_a = src_a.shape[0]
+    idx = src_index.long()
+    out = torch.empty((idx.numel(), *src_a.shape[1:]), dtype=src_a.dtype, device=src_a.device)
+    in_a = idx < n_a
+    out[in_a] = src_a[idx[in_a]]
+    if src_b is not None and not bool(in_a.all()):
+        b = src_b.reshape(-1, *src_a.shape[1:]).to(src_a.dtype)
+        out[~in_a] = b[idx[~in_a] - n_a]
+    return out
+
+
 class AscendKiviInt4AttentionBackendMixin:
     """KIVI INT4 (int4 history + full-precision residual window) attention path."""
 
@@ -273,8 +295,8 @@ class AscendKiviInt4AttentionBackendMixin:
             plan,
             key,
             value,
-            pack_key=self._launch_kivi_key_pack,
-            pack_value=self._launch_kivi_value_pack,
+            pack_key=self._launch_kivi_key_pack_rows,
+            pack_value=self._launch_kivi_value_pack_rows,
             ring_write=self._launch_kivi_ring_write,
         )
 
@@ -384,8 +406,8 @@ class AscendKiviInt4AttentionBackendMixin:
         bs, g = self._get_kivi_block_size(), self.kivi_group_size
         ring = self._ensure_kivi_residual_buffers()
         na = ring.rows * ring.ring_len
+        self._adopt_ring_dtype(key, value)
         plan = StorePlan()
-        adopted = False
         for i, (start, end) in enumerate(spans):
             if end <= start:
                 continue
@@ -399,9 +421,6 @@ class AscendKiviInt4AttentionBackendMixin:
                     side.pack_src.extend(na + t for t in rows[:flush])
                     side.pack_slots.extend(slots[t] for t in rows[:flush])
             if flush < len(rows):
-                if not adopted:
-                    self._adopt_ring_dtype(key, value)
-                    adopted = True
                 row = self._get_kivi_residual_row(keys[i], create=True)
                 rest = rows[flush:]
                 rest_slots = [slots[t] for t in rest]
@@ -457,7 +476,7 @@ class AscendKiviInt4AttentionBackendMixin:
             slots = [slots[i] for i in keep]
         self._check_key_flush(key, slots)
         slot_t = torch.tensor(slots, dtype=torch.long).to(self.k_quant_cache.device)
-        self._launch_kivi_key_pack(key.contiguous(), None, None, slot_t)
+        self._launch_kivi_key_pack(key.to(self.k_scale_cache.dtype).contiguous(), slot_t)
 
     def _write_kivi_value_quant_cache(self, value: Any, slot_mapping: Any) -> None:
         self._check_kivi_cache_bound()
@@ -478,24 +497,63 @@ class AscendKiviInt4AttentionBackendMixin:
                 f"KIVI INT4 value head_size ({head_size}) must be divisible by "
                 f"kivi_group_size ({self.kivi_group_size})."
             )
+        if head_size % 8 != 0:
+            raise RuntimeError(
+                f"KIVI INT4 int32 packing requires head_size ({head_size}) "
+                "to be divisible by 8."
+            )
+        if self.kivi_group_size % 8 != 0:
+            raise RuntimeError(
+                "KIVI INT4 value packing requires kivi_group_size "
+                f"({self.kivi_group_size}) to be divisible by 8."
+            )
         if len(keep) != len(slots):
             idx = torch.tensor(keep, dtype=torch.long, device=value.device)
             value = value.index_select(0, idx)
             slots = [slots[i] for i in keep]
         slot_t = torch.tensor(slots, dtype=torch.long).to(self.v_quant_cache.device)
-        self._launch_kivi_value_pack(value.contiguous(), None, None, slot_t)
+        self._launch_kivi_value_pack(value.to(self.v_scale_cache.dtype).contiguous(), slot_t)
 
     # ------------------------------------------------------------------
     # launch hooks (HIP kernels; tests replace them)
     # ------------------------------------------------------------------
 
-    def _launch_kivi_key_pack(self, src_a: Any, src_b: Any, src_index: Any, slots: Any) -> None:
+    def _launch_kivi_key_pack(self, key: Any, slots: Any) -> None:
+        """Pack ``key[T, KVH, D]`` into history at ``slots`` (``ab.py:728-739``)."""
+        from ...ops.kivi_pack import kivi_pack_key_cache
+
+        kivi_pack_key_cache(key, slots, self.k_quant_cache, self.k_scale_cache,
+                            self.k_mn_cache, self.kivi_group_size)
+
+    def _launch_kivi_value_pack(self, value: Any, slots: Any) -> None:
+        """Pack ``value[T, KVH, D]`` into history at ``slots`` (``ab.py:779-790``)."""
+        from ...ops.kivi_pack import kivi_pack_value_cache
+
+        kivi_pack_value_cache(value, slots, self.v_quant_cache, self.v_scale_cache,
+                              self.v_mn_cache, self.kivi_group_size)
+
+    def _launch_kivi_key_pack_rows(self, src_a: Any, src_b: Any, src_index: Any,
+                                   slots: Any) -> None:
+        """Pack rows picked from ``[ring ; step input]`` in one launch (flush path).
+
+        If the reference-signature hook ``_launch_kivi_key_pack`` has been
+        replaced, the rows are materialized (cast to the scale dtype, as the
+        reference hands them over) and passed to it instead.
+        """
+        if _hook_replaced(self, "_launch_kivi_key_pack"):
+            rows = _gather_rows(src_a, src_b, src_index).to(self.k_scale_cache.dtype)
+            return self._launch_kivi_key_pack(rows, slots)
         from ...ops.kivi_pack import pack_key_rows
 
         pack_key_rows(src_a, src_b, src_index, slots, self.k_quant_cache, self.k_scale_cache,
                       self.k_mn_cache, self.kivi_group_size)
 
-    def _launch_kivi_value_pack(self, src_a: Any, src_b: Any, src_index: Any, slots: Any) -> None:
+    def _launch_kivi_value_pack_rows(self, src_a: Any, src_b: Any, src_index: Any,
+                                     slots: Any) -> None:
+        """Value counterpart of ``_launch_kivi_key_pack_rows``."""
+        if _hook_replaced(self, "_launch_kivi_value_pack"):
+            rows = _gather_rows(src_a, src_b, src_index).to(self.v_scale_cache.dtype)
+            return self._launch_kivi_value_pack(rows, slots)
         from ...ops.kivi_pack import pack_value_rows
 
         pack_value_rows(src_a, src_b, src_index, slots, self.v_quant_cache, self.v_scale_cache,
@@ -700,9 +758,10 @@ class AscendKiviInt4AttentionBackendMixin:
             self._release_finished_kivi_residual_rows({str(r) for r in finished})
 
         state = _attn_state_name(attn_metadata)
-        qlen = attn_metadata.actual_seq_lengths_q
-        if state == "DecodeOnly":
+        if state == "DecodeOnly":  # one query token per request
             qlen = list(range(1, len(attn_metadata.seq_lens_list) + 1))
+        else:
+            qlen = attn_metadata.actual_seq_lengths_q
         num_tokens = int(qlen[-1])
         query = query[:num_tokens]
         req_ids = getattr(attn_metadata, "req_ids", None)

@@ -171,15 +171,6 @@ def int8_decode_attention(
     return out
 
 
-__all__ = [
-    "int8_calc_scales",
-    "int8_decode_attention",
-    "int8_dequant_gather",
-    "int8_quant_scatter",
-    "plan_int8_work",
-]
-
-
 def int8_quantize(x: torch.Tensor, inv: torch.Tensor) -> torch.Tensor:
     """Codes of ``x [T, KVH, D]`` through the quantize+scatter kernel (slot t -> row t)."""
     t = x.shape[0]
@@ -202,3 +193,14 @@ def int8_dequantize(x: torch.Tensor, inv: torch.Tensor, target_dtype) -> torch.T
     table = torch.arange(t, dtype=torch.int32, device=x.device).view(1, t)
     dk, _ = int8_dequant_gather(pages, pages, table, [t], target_dtype, aq, aq)
     return dk.view(x.shape)
+
+
+__all__ = [
+    "int8_calc_scales",
+    "int8_decode_attention",
+    "int8_dequant_gather",
+    "int8_dequantize",
+    "int8_quant_scatter",
+    "int8_quantize",
+    "plan_int8_work",
+]
