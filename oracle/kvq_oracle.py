@@ -354,7 +354,14 @@ def int8_paged_dequant(
     k_inv: torch.Tensor,
     v_inv: torch.Tensor,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Paged int8 -> dense TND; i8ab.py:370-404 (``(x - 0) * (1/inv)``)."""
+    """Paged int8 -> dense TND; i8ab.py:370-404 (``(x - 0) * (1/inv)``).
+
+    With ``target_dtype`` equal to the activation dtype this is the dense
+    dequant of the prefill branches.  With ``torch.float32`` it is the
+    per-channel antiquant of the fused decode (``i8ab.py:183-199``,
+    ``antiquant_mode=0``): ``code * aq`` with ``aq = 1/inv`` still rounded to
+    the activation dtype, the product kept in fp32.
+    """
     nb, bs, kvh, d = key_cache.shape
     batch, maxb = block_table.shape
     ids = block_table.reshape(-1).long()

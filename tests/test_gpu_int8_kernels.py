@@ -101,7 +101,8 @@ def test_int8_decode_matches_oracle(gpu_device, rep, kvh, d, bs):
     hq = kvh * rep
     q = torch.randn(len(lens), hq, d, generator=torch.Generator().manual_seed(2)).to(dtype)
     scale = d ** -0.5
-    dk, dv = ref.int8_paged_dequant(kc, vc, table, lens, dtype, k_inv, v_inv)
+    # antiquant semantics: code * aq with aq = dtype(1/inv), evaluated in fp32
+    dk, dv = ref.int8_paged_dequant(kc, vc, table, lens, torch.float32, k_inv, v_inv)
     want = ref.attention(q, dk, dv, [1] * len(lens), lens, scale, causal=True)
     for split in (None, 100):
         got = int8_decode_attention(

@@ -107,7 +107,9 @@ def test_kivi_mixin_serving_flow_matches_oracle(gpu_device, geom):
             for name in ("slot_mapping", "block_tables"):
                 if hasattr(m, name):
                     setattr(m, name, getattr(m, name).to(dev))
-            out = torch.zeros(out_shape, dtype=dt, device=dev)
+            # the oracle side keeps its fp32 result (no second bf16 rounding)
+            out = torch.zeros(out_shape, dtype=dt if impl is gpu else torch.float32,
+                              device=dev)
             impl.forward(None, q.to(dev), None if k is None else k.to(dev),
                          None if v is None else v.to(dev), None, m, out)
             outs.append(out.float().cpu())
@@ -247,6 +249,8 @@ def test_int8_mixin_prefill_then_decode_matches_oracle(gpu_device):
     ref.int8_reshape_and_cache(kd, vd, k_inv, v_inv, torch.tensor(new), want_cache[0],
                                want_cache[1])
     assert torch.equal(cache.cpu(), want_cache)
-    dk, dv = ref.int8_paged_dequant(want_cache[0], want_cache[1], table, lens, dt, k_inv, v_inv)
+    # decode is FIA's per-channel antiquant: code * aq (aq = bf16(1/inv)) in fp32
+    dk, dv = ref.int8_paged_dequant(want_cache[0], want_cache[1], table, lens, torch.float32,
+                                    k_inv, v_inv)
     want = ref.attention(qd, dk, dv, [1, 1, 1], lens, d ** -0.5, True)
     torch.testing.assert_close(out.float().cpu(), want, **TOL)

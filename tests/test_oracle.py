@@ -333,3 +333,17 @@ def test_oracle_is_deterministic_under_shuffle():
     ref.pack_value_cache(value[perm], slots[perm], *b[3:], g)
     for x, y in zip(a[3:], b[3:]):
         assert torch.equal(x, y)
+
+
+def test_int8_antiquant_keeps_bf16_scale_in_fp32_product():
+    """Decode antiquant: code * bf16(1/inv), product in fp32 (no bf16 rounding of K)."""
+    g = torch.Generator().manual_seed(13)
+    kc = torch.randint(-128, 128, (2, 4, 1, 8), generator=g, dtype=torch.int8)
+    inv = (torch.rand(1, 1, 8, generator=g) * 300 + 1).to(torch.bfloat16)
+    dk, _ = ref.int8_paged_dequant(kc, kc, torch.tensor([[1, 0]]), [7], torch.float32, inv, inv)
+    aq = (1.0 / inv).to(torch.bfloat16).float()[0]  # the scale itself is a bf16 value
+    rows = [kc[[1, 0][p // 4], p % 4].float() * aq for p in range(7)]
+    assert dk.dtype == torch.float32 and torch.equal(dk, torch.stack(rows))
+    dense, _ = ref.int8_paged_dequant(kc, kc, torch.tensor([[1, 0]]), [7], torch.bfloat16, inv,
+                                      inv)
+    assert torch.equal(dense, dk.to(torch.bfloat16))  # dense prefill path rounds once more

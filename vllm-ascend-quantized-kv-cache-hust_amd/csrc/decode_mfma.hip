@@ -10,11 +10,13 @@
 //   A = key codes, row m = token, 8 head dims per lane.  A key word packs 8
 //       tokens of one dim, so a lane loads 8 words (8 dims x 8 tokens of its
 //       chunk) and builds each register from one nibble of two words with
-//       v_perm_b32 + v_and_or_b32 as the exact fp16 value 1024 + code.
-//   B = Q' = q * softmax_scale * log2(e) * key_scale(dim, group), fp16,
-//       column n = query head of the GQA group.
-//   The 1024 offset is removed with one more MFMA per k-step whose A operand
-//   is the constant 1024: it sees exactly the B operand the score MFMA saw.
+//       v_perm_b32 + v_and_or_b32 as the fp16 value 1024 + code, then one
+//       packed fp16 subtract leaves the exact code (0..15).
+//   B = Q' = q * softmax_scale * log2(e) * key_scale(dim, group), column n =
+//       query head of the GQA group, split into two fp16 parts hi + lo
+//       (hi = fp16(Q'), lo = fp16(Q' - hi)) and applied with two MFMAs: the
+//       products are exact and Q' keeps ~22 bits, so outlier key channels
+//       (large key_scale) do not turn fp16 rounding into score error.
 //   The per-group key minimum adds sum_d q*mn (fp32) to every score.
 // PV (O = P' * V):
 //   A = P' = p * value_scale(token, group), fp16, row = query head; the lane
@@ -34,6 +36,7 @@ namespace {
 using namespace kvq;
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
@@ -43,6 +46,17 @@ constexpr uint32_t kZeroSel = 0x0c0c0c0cu;
 __device__ __forceinline__ h8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   u4v v = {a, b, c, d};
   return __builtin_bit_cast(h8, v);
+}
+
+// (hi, lo) fp16 parts of x: hi = fp16(x), lo = fp16(x - hi).
+__device__ __forceinline__ void split_h(float x, _Float16& hi, _Float16& lo) {
+  hi = static_cast<_Float16>(x);
+  lo = static_cast<_Float16>(x - static_cast<float>(hi));
+}
+
+__device__ __forceinline__ uint32_t h2_bits(_Float16 a, _Float16 b) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
 }
 
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
@@ -62,6 +76,12 @@ __device__ __forceinline__ uint32_t code_pair(uint32_t lo, uint32_t hi, uint32_t
   uint32_t x = __builtin_amdgcn_perm(hi, lo, pair_sel(j >> 1));
   x >>= (j & 1u) * 4u;
   return (x & 0x000f000fu) | kMagic;
+}
+
+// fp16 pair (nibble j of lo, nibble j of hi): the exact codes (1024 + c - 1024).
+__device__ __forceinline__ uint32_t code_pair_exact(uint32_t lo, uint32_t hi, uint32_t j) {
+  const h2 v = __builtin_bit_cast(h2, code_pair(lo, hi, j)) - h2{1024.0f16, 1024.0f16};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 __device__ __forceinline__ float sum_kg(float v) {  // over the 4 lane groups of 16
@@ -208,38 +228,42 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
     const int sub = n / CPG;
     float kb = 0.0f;
     f4 sacc[NJ];
-    f4 cacc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NJ; ++j) sacc[j] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
-      uint32_t qh[4];
+      uint32_t qh[4], ql[4];
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
         const int d0 = 32 * s4 + 8 * p + kg;  // element 2p
         const int d1 = d0 + 4;                // element 2p + 1
         const float q0 = to_f32(qv[8 * s4 + 2 * p]) * qscale;
         const float q1 = to_f32(qv[8 * s4 + 2 * p + 1]) * qscale;
-        qh[p] = pack_h2(q0 * sks[d0], q1 * sks[d1]);
+        _Float16 h0, l0, h1, l1;
+        split_h(q0 * sks[d0], h0, l0);
+        split_h(q1 * sks[d1], h1, l1);
+        qh[p] = h2_bits(h0, h1);
+        ql[p] = h2_bits(l0, l1);
         kb += q0 * skm[d0] + q1 * skm[d1];
       }
       uint32_t w[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) w[i] = skw[(32 * s4 + 4 * i + kg) * CPG + chunk];
       const h8 bq = as_h8(qh[0], qh[1], qh[2], qh[3]);
-      cacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones_a, bq, cacc, 0, 0, 0);
+      const h8 bl = as_h8(ql[0], ql[1], ql[2], ql[3]);
 #pragma unroll
       for (int jm = 0; jm < NJ; ++jm) {
         const uint32_t j = static_cast<uint32_t>(jm * SUB + sub);
-        const h8 a = as_h8(code_pair(w[0], w[1], j), code_pair(w[2], w[3], j),
-                           code_pair(w[4], w[5], j), code_pair(w[6], w[7], j));
+        const h8 a = as_h8(code_pair_exact(w[0], w[1], j), code_pair_exact(w[2], w[3], j),
+                           code_pair_exact(w[4], w[5], j), code_pair_exact(w[6], w[7], j));
         sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, sacc[jm], 0, 0, 0);
+        sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, sacc[jm], 0, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     kb = sum_kg(kb);
     // lane holds head n, rows m' = 4*kg + r: token 8*(m' % CPG) + jm*SUB + m'/CPG
-    const float kcorr = kb - cacc[0];
+    const float kcorr = kb;
     float tmax = -INFINITY;
 #pragma unroll
     for (int jm = 0; jm < NJ; ++jm) {
