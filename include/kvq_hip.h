@@ -212,6 +212,13 @@ int kvq_int8_decode_attn(const void* query, int dtype, int64_t batch, int num_he
  * the gfx950 matrix-core lane layout directly. */
 int kvq_selftest_mfma_f16(const void* a, const void* b, float* d, void* stream);
 
+/* One wave copies src[0..320) uint32 through LDS with the LDS-DMA loads the
+ * decode kernel stages its tiles with (global_load_lds, 16-byte lanes for
+ * words 0..255, 4-byte lanes for words 256..319) and writes the LDS image to
+ * dst[0..320); dst == src pins the lane -> LDS address mapping.  No
+ * counterpart in the reference. */
+int kvq_selftest_lds_dma(const void* src, void* dst, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

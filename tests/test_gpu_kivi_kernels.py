@@ -216,3 +216,17 @@ def test_mfma_lane_layout(gpu_device):
     )
     _native.check(rc, "kvq_selftest_mfma_f16")
     assert torch.equal(d.cpu(), a.float() @ b.float())
+
+
+def test_lds_dma_lane_layout(gpu_device):
+    """global_load_lds writes lane i's bytes at LDS base + size * i (16 B and 4 B lanes)."""
+    from vllm_ascend_quantized_kv_cache.ops import _native
+
+    src = torch.randint(0, 2**31 - 1, (320,), dtype=torch.int32,
+                        generator=torch.Generator().manual_seed(4))
+    dsrc = src.to(gpu_device)
+    dst = torch.zeros(320, dtype=torch.int32, device=gpu_device)
+    rc = _native.lib().kvq_selftest_lds_dma(dsrc.data_ptr(), dst.data_ptr(),
+                                            _native.stream_of(dst))
+    _native.check(rc, "kvq_selftest_lds_dma")
+    assert torch.equal(dst.cpu(), src)

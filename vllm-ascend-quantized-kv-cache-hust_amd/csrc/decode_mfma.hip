@@ -1,14 +1,20 @@
 // SPDX-License-Identifier: Apache-2.0
 // MFMA decode attention over KIVI int4 pages (kind-0 work items) for gfx950.
 //
-// One workgroup per work item, one wave per kv head.  A work item is a range
-// of positions whose keys and values are both in int4 pages; the range is cut
-// into "group tiles" of GT = 8*CPG tokens (CPG = min(16, G/8) 8-token chunks),
-// each inside one page and one key-scale group.
+// One wave per (work item, kv head).  A work item is a 128-aligned range of
+// positions whose keys and values are both in int4 pages; the wave walks it in
+// "group tiles" of GT = 8*CPG tokens (CPG = 8 for G >= 64, 4 for G = 32), each
+// inside one page and one key-scale group.
+//
+// Tiles are double-buffered in the wave's LDS: while tile i is computed, the
+// DMA loads of tile i+1 (global_load_lds, 16-byte and 4-byte lanes, written
+// straight into LDS without passing through registers) are in flight.  Each
+// wave owns its two buffers, so there is no workgroup barrier; a wave waits
+// only on its own vector-memory counter.
 //
 // QK^T (v_mfma_f32_16x16x32_f16, S^T = K * Q'^T):
 //   A = key codes, row m = token, 8 head dims per lane.  A key word packs 8
-//       tokens of one dim, so a lane loads 8 words (8 dims x 8 tokens of its
+//       tokens of one dim, so a lane reads 8 words (8 dims x 8 tokens of its
 //       chunk) and builds each register from one nibble of two words with
 //       v_perm_b32 + v_and_or_b32 as the fp16 value 1024 + code, then one
 //       packed fp16 subtract leaves the exact code (0..15).
@@ -95,41 +101,118 @@ __device__ __forceinline__ float max_kg(float v) {
   return v;
 }
 
-constexpr int kHeadsPerWg = 4;  // waves (kv heads) per workgroup
+// ---- LDS DMA -------------------------------------------------------------
+// global_load_lds: every lane reads `size` bytes at its own global address and
+// the wave writes them to LDS at base + size * lane (base must be uniform).
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)(lds), 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)(lds), 4, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) with lgkmcnt/expcnt left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+
+// Tile buffer layout (bytes) for one wave.
+template <int CPG>
+struct TileLayout {
+  static constexpr int D = 128;
+  static constexpr int GT = 8 * CPG;
+  static constexpr int NVG = 16 / CPG;
+  static constexpr int KW = 0;                      // key words  [d][CPG] u32
+  static constexpr int VW = KW + D * CPG * 4;       // value words [t][16] u32
+  static constexpr int KS = VW + GT * 64;           // key scale   [d] f32
+  static constexpr int KM = KS + D * 4;             // key min     [d] f32
+  static constexpr int VS = KM + D * 4;             // value scale [t][NVG] f32
+  static constexpr int VM = VS + GT * NVG * 4;      // value min   [t][NVG] f32
+  static constexpr int BYTES = VM + GT * NVG * 4;
+  // DMA instructions per tile: the wait counts below rely on this number
+  static constexpr int KW_INST = D * CPG * 4 / 1024;
+  static constexpr int VW_INST = GT * 64 / 1024;
+  static constexpr int NINST = KW_INST + VW_INST + 2 * (D / 64) + 2 * (GT * NVG / 64);
+};
+
+// Issue the DMA loads of one tile (page blk, offsets [off0, off0 + GT), key
+// group grp) of kv head h into `buf`.  Every load is in bounds: the tile lies
+// inside page blk, which the caller has checked is a live block id.
+template <int CPG>
+__device__ __forceinline__ void issue_tile(char* buf, int lane, int64_t blk, int off0, int grp,
+                                           int h, int kvh, int bs, int gpb, int ng,
+                                           const uint32_t* __restrict__ kq,
+                                           const float* __restrict__ ks,
+                                           const float* __restrict__ km,
+                                           const uint32_t* __restrict__ vq,
+                                           const float* __restrict__ vs,
+                                           const float* __restrict__ vm) {
+  using L = TileLayout<CPG>;
+  constexpr int D = L::D;
+  constexpr int LPR = CPG / 4;   // 16-byte lanes per key dim row (CPG words)
+  constexpr int DPI = 64 / LPR;  // key dim rows per instruction
+  const int wpd = bs / 8;
+  const int64_t krow0 = (blk * kvh + h) * D;
+#pragma unroll
+  for (int i = 0; i < L::KW_INST; ++i) {
+    const int d = i * DPI + lane / LPR;
+    const int part = lane % LPR;
+    dma16(kq + (krow0 + d) * wpd + off0 / 8 + 4 * part, buf + L::KW + i * 1024);
+  }
+#pragma unroll
+  for (int i = 0; i < L::VW_INST; ++i) {
+    const int t = 16 * i + lane / 4;
+    const int part = lane % 4;
+    dma16(vq + ((blk * bs + off0 + t) * kvh + h) * 16 + 4 * part, buf + L::VW + i * 1024);
+  }
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) {
+    const int d = 64 * i + lane;
+    dma4(ks + (krow0 + d) * gpb + grp, buf + L::KS + i * 256);
+    dma4(km + (krow0 + d) * gpb + grp, buf + L::KM + i * 256);
+  }
+#pragma unroll
+  for (int i = 0; i < L::GT * L::NVG / 64; ++i) {
+    const int e = 64 * i + lane;
+    const int t = e / L::NVG;
+    int vg = e % L::NVG;
+    vg = vg < ng ? vg : 0;  // slots past the tile's groups load a duplicate (never read)
+    const int64_t idx = ((blk * bs + off0 + t) * kvh + h) * ng + vg;
+    dma4(vs + idx, buf + L::VS + i * 256);
+    dma4(vm + idx, buf + L::VM + i * 256);
+  }
+}
 
 template <typename TQ, int CPG>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(64, 2)
 kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qscale,
                         const uint32_t* __restrict__ kq, const float* __restrict__ ks,
                         const float* __restrict__ km, const uint32_t* __restrict__ vq,
                         const float* __restrict__ vs, const float* __restrict__ vm, int bs,
-                        int g, const int32_t* __restrict__ block_table, int64_t maxb,
-                        const int32_t* __restrict__ work, float* __restrict__ ws_o,
-                        float* __restrict__ ws_ml) {
-  constexpr int D = 128;
-  constexpr int GT = 8 * CPG;    // tokens per group tile
+                        int g, int64_t nb, const int32_t* __restrict__ block_table,
+                        int64_t maxb, const int32_t* __restrict__ work,
+                        float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+  using L = TileLayout<CPG>;
+  constexpr int D = L::D;
+  constexpr int GT = L::GT;      // tokens per tile
   constexpr int NJ = CPG / 2;    // score MFMAs per k-step (16 tokens each)
   constexpr int SUB = 16 / CPG;  // tokens of one chunk inside one score MFMA
-  constexpr int NVG = 16 / CPG;  // PV column groups (one value group each)
+  constexpr int NVG = L::NVG;    // PV column groups (one value group each)
   constexpr int NJJ = CPG / 2;   // PV MFMAs per column group (NVG * NJJ == 8)
-  constexpr int PVS = CPG / 4;   // PV k-steps (32 tokens) per group tile
-  constexpr int HW = kHeadsPerWg;
+  constexpr int PVS = CPG / 4;   // PV k-steps (32 tokens) per tile
 
-  __shared__ uint32_t s_kw[HW * D * CPG];       // key words   [hl][d][chunk]
-  __shared__ uint32_t s_vw[HW * GT * 16];       // value words [hl][t][word]
-  __shared__ float s_ks[HW * D], s_km[HW * D];  // key scale/min of the tile's group
-  __shared__ float s_vs[GT * HW * NVG], s_vm[GT * HW * NVG];  // value scale/min [t][hl][vg]
-
+  extern __shared__ __align__(16) char lds_raw[];
   const int wi = blockIdx.x;
-  const int h0 = blockIdx.y * HW;
-  const int tid = threadIdx.x;
-  const int hl = tid >> 6;
-  const int h = h0 + hl;
-  const int lane = tid & 63;
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x;
   const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
   if (wk[3] != 0) return;  // kind-1 items belong to the generic kernel (uniform)
-  const int heads = (kvh - h0) < HW ? (kvh - h0) : HW;
-  const bool wave_live = hl < heads;
   const int b = wk[0];
   const int pb = wk[1];
   const int pe = wk[2];
@@ -137,21 +220,24 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   const int n = lane & 15;
   const int kg = lane >> 4;
   const int gpb = bs / g;
-  const int wpd = bs / 8;
-  const int ng = D / g;  // == NVG: the kernel runs only for 8*CPG == G <= 128
+  const int ng = D / g;
   const int32_t* bt = block_table + static_cast<int64_t>(b) * maxb;
 
-  // q of head n for the lane's dims d = 32*s + 4*i + kg, kept in the input
-  // dtype (two 16-bit values per VGPR); softmax scale * log2(e) applies on use
+  // q of head n for the lane's dims d = 32*s + 4*i + kg, in the input dtype.
+  // Lanes past the GQA group read head 0's row (always valid) and zero it, so
+  // the 32 loads issue back to back instead of behind per-lane branches.
   TQ qv[32];
   {
-    const bool live = wave_live && n < rep;
-    const TQ* qrow = query + (static_cast<int64_t>(b) * hq + (live ? h * rep + n : 0)) * D;
+    const bool live = n < rep;
+    const TQ* qrow = query + (static_cast<int64_t>(b) * hq + h * rep + (live ? n : 0)) * D;
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        qv[8 * s4 + i] = live ? qrow[32 * s4 + 4 * i + kg] : from_f32<TQ>(0.0f);
+      for (int i = 0; i < 8; ++i) qv[8 * s4 + i] = qrow[32 * s4 + 4 * i + kg];
+    if (!live) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) qv[i] = from_f32<TQ>(0.0f);
+    }
   }
   const h8 ones_a = as_h8(kMagic, kMagic, kMagic, kMagic);
 
@@ -168,62 +254,39 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
     bias_v[v] = 0.0f;
   }
 
+  // page ids are clamped into [0, nb): the host validates live ids, the clamp
+  // only guarantees that no DMA can leave the cache whatever the table holds
+  auto page = [&](int p) -> int64_t {
+    const int64_t blk = bt[p / bs];
+    return blk < 0 ? 0 : (blk >= nb ? nb - 1 : blk);
+  };
+  // prologue: tile 0 into buffer 0
+  {
+    const int64_t blk = page(pb);
+    issue_tile<CPG>(lds_raw, lane, blk, pb % bs, (pb % bs) / g, h, kvh, bs, gpb, ng, kq, ks, km,
+                    vq, vs, vm);
+  }
+  int cur = 0;
   for (int p0 = pb; p0 < pe; p0 += GT) {
-    const int64_t blk = bt[p0 / bs];
-    const int off0 = p0 % bs;
-    const int grp = off0 / g;
-    __syncthreads();  // the previous tile's LDS reads are done
-    // ---- stage the tile: every load 16 B and coalesced -------------------
-    {
-      // key words: row (hl, d) holds CPG words at kq[((blk*kvh + h)*D + d)*wpd + off0/8]
-      constexpr int QPR = CPG / 4;  // 16-byte pieces per row
-      for (int e = tid; e < heads * D * QPR; e += 64 * HW) {
-        const int row = e / QPR;
-        const int q4 = e - row * QPR;
-        const int rh = row / D;
-        const int d = row - rh * D;
-        const uint4 w = *reinterpret_cast<const uint4*>(
-            kq + ((blk * kvh + h0 + rh) * D + d) * wpd + off0 / 8 + 4 * q4);
-        *reinterpret_cast<uint4*>(s_kw + row * CPG + 4 * q4) = w;
-      }
-      // value words: token t, head hl -> 16 words (64 B)
-      for (int e = tid; e < GT * heads * 4; e += 64 * HW) {
-        const int q4 = e & 3;
-        const int th = e >> 2;
-        const int t = th / heads;
-        const int rh = th - t * heads;
-        const uint4 w = *reinterpret_cast<const uint4*>(
-            vq + ((blk * bs + off0 + t) * kvh + h0 + rh) * 16 + 4 * q4);
-        *reinterpret_cast<uint4*>(s_vw + (rh * GT + t) * 16 + 4 * q4) = w;
-      }
-      for (int e = tid; e < heads * D; e += 64 * HW) {
-        const int rh = e / D;
-        const int d = e - rh * D;
-        const int64_t idx = ((blk * kvh + h0 + rh) * D + d) * gpb + grp;
-        s_ks[e] = ks[idx];
-        s_km[e] = km[idx];
-      }
-      for (int e = tid; e < GT * heads * ng; e += 64 * HW) {
-        const int vg = e % ng;
-        const int th = e / ng;
-        const int t = th / heads;
-        const int rh = th - t * heads;
-        // positions past the range keep p = 0; zeroing their scale/min keeps
-        // p*scale and p*min exact zeros without a branch (the bytes past the
-        // sequence end are not written history and may hold anything)
-        const bool live_t = p0 + t < pe;
-        const int64_t idx = ((blk * bs + off0 + t) * kvh + h0 + rh) * ng + vg;
-        s_vs[(t * HW + rh) * NVG + vg] = live_t ? vs[idx] : 0.0f;
-        s_vm[(t * HW + rh) * NVG + vg] = live_t ? vm[idx] : 0.0f;
-      }
+    // prefetch tile p0 + GT into the other buffer, then wait for this tile only
+    const int p1 = p0 + GT;
+    if (p1 < pe) {
+      const int64_t blk1 = page(p1);
+      issue_tile<CPG>(lds_raw + (cur ^ 1) * L::BYTES, lane, blk1, p1 % bs, (p1 % bs) / g, h,
+                      kvh, bs, gpb, ng, kq, ks, km, vq, vs, vm);
+      wait_vmcnt<L::NINST>();
+    } else {
+      wait_vmcnt<0>();
     }
-    __syncthreads();
-    if (!wave_live) continue;
+    const char* buf = lds_raw + cur * L::BYTES;
+    const float* sks = reinterpret_cast<const float*>(buf + L::KS);
+    const float* skm = reinterpret_cast<const float*>(buf + L::KM);
+    const uint32_t* skw = reinterpret_cast<const uint32_t*>(buf + L::KW);
+    const uint32_t* svw = reinterpret_cast<const uint32_t*>(buf + L::VW);
+    const float* svs = reinterpret_cast<const float*>(buf + L::VS);
+    const float* svm = reinterpret_cast<const float*>(buf + L::VM);
 
-    // ---- scores: per k-step, Q' for this key group then the MFMAs -------
-    const float* sks = s_ks + hl * D;
-    const float* skm = s_km + hl * D;
-    const uint32_t* skw = s_kw + hl * D * CPG;
+    // ---- scores ------------------------------------------------------------
     const int chunk = n % CPG;
     const int sub = n / CPG;
     float kb = 0.0f;
@@ -259,11 +322,9 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
         sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, sacc[jm], 0, 0, 0);
         sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, sacc[jm], 0, 0, 0);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
     kb = sum_kg(kb);
     // lane holds head n, rows m' = 4*kg + r: token 8*(m' % CPG) + jm*SUB + m'/CPG
-    const float kcorr = kb;
     float tmax = -INFINITY;
 #pragma unroll
     for (int jm = 0; jm < NJ; ++jm) {
@@ -271,7 +332,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
       for (int r = 0; r < 4; ++r) {
         const int mr = 4 * kg + r;
         const int pos = p0 + 8 * (mr % CPG) + jm * SUB + mr / CPG;
-        const float sv = pos < pe ? sacc[jm][r] + kcorr : -INFINITY;
+        const float sv = pos < pe ? sacc[jm][r] + kb : -INFINITY;
         sacc[jm][r] = sv;
         tmax = fmaxf(tmax, sv);
       }
@@ -302,18 +363,19 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
 #pragma unroll
     for (int v = 0; v < NVG; ++v) bias_v[v] *= alpha;
 
-    // ---- PV ----------------------------------------------------------------
-    const uint32_t* svw = s_vw + hl * GT * 16;
+    // ---- PV ------------------------------------------------------------------
 #pragma unroll
     for (int st = 0; st < PVS; ++st) {
       int tk[8];
       float pv[8];
+      bool live[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int jm = 2 * st + i / 4;
         const int mr = 4 * kg + (i % 4);
         tk[i] = 8 * (mr % CPG) + jm * SUB + mr / CPG;
         pv[i] = sacc[jm][i % 4];
+        live[i] = p0 + tk[i] < pe;
       }
 #pragma unroll
       for (int v = 0; v < NVG; ++v) {
@@ -321,8 +383,13 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
         float pp[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float sc = s_vs[(tk[i] * HW + hl) * NVG + vgrp];
-          const float mn = s_vm[(tk[i] * HW + hl) * NVG + vgrp];
+          // tokens past the range have p = 0 but unwritten scale/min bytes:
+          // select zeros so a stale NaN cannot leak into the sums (the reads
+          // stay inside the tile buffer, so they are unconditional)
+          const float sc_raw = svs[tk[i] * NVG + vgrp];
+          const float mn_raw = svm[tk[i] * NVG + vgrp];
+          const float sc = live[i] ? sc_raw : 0.0f;
+          const float mn = live[i] ? mn_raw : 0.0f;
           pp[i] = pv[i] * sc;
           bias_v[v] += pv[i] * mn;
         }
@@ -342,10 +409,12 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
               __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv, o_acc[v * NJJ + jj], 0, 0, 0);
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
+    // every LDS read of this buffer has been consumed before the next
+    // iteration's DMA may overwrite it
+    asm volatile("" ::: "memory");
+    cur ^= 1;
   }
-  if (!wave_live) return;
 
   // ---- epilogue: remove the PV offset, add the value-minimum term --------
 #pragma unroll
@@ -368,6 +437,20 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
     ws_ml[2 * (head0 + n)] = m_run;
     ws_ml[2 * (head0 + n) + 1] = l_run;
   }
+}
+
+// Copies 1 KiB with 16-byte DMA lanes and 256 B with 4-byte DMA lanes through
+// LDS and writes the LDS image back, so a test can pin the lane -> LDS address
+// mapping the decode kernel's tile layout relies on.
+__global__ void lds_dma_probe_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst) {
+  extern __shared__ __align__(16) char lds_raw[];
+  const int lane = threadIdx.x;
+  dma16(src + 4 * lane, lds_raw);
+  dma4(src + 256 + lane, lds_raw + 1024);
+  wait_vmcnt<0>();
+  const uint32_t* l = reinterpret_cast<const uint32_t*>(lds_raw);
+#pragma unroll
+  for (int i = 0; i < 5; ++i) dst[64 * i + lane] = l[64 * i + lane];
 }
 
 // 16x32 (A) times 32x16 (B) through the same intrinsic and operand mapping the
@@ -395,27 +478,27 @@ namespace kvq {
 int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int d, float qscale,
                             const int32_t* kq, const float* ks, const float* km,
                             const int32_t* vq, const float* vs, const float* vm, int bs, int g,
-                            const int32_t* block_table, int64_t maxb, const int32_t* seq_meta,
+                            int64_t nb, const int32_t* block_table, int64_t maxb,
+                            const int32_t* seq_meta,
                             const int32_t* work, int64_t num_work, float* ws_o, float* ws_ml,
                             hipStream_t s, bool* launched) {
   (void)seq_meta;
   *launched = false;
-  if (d != 128 || hq / kvh > 16 || g < 32 || g % 8 || d % g) return KVQ_OK;
-  const int cpg = g / 8 >= 16 ? 16 : g / 8;
-  if (cpg != 16 && cpg != 8 && cpg != 4) return KVQ_OK;
-  if (g > 128) return KVQ_OK;  // one value group per 16 MFMA columns needs G <= 128
-  const dim3 grid(static_cast<unsigned>(num_work), (kvh + kHeadsPerWg - 1) / kHeadsPerWg);
-  const dim3 block(64 * kHeadsPerWg);
+  if (d != 128 || hq / kvh > 16 || g % 8 || d % g || g < 32 || g > 128) return KVQ_OK;
+  // tiles of 64 tokens (32 for G = 32): inside one key group and one page
+  const int cpg = g >= 64 ? 8 : 4;
+  if (bs % (8 * cpg)) return KVQ_OK;
+  const dim3 grid(static_cast<unsigned>(num_work), kvh);
+  const dim3 block(64);
   const uint32_t* kqu = reinterpret_cast<const uint32_t*>(kq);
   const uint32_t* vqu = reinterpret_cast<const uint32_t*>(vq);
 #define KVQ_LAUNCH_MFMA(C)                                                                   \
   KVQ_DISPATCH_FLOAT(q_dtype, TQ,                                                           \
-    hipLaunchKernelGGL((kivi_decode_mfma_kernel<TQ, C>), grid, block, 0, s,                 \
-                       static_cast<const TQ*>(query), hq, kvh, qscale, kqu, ks, km, vqu, vs, \
-                       vm, bs, g, block_table, maxb, work, ws_o, ws_ml))
-  if (cpg == 16) {
-    KVQ_LAUNCH_MFMA(16);
-  } else if (cpg == 8) {
+    hipLaunchKernelGGL((kivi_decode_mfma_kernel<TQ, C>), grid, block,                       \
+                       2 * TileLayout<C>::BYTES, s, static_cast<const TQ*>(query), hq, kvh, \
+                       qscale, kqu, ks, km, vqu, vs, vm, bs, g, nb, block_table, maxb, work,\
+                       ws_o, ws_ml))
+  if (cpg == 8) {
     KVQ_LAUNCH_MFMA(8);
   } else {
     KVQ_LAUNCH_MFMA(4);
@@ -441,6 +524,15 @@ extern "C" int kvq_selftest_mfma_f16(const void* a, const void* b, float* d, voi
   hipLaunchKernelGGL(mfma_layout_probe_kernel, dim3(1), dim3(64), 0,
                      static_cast<hipStream_t>(stream), static_cast<const _Float16*>(a),
                      static_cast<const _Float16*>(b), d);
+  KVQ_LAUNCH_CHECK();
+  return KVQ_OK;
+}
+
+extern "C" int kvq_selftest_lds_dma(const void* src, void* dst, void* stream) {
+  if (!src || !dst) return KVQ_ERR_INVALID;
+  hipLaunchKernelGGL(lds_dma_probe_kernel, dim3(1), dim3(64), 1280,
+                     static_cast<hipStream_t>(stream), static_cast<const uint32_t*>(src),
+                     static_cast<uint32_t*>(dst));
   KVQ_LAUNCH_CHECK();
   return KVQ_OK;
 }

@@ -38,55 +38,129 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Stage the K (is_key) or V rows of positions [p0, p0 + n) of one kv head into
-// LDS as fp32 [64][d + 1]: int4 history dequantized exactly, ring rows copied.
+// Staging of the K or V rows of positions [p0, p0 + n) (n <= 64) of one kv
+// head into LDS as fp32 [64][d + 1].  Positions below `hist` come from the
+// int4 pages (dequantized exactly: q*scale then +mn), the rest from the
+// residual ring.  Every path issues its loads in independent batches before
+// using them, so a wave waits for a few memory round trips, not one per load.
+
+constexpr int kBatch = 8;
+
+__device__ __forceinline__ int64_t clamp_page(const int32_t* __restrict__ bt, int p, int bs,
+                                              int64_t nb) {
+  const int64_t blk = bt[p / bs];
+  return blk < 0 ? 0 : (blk >= nb ? nb - 1 : blk);  // never leave the cache
+}
+
+// Ring rows of positions [p0 + i0, p0 + n): task = (position, 8-dim chunk).
 template <typename TR>
-__device__ __forceinline__ void stage_rows(float* __restrict__ dst, bool is_key, int p0, int n,
-                                           int hist, const int32_t* __restrict__ bt, int bs,
-                                           int kvh, int h, int d, int g,
-                                           const uint32_t* __restrict__ q4,
-                                           const float* __restrict__ sc,
-                                           const float* __restrict__ mn,
+__device__ __forceinline__ void stage_ring(float* __restrict__ dst, int p0, int i0, int n,
+                                           int hist, int kvh, int h, int d,
                                            const TR* __restrict__ ring, int64_t ring_row0,
                                            int ring_first, int ring_len, int lane) {
   const int ndv = d / 8;
   const int pitch = d + 1;
-  const int gpb = bs / g;
-  const int wpd = bs / 8;
-  // one task = 8 consecutive dims of one position
-  for (int t = lane; t < 64 * ndv; t += 64) {
-    const int pi = t / ndv;
-    const int dv = t - pi * ndv;
-    if (pi >= n) continue;
-    const int p = p0 + pi;
-    float x[8];
-    if (p < hist) {
-      int64_t blk = bt[p / bs];
-      if (blk < 0) blk = 0;
-      const int off = p % bs;
-      if (is_key) {
-        const int64_t base = (blk * kvh + h) * static_cast<int64_t>(d) + dv * 8;
+  const int tasks = (n - i0) * ndv;
+  for (int t0 = 0; t0 < tasks; t0 += 64 * kBatch) {
+    float x[kBatch][8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t w = q4[(base + i) * wpd + off / 8];
-          x[i] = kivi_dequant((w >> (4 * (off % 8))) & 0xfu, sc[(base + i) * gpb + off / g],
-                              mn[(base + i) * gpb + off / g]);
-        }
-      } else {
-        const int64_t vrow = (blk * bs + off) * kvh + h;
-        const uint32_t w = q4[vrow * ndv + dv];
-        const int gi = (dv * 8) / g;
-        const float s_ = sc[vrow * (d / g) + gi];
-        const float m_ = mn[vrow * (d / g) + gi];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = kivi_dequant((w >> (4 * i)) & 0xfu, s_, m_);
-      }
-    } else {
-      const int rl = (ring_first + (p - hist)) % ring_len;
-      load8(ring + ((ring_row0 + rl) * kvh + h) * d + dv * 8, x);
+    for (int k = 0; k < kBatch; ++k) {
+      const int tk = t0 + 64 * k + lane;
+      const int t = tk < tasks ? tk : tasks - 1;  // clamped: unconditional load
+      const int pi = i0 + t / ndv;
+      const int dv = t % ndv;
+      const int rl = (ring_first + (p0 + pi - hist)) % ring_len;
+      load8(ring + ((ring_row0 + rl) * kvh + h) * d + dv * 8, x[k]);
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dst[pi * pitch + dv * 8 + i] = x[i];
+    for (int k = 0; k < kBatch; ++k) {
+      const int t = t0 + 64 * k + lane;
+      if (t < tasks) {
+        const int pi = i0 + t / ndv;
+        const int dv = t % ndv;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dst[pi * pitch + dv * 8 + i] = x[k][i];
+      }
+    }
+  }
+}
+
+// Int4 keys of positions [p0, p0 + m): lane = dim; the <= 9 words holding the
+// m tokens of that dim (and their group scale/min) load in one batch.
+__device__ __forceinline__ void stage_int4_keys(float* __restrict__ dst, int p0, int m,
+                                                const int32_t* __restrict__ bt, int64_t nb,
+                                                int bs, int kvh, int h, int d, int g,
+                                                const uint32_t* __restrict__ kq,
+                                                const float* __restrict__ ks,
+                                                const float* __restrict__ km, int lane) {
+  constexpr int kMaxWords = 9;  // 64 tokens starting anywhere inside a word
+  const int pitch = d + 1;
+  const int gpb = bs / g;
+  const int wpd = bs / 8;
+  const int first = p0 & ~7;
+  for (int c = lane; c < d; c += 64) {
+    uint32_t w[kMaxWords];
+    float sc[kMaxWords], mn[kMaxWords];
+#pragma unroll
+    for (int k = 0; k < kMaxWords; ++k) {
+      // clamped into [p0, p0 + m): every load is valid and unconditional
+      const int p = first + 8 * k;
+      const int pp = p < p0 ? p0 : (p < p0 + m ? p : p0 + m - 1);
+      const int64_t blk = clamp_page(bt, pp, bs, nb);
+      const int off = pp % bs;
+      const int64_t row = (blk * kvh + h) * static_cast<int64_t>(d) + c;
+      w[k] = kq[row * wpd + off / 8];
+      sc[k] = ks[row * gpb + off / g];
+      mn[k] = km[row * gpb + off / g];
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxWords; ++k) {
+      const int p = first + 8 * k;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int pi = p + j - p0;
+        if (pi >= 0 && pi < m) dst[pi * pitch + c] = kivi_dequant((w[k] >> (4 * j)) & 0xfu, sc[k], mn[k]);
+      }
+    }
+  }
+}
+
+// Int4 values of positions [p0, p0 + m): task = (position, word of 8 dims).
+__device__ __forceinline__ void stage_int4_values(float* __restrict__ dst, int p0, int m,
+                                                  const int32_t* __restrict__ bt, int64_t nb,
+                                                  int bs, int kvh, int h, int d, int g,
+                                                  const uint32_t* __restrict__ vq,
+                                                  const float* __restrict__ vs,
+                                                  const float* __restrict__ vm, int lane) {
+  const int ndv = d / 8;
+  const int pitch = d + 1;
+  const int tasks = m * ndv;
+  for (int t0 = 0; t0 < tasks; t0 += 64 * kBatch) {
+    uint32_t w[kBatch];
+    float sc[kBatch], mn[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int tk = t0 + 64 * k + lane;
+      const int t = tk < tasks ? tk : tasks - 1;  // clamped: unconditional load
+      const int pi = t / ndv;
+      const int dv = t % ndv;
+      const int p = p0 + pi;
+      const int64_t vrow = (clamp_page(bt, p, bs, nb) * bs + p % bs) * kvh + h;
+      w[k] = vq[vrow * ndv + dv];
+      sc[k] = vs[vrow * (d / g) + (dv * 8) / g];
+      mn[k] = vm[vrow * (d / g) + (dv * 8) / g];
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int t = t0 + 64 * k + lane;
+      if (t < tasks) {
+        const int pi = t / ndv;
+        const int dv = t % ndv;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          dst[pi * pitch + dv * 8 + i] = kivi_dequant((w[k] >> (4 * i)) & 0xfu, sc[k], mn[k]);
+      }
+    }
   }
 }
 
@@ -96,17 +170,17 @@ kivi_decode_generic_kernel(const TQ* __restrict__ query, int hq, int kvh, int d,
                            const int32_t* __restrict__ kq, const float* __restrict__ ks,
                            const float* __restrict__ km, const int32_t* __restrict__ vq,
                            const float* __restrict__ vs, const float* __restrict__ vm, int bs,
-                           int g, const int32_t* __restrict__ block_table, int64_t maxb,
-                           const int32_t* __restrict__ seq_meta,
+                           int g, int64_t nb, const int32_t* __restrict__ block_table,
+                           int64_t maxb, const int32_t* __restrict__ seq_meta,
                            const int32_t* __restrict__ work, const TR* __restrict__ ring_k,
                            const TR* __restrict__ ring_v, int ring_len,
                            float* __restrict__ ws_o, float* __restrict__ ws_ml,
-                           int skip_kind0) {
+                           int skip_kind0, int skip_kind1) {
   const int wi = blockIdx.x;
   const int h = blockIdx.y;
   const int lane = threadIdx.x;
   const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
-  if (skip_kind0 && wk[3] == 0) return;  // the MFMA kernel owns these items
+  if ((skip_kind0 && wk[3] == 0) || (skip_kind1 && wk[3] == 1)) return;  // MFMA kernels own these
   const int b = wk[0];
   const int pb = wk[1];
   const int pe = wk[2];
@@ -140,8 +214,13 @@ kivi_decode_generic_kernel(const TQ* __restrict__ query, int hq, int kvh, int d,
 
   for (int p0 = pb; p0 < pe; p0 += 64) {
     const int n = (pe - p0) < 64 ? (pe - p0) : 64;
-    stage_rows(s_rows, true, p0, n, khist, bt, bs, kvh, h, d, g, kqu, ks, km, ring_k,
-               static_cast<int64_t>(row) * ring_len, kfirst, ring_len, lane);
+    {
+      const int m = khist - p0 < 0 ? 0 : (khist - p0 < n ? khist - p0 : n);  // int4 keys
+      if (m > 0) stage_int4_keys(s_rows, p0, m, bt, nb, bs, kvh, h, d, g, kqu, ks, km, lane);
+      if (m < n)
+        stage_ring(s_rows, p0, m, n, khist, kvh, h, d, ring_k,
+                   static_cast<int64_t>(row) * ring_len, kfirst, ring_len, lane);
+    }
     __syncthreads();
     const bool live = lane < n;
     float s[kMaxRep];
@@ -170,8 +249,13 @@ kivi_decode_generic_kernel(const TQ* __restrict__ query, int hq, int kvh, int d,
       s_p[r * 64 + lane] = pr;
     }
     __syncthreads();
-    stage_rows(s_rows, false, p0, n, vhist, bt, bs, kvh, h, d, g, vqu, vs, vm, ring_v,
-               static_cast<int64_t>(row) * ring_len, vfirst, ring_len, lane);
+    {
+      const int m = vhist - p0 < 0 ? 0 : (vhist - p0 < n ? vhist - p0 : n);  // int4 values
+      if (m > 0) stage_int4_values(s_rows, p0, m, bt, nb, bs, kvh, h, d, g, vqu, vs, vm, lane);
+      if (m < n)
+        stage_ring(s_rows, p0, m, n, vhist, kvh, h, d, ring_v,
+                   static_cast<int64_t>(row) * ring_len, vfirst, ring_len, lane);
+    }
     __syncthreads();
     for (int i = 0; i < n; ++i) {
       const float* vrow = s_rows + i * pitch;
@@ -284,21 +368,31 @@ extern "C" int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batc
   bool mfma = false;
   int rc = kvq::launch_kivi_decode_mfma(query, q_dtype, num_heads, num_kv_heads, head_size,
                                        qscale, k_quant, k_scale, k_mn, v_quant, v_scale, v_mn,
-                                       block_size, group_size, block_table, max_blocks, seq_meta,
+                                       block_size, group_size, num_blocks, block_table,
+                                       max_blocks, seq_meta,
                                        work, num_work, ws_o, ws_ml, s, &mfma);
   if (rc != KVQ_OK) return rc;
-  const dim3 grid(static_cast<unsigned>(num_work), num_kv_heads);
-  const int rep = num_heads / num_kv_heads;
-  const size_t lds = sizeof(float) * (64 * (head_size + 1) + rep * head_size + rep * 64);
-  KVQ_DISPATCH_FLOAT(q_dtype, TQ,
-    KVQ_DISPATCH_FLOAT(ring_dtype, TR,
-      hipLaunchKernelGGL((kivi_decode_generic_kernel<TQ, TR>), grid, dim3(64), lds, s,
-                         static_cast<const TQ*>(query), num_heads, num_kv_heads, head_size,
-                         qscale, k_quant, k_scale, k_mn, v_quant, v_scale, v_mn, block_size,
-                         group_size, block_table, max_blocks, seq_meta, work,
-                         static_cast<const TR*>(ring_k), static_cast<const TR*>(ring_v),
-                         ring_len, ws_o, ws_ml, mfma ? 1 : 0)));
-  KVQ_LAUNCH_CHECK();
+  bool tail = false;
+  rc = kvq::launch_kivi_decode_tail_mfma(query, q_dtype, num_heads, num_kv_heads, head_size,
+                                         qscale, k_quant, k_scale, k_mn, v_quant, v_scale,
+                                         v_mn, block_size, group_size, num_blocks, block_table,
+                                         max_blocks, seq_meta, work, num_work, ring_k, ring_v,
+                                         ring_dtype, ring_len, ws_o, ws_ml, s, &tail);
+  if (rc != KVQ_OK) return rc;
+  if (!mfma || !tail) {
+    const dim3 grid(static_cast<unsigned>(num_work), num_kv_heads);
+    const int rep = num_heads / num_kv_heads;
+    const size_t lds = sizeof(float) * (64 * (head_size + 1) + rep * head_size + rep * 64);
+    KVQ_DISPATCH_FLOAT(q_dtype, TQ,
+      KVQ_DISPATCH_FLOAT(ring_dtype, TR,
+        hipLaunchKernelGGL((kivi_decode_generic_kernel<TQ, TR>), grid, dim3(64), lds, s,
+                           static_cast<const TQ*>(query), num_heads, num_kv_heads, head_size,
+                           qscale, k_quant, k_scale, k_mn, v_quant, v_scale, v_mn, block_size,
+                           group_size, num_blocks, block_table, max_blocks, seq_meta, work,
+                           static_cast<const TR*>(ring_k), static_cast<const TR*>(ring_v),
+                           ring_len, ws_o, ws_ml, mfma ? 1 : 0, tail ? 1 : 0)));
+    KVQ_LAUNCH_CHECK();
+  }
   return kvq::launch_decode_combine(q_dtype, batch, num_heads, head_size, seq_meta, 8, 6, ws_o,
                                     ws_ml, out, s);
 }

@@ -19,9 +19,22 @@ inline int64_t decode_workspace_bytes(int64_t num_work, int num_heads, int head_
 int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int d, float qscale,
                             const int32_t* kq, const float* ks, const float* km,
                             const int32_t* vq, const float* vs, const float* vm, int bs, int g,
-                            const int32_t* block_table, int64_t maxb, const int32_t* seq_meta,
-                            const int32_t* work, int64_t num_work, float* ws_o, float* ws_ml,
-                            hipStream_t s, bool* launched);
+                            int64_t nb, const int32_t* block_table, int64_t maxb,
+                            const int32_t* seq_meta, const int32_t* work, int64_t num_work,
+                            float* ws_o, float* ws_ml, hipStream_t s, bool* launched);
+
+// MFMA kernel for the kind-1 (mixed-source tail) items: D = 128, query and
+// ring in the same 16-bit dtype.  *launched tells the caller whether kind-1
+// items still need the generic kernel.
+int launch_kivi_decode_tail_mfma(const void* query, int q_dtype, int hq, int kvh, int d,
+                                 float qscale, const int32_t* kq, const float* ks,
+                                 const float* km, const int32_t* vq, const float* vs,
+                                 const float* vm, int bs, int g, int64_t nb,
+                                 const int32_t* block_table, int64_t maxb,
+                                 const int32_t* seq_meta, const int32_t* work, int64_t num_work,
+                                 const void* ring_k, const void* ring_v, int ring_dtype,
+                                 int ring_len, float* ws_o, float* ws_ml, hipStream_t s,
+                                 bool* launched);
 
 // INT8 counterpart: kind-0 items (all positions in int8 pages) on MFMA.
 int launch_int8_decode_mfma(const void* query, int dtype, int hq, int kvh, int d, float qscale,

@@ -838,12 +838,21 @@ class AscendKiviInt4AttentionBackendMixin:
         output: Any,
     ) -> Any:
         """One query token per request over int4 history + residual (``ab.py:1193-1230``)."""
+        from ...ops.kivi_layout import check_gather_metadata_host
+
         batch = len(seq_lens)
         keys = self._get_kivi_req_keys(req_ids, batch)
-        seqs = self._decode_seqs([int(n) for n in seq_lens], keys)
+        lens = [int(n) for n in seq_lens]
+        seqs = self._decode_seqs(lens, keys)
         q = query[:batch].reshape(batch, self.num_heads, self.head_size)
         out_view = output[:batch].view(batch, self.num_heads, self.head_size)
         bt = block_table[:batch].to(device=q.device, dtype=torch.int32).contiguous()
+        # the same live-block gate the reference's gather applies on this path
+        # (pkg/ops/kivi_layout.py:205-238); one host copy of the table
+        check_gather_metadata_host(
+            bt.to("cpu").tolist(), lens, max_blocks=bt.shape[1],
+            num_blocks=self.k_quant_cache.shape[0], block_size=self._get_kivi_block_size(),
+        )
         got = self._launch_kivi_decode(q.contiguous(), bt, seqs, out_view)
         if got is not None and got is not out_view:
             out_view.copy_(got)

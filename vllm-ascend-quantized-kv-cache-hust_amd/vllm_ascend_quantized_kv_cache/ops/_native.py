@@ -60,6 +60,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_P, _P, _I64, _I, _I, _I, _P, _P, _I, _P, _I64, _P, _I64, _P, _P, _P],
     ),
     "kvq_selftest_mfma_f16": (_I, [_P, _P, _P, _P]),
+    "kvq_selftest_lds_dma": (_I, [_P, _P, _P]),
     "kvq_int8_decode_workspace_bytes": (_I64, [_I64, _I, _I]),
     "kvq_int8_decode_attn": (
         _I,
