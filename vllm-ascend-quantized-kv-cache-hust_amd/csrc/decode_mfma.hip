@@ -122,70 +122,343 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("" ::: "memory");
 }
 
-// Tile buffer layout (bytes) for one wave.
+// ---- tile layout -------------------------------------------------------------
+// One wave's tile buffer.  Key and value words arrive with 16-byte DMA lanes in
+// their page order; the small scale/min regions are gathered with 4-byte lanes
+// so that what one lane needs for one MFMA step is 8 consecutive floats:
+//   KW [dim][chunk]          key word (dim, 8-token chunk), CPG words per dim
+//   VW [token][word]         value words, 16 per token
+//   KS, KM [s4][kg][ii]      key scale / min of dim 32*s4 + 4*ii + kg
+//   VS, VM [st][v][kg][i]    value scale / min of token tk(st, kg, i), group of v
+// A lane reads its 8 key words (dims 4 apart) and 8 value words (tokens 8
+// apart) as pairs with ds_read2_b32.  tk(st, kg, i) is the token of PV slot
+// 8*kg + i in k-step st: the token whose p the lane already holds from the
+// score layout.
 template <int CPG>
-struct TileLayout {
+struct Tile {
   static constexpr int D = 128;
-  static constexpr int GT = 8 * CPG;
-  static constexpr int NVG = 16 / CPG;
-  static constexpr int KW = 0;                      // key words  [d][CPG] u32
-  static constexpr int VW = KW + D * CPG * 4;       // value words [t][16] u32
-  static constexpr int KS = VW + GT * 64;           // key scale   [d] f32
-  static constexpr int KM = KS + D * 4;             // key min     [d] f32
-  static constexpr int VS = KM + D * 4;             // value scale [t][NVG] f32
-  static constexpr int VM = VS + GT * NVG * 4;      // value min   [t][NVG] f32
-  static constexpr int BYTES = VM + GT * NVG * 4;
-  // DMA instructions per tile: the wait counts below rely on this number
-  static constexpr int KW_INST = D * CPG * 4 / 1024;
-  static constexpr int VW_INST = GT * 64 / 1024;
-  static constexpr int NINST = KW_INST + VW_INST + 2 * (D / 64) + 2 * (GT * NVG / 64);
+  static constexpr int GT = 8 * CPG;    // tokens per tile
+  static constexpr int NJ = CPG / 2;    // score MFMAs per k-step (16 tokens each)
+  static constexpr int SUB = 16 / CPG;  // tokens of one chunk inside one score MFMA
+  static constexpr int NVG = 16 / CPG;  // PV column groups (one value group each)
+  static constexpr int NJJ = CPG / 2;   // PV MFMAs per column group (NVG * NJJ == 8)
+  static constexpr int PVS = CPG / 4;   // PV k-steps (32 tokens) per tile
+  static constexpr int KW = 0;
+  static constexpr int VW = KW + D * CPG;
+  static constexpr int KS = VW + GT * 16;
+  static constexpr int KM = KS + D;
+  static constexpr int VS = KM + D;
+  static constexpr int VM = VS + PVS * NVG * 32;
+  static constexpr int WORDS = VM + PVS * NVG * 32;
+  static constexpr int BYTES = 4 * WORDS;
+  // DMA instructions per tile; the waits rely on this number
+  static constexpr int KW_INST = D * CPG * 4 / 1024;  // 16-byte lanes
+  static constexpr int VW_INST = GT * 64 / 1024;      // 16-byte lanes
+  static constexpr int KS_INST = D / 64;              // 4-byte lanes
+  static constexpr int VS_INST = PVS * NVG * 32 / 64; // 4-byte lanes
+  static constexpr int NINST = KW_INST + VW_INST + 2 * KS_INST + 2 * VS_INST;
+  static_assert(NINST < 64, "vmcnt range");
 };
 
-// Issue the DMA loads of one tile (page blk, offsets [off0, off0 + GT), key
-// group grp) of kv head h into `buf`.  Every load is in bounds: the tile lies
-// inside page blk, which the caller has checked is a live block id.
 template <int CPG>
-__device__ __forceinline__ void issue_tile(char* buf, int lane, int64_t blk, int off0, int grp,
-                                           int h, int kvh, int bs, int gpb, int ng,
-                                           const uint32_t* __restrict__ kq,
-                                           const float* __restrict__ ks,
-                                           const float* __restrict__ km,
-                                           const uint32_t* __restrict__ vq,
-                                           const float* __restrict__ vs,
-                                           const float* __restrict__ vm) {
-  using L = TileLayout<CPG>;
-  constexpr int D = L::D;
-  constexpr int LPR = CPG / 4;   // 16-byte lanes per key dim row (CPG words)
+__device__ __forceinline__ int tile_token(int st, int kg, int i) {
+  constexpr int SUB = 16 / CPG;
+  const int jm = 2 * st + i / 4;
+  const int mr = 4 * kg + (i % 4);
+  return 8 * (mr % CPG) + jm * SUB + mr / CPG;
+}
+
+// Offsets of DMA lane e = 64*i + lane for the gathered scale/min regions.
+// Every field of e used below is a bit field and the maps are linear in
+// them, so off(64*i + lane) == off(64*i) + off(lane): the lane part is
+// computed once per wave, the instruction part folds to a uniform value.
+template <int CPG>
+__device__ __forceinline__ int key_scale_off(int e, int gpb) {
+  const int ii = e % 8, kg = (e / 8) % 4, s4 = e / 32;
+  return (32 * s4 + 4 * ii + kg) * gpb;
+}
+template <int CPG>
+__device__ __forceinline__ int value_scale_off(int e, int kvh, int ng, int g) {
+  constexpr int NVG = 16 / CPG;
+  const int i8 = e % 8, kg = (e / 8) % 4, v = (e / 32) % NVG, st = e / (32 * NVG);
+  return tile_token<CPG>(st, kg, i8) * kvh * ng + (8 * CPG * v) / g;
+}
+
+struct LaneDma {
+  uint32_t k, v, ks, vs;  // byte offsets of this lane's DMA data (lane part)
+};
+
+template <int CPG>
+__device__ __forceinline__ LaneDma lane_dma(int lane, int wpd, int kvh, int gpb, int ng, int g) {
+  constexpr int LPR = CPG / 4;  // 16-byte lanes per key dim row (CPG words)
+  LaneDma ld;
+  ld.k = static_cast<uint32_t>(4 * ((lane / LPR) * wpd + 4 * (lane % LPR)));
+  ld.v = static_cast<uint32_t>(4 * ((lane / 4) * kvh * 16 + 4 * (lane % 4)));
+  ld.ks = static_cast<uint32_t>(4 * key_scale_off<CPG>(lane, gpb));
+  ld.vs = static_cast<uint32_t>(4 * value_scale_off<CPG>(lane, kvh, ng, g));
+  return ld;
+}
+
+// DMA of one tile.  kq_t, vq_t, ks_t, km_t, vs_t, vm_t point at the tile's
+// first word/scale of kv head h (page blk, token offset off0, key group grp);
+// every lane address stays inside the tile's rows of that page.
+template <int CPG>
+__device__ __forceinline__ void issue_tile(char* buf, const LaneDma& ld, const uint32_t* kq_t,
+                                           int wpd, const uint32_t* vq_t, int kvh,
+                                           const float* ks_t, const float* km_t, int gpb,
+                                           const float* vs_t, const float* vm_t, int ng, int g) {
+  using T = Tile<CPG>;
+  constexpr int LPR = CPG / 4;
   constexpr int DPI = 64 / LPR;  // key dim rows per instruction
-  const int wpd = bs / 8;
-  const int64_t krow0 = (blk * kvh + h) * D;
+  const char* kb = reinterpret_cast<const char*>(kq_t);
+  const char* vb = reinterpret_cast<const char*>(vq_t);
+  const char* sb = reinterpret_cast<const char*>(ks_t);
+  const char* mb = reinterpret_cast<const char*>(km_t);
+  const char* vsb = reinterpret_cast<const char*>(vs_t);
+  const char* vmb = reinterpret_cast<const char*>(vm_t);
 #pragma unroll
-  for (int i = 0; i < L::KW_INST; ++i) {
-    const int d = i * DPI + lane / LPR;
-    const int part = lane % LPR;
-    dma16(kq + (krow0 + d) * wpd + off0 / 8 + 4 * part, buf + L::KW + i * 1024);
+  for (int i = 0; i < T::KW_INST; ++i)
+    dma16(kb + 4 * (i * DPI * wpd) + ld.k, buf + 4 * T::KW + 1024 * i);
+#pragma unroll
+  for (int i = 0; i < T::VW_INST; ++i)
+    dma16(vb + 4 * (16 * i * kvh * 16) + ld.v, buf + 4 * T::VW + 1024 * i);
+#pragma unroll
+  for (int i = 0; i < T::KS_INST; ++i) {
+    const int o = 4 * key_scale_off<CPG>(64 * i, gpb);
+    dma4(sb + o + ld.ks, buf + 4 * (T::KS + 64 * i));
+    dma4(mb + o + ld.ks, buf + 4 * (T::KM + 64 * i));
   }
 #pragma unroll
-  for (int i = 0; i < L::VW_INST; ++i) {
-    const int t = 16 * i + lane / 4;
-    const int part = lane % 4;
-    dma16(vq + ((blk * bs + off0 + t) * kvh + h) * 16 + 4 * part, buf + L::VW + i * 1024);
+  for (int i = 0; i < T::VS_INST; ++i) {
+    const int o = 4 * value_scale_off<CPG>(64 * i, kvh, ng, g);
+    dma4(vsb + o + ld.vs, buf + 4 * (T::VS + 64 * i));
+    dma4(vmb + o + ld.vs, buf + 4 * (T::VM + 64 * i));
+  }
+}
+
+__device__ __forceinline__ void read8(const uint32_t* p, uint32_t (&w)[8]) {
+  const uint4 a = *reinterpret_cast<const uint4*>(p);
+  const uint4 b = *reinterpret_cast<const uint4*>(p + 4);
+  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+}
+__device__ __forceinline__ void read8f(const uint32_t* p, float (&f)[8]) {
+  uint32_t w[8];
+  read8(p, w);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = __uint_as_float(w[i]);
+}
+
+// fp16 pair of nibbles from two words: byte `sel` of lo and of hi, the nibble
+// picked by `mask` (0x000f000f: low nibble -> 1024 + c; 0x00f000f0: high
+// nibble -> 1024 + 16c, exact as well).
+__device__ __forceinline__ uint32_t nib_pair(uint32_t lo, uint32_t hi, uint32_t sel,
+                                             uint32_t mask) {
+  return (__builtin_amdgcn_perm(hi, lo, sel) & mask) | kMagic;
+}
+// ... with the 1024 removed exactly: c or 16c.
+__device__ __forceinline__ uint32_t nib_pair_exact(uint32_t lo, uint32_t hi, uint32_t sel,
+                                                   uint32_t mask) {
+  const h2 v = __builtin_bit_cast(h2, nib_pair(lo, hi, sel, mask)) - h2{1024.0f16, 1024.0f16};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Per-lane constants of the nibble selection (lanes of odd nibble parity read
+// codes as 16c; their score rows / output columns are scaled back by 1/16).
+template <int CPG>
+struct LaneNib {
+  uint32_t selk[CPG / 2];  // byte selectors of the score MFMAs (per jm)
+  uint32_t selv[CPG / 2];  // byte selectors of the PV MFMAs (per jj)
+  uint32_t maskk, maskv;
+  float row_scale;         // score rows held by this lane: 1 or 1/16
+  float col_scale;         // output column held by this lane: 1 or 1/16
+  __device__ __forceinline__ LaneNib(int n, int kg) {
+    constexpr int SUB = 16 / CPG;
+    const int sub = n / CPG;
+    // (jm*SUB + sub) >> 1 with SUB even: jm*SUB/2 + sub/2 (sub/2 == 0 for CPG 8)
+#pragma unroll
+    for (int jm = 0; jm < CPG / 2; ++jm) {
+      selk[jm] = pair_sel(static_cast<uint32_t>(jm * (SUB / 2) + (sub >> 1)));
+      selv[jm] = selk[jm];
+    }
+    const bool odd = (sub & 1) != 0;  // SUB is even, so the parity is sub's
+    maskk = maskv = odd ? 0x00f000f0u : 0x000f000fu;
+    const int row_sub = (4 * kg) / CPG;  // score rows 4*kg + r all share it
+    row_scale = (row_sub & 1) ? 0.0625f : 1.0f;
+    col_scale = odd ? 0.0625f : 1.0f;
+  }
+};
+
+// The lane's 32 query values (dims 32*s4 + 4*ii + kg) kept as 16 packed
+// pairs for 16-bit inputs (pair 4*s4 + p = elements 2p, 2p+1 of k-step s4).
+template <typename TQ>
+struct QRegs {
+  uint32_t w[16];
+  __device__ __forceinline__ void set(int i, TQ lo, TQ hi) {
+    w[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
+  }
+  __device__ __forceinline__ float lo(int i) const {
+    return to_f32(__builtin_bit_cast(TQ, static_cast<uint16_t>(w[i] & 0xffffu)));
+  }
+  __device__ __forceinline__ float hi(int i) const {
+    return to_f32(__builtin_bit_cast(TQ, static_cast<uint16_t>(w[i] >> 16)));
+  }
+};
+template <>
+struct QRegs<float> {
+  float w[32];
+  __device__ __forceinline__ void set(int i, float lo, float hi) {
+    w[2 * i] = lo;
+    w[2 * i + 1] = hi;
+  }
+  __device__ __forceinline__ float lo(int i) const { return w[2 * i]; }
+  __device__ __forceinline__ float hi(int i) const { return w[2 * i + 1]; }
+};
+
+// One tile of scores, softmax update and PV.  FULL: every token < pe.
+template <typename TQ, int CPG, bool FULL>
+__device__ __forceinline__ void compute_tile(const uint32_t* W, int p0, int pe, int n, int kg,
+                                             const QRegs<TQ>& qv, float qscale,
+                                             const LaneNib<CPG>& ln, float& m_run, float& l_run, f4 (&o_acc)[8],
+                                             f4 (&c_acc)[16 / CPG], float (&bias_v)[16 / CPG]) {
+  // attention math is tolerance-checked: let mul+add fuse here (the library
+  // builds with -ffp-contract=off for the bit-exact pack/dequant paths)
+#pragma clang fp contract(fast)
+  using T = Tile<CPG>;
+  const int chunk = n % CPG;
+  const h8 ones_b = as_h8(kMagic, kMagic, kMagic, kMagic);
+  // ---- scores ----------------------------------------------------------------
+  float kb = 0.0f;
+  f4 sacc[T::NJ];
+#pragma unroll
+  for (int j = 0; j < T::NJ; ++j) sacc[j] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) {
+    float sc[8], mn[8];
+    read8f(W + T::KS + (s4 * 4 + kg) * 8, sc);
+    read8f(W + T::KM + (s4 * 4 + kg) * 8, mn);
+    uint32_t w[8];  // dims 32*s4 + 4*ii + kg of chunk `chunk`: pairs 32 words apart
+    {
+      const uint32_t* kw = W + T::KW + (32 * s4 + kg) * CPG + chunk;
+#pragma unroll
+      for (int ii = 0; ii < 8; ++ii) w[ii] = kw[4 * ii * CPG];
+    }
+    uint32_t qh[4], ql[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float q0 = qv.lo(4 * s4 + p);  // exact widening of the input
+      const float q1 = qv.hi(4 * s4 + p);
+      _Float16 h0, l0, h1, l1;
+      split_h(q0 * sc[2 * p], h0, l0);
+      split_h(q1 * sc[2 * p + 1], h1, l1);
+      qh[p] = h2_bits(h0, h1);
+      ql[p] = h2_bits(l0, l1);
+      kb += q0 * mn[2 * p] + q1 * mn[2 * p + 1];
+    }
+    const h8 bq = as_h8(qh[0], qh[1], qh[2], qh[3]);
+    const h8 bl = as_h8(ql[0], ql[1], ql[2], ql[3]);
+#pragma unroll
+    for (int jm = 0; jm < T::NJ; ++jm) {
+      const uint32_t sel = ln.selk[jm];
+      const h8 a = as_h8(nib_pair_exact(w[0], w[1], sel, ln.maskk),
+                         nib_pair_exact(w[2], w[3], sel, ln.maskk),
+                         nib_pair_exact(w[4], w[5], sel, ln.maskk),
+                         nib_pair_exact(w[6], w[7], sel, ln.maskk));
+      sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, sacc[jm], 0, 0, 0);
+      sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, sacc[jm], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the k-steps' live ranges apart
+  }
+  kb = sum_kg(kb) * qscale;
+  // softmax scale * log2(e), and 1/16 on the rows read as 16c
+  const float rs = qscale * ln.row_scale;
+  // lane holds head n, rows m' = 4*kg + r: token tk = tile_token(jm/2, kg, 4*(jm%2) + r)
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int jm = 0; jm < T::NJ; ++jm) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float sv = sacc[jm][r] * rs + kb;
+      if (!FULL) {
+        const int pos = p0 + tile_token<CPG>(jm / 2, kg, 4 * (jm % 2) + r);
+        sv = pos < pe ? sv : -INFINITY;
+      }
+      sacc[jm][r] = sv;
+      tmax = fmaxf(tmax, sv);
+    }
+  }
+  tmax = max_kg(tmax);
+  const float m_new = fmaxf(m_run, tmax);
+  const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+  float psum = 0.0f;
+#pragma unroll
+  for (int jm = 0; jm < T::NJ; ++jm) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pr = __builtin_amdgcn_exp2f(sacc[jm][r] - m_new);  // v_exp_f32
+      sacc[jm][r] = pr;
+      psum += pr;
+    }
+  }
+  l_run = l_run * alpha + sum_kg(psum);
+  m_run = m_new;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float ar = __shfl(alpha, 4 * kg + r, 64);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) o_acc[q][r] *= ar;
+#pragma unroll
+    for (int v = 0; v < T::NVG; ++v) c_acc[v][r] *= ar;
   }
 #pragma unroll
-  for (int i = 0; i < D / 64; ++i) {
-    const int d = 64 * i + lane;
-    dma4(ks + (krow0 + d) * gpb + grp, buf + L::KS + i * 256);
-    dma4(km + (krow0 + d) * gpb + grp, buf + L::KM + i * 256);
-  }
+  for (int v = 0; v < T::NVG; ++v) bias_v[v] *= alpha;
+
+  // ---- PV ----------------------------------------------------------------------
 #pragma unroll
-  for (int i = 0; i < L::GT * L::NVG / 64; ++i) {
-    const int e = 64 * i + lane;
-    const int t = e / L::NVG;
-    int vg = e % L::NVG;
-    vg = vg < ng ? vg : 0;  // slots past the tile's groups load a duplicate (never read)
-    const int64_t idx = ((blk * bs + off0 + t) * kvh + h) * ng + vg;
-    dma4(vs + idx, buf + L::VS + i * 256);
-    dma4(vm + idx, buf + L::VM + i * 256);
+  for (int st = 0; st < T::PVS; ++st) {
+    float pv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pv[i] = sacc[2 * st + i / 4][i % 4];
+#pragma unroll
+    for (int v = 0; v < T::NVG; ++v) {
+      const int base = ((st * T::NVG + v) * 4 + kg) * 8;
+      float sc[8], mn[8];
+      read8f(W + T::VS + base, sc);
+      read8f(W + T::VM + base, mn);
+      float pp[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float s_ = sc[i], m_ = mn[i];
+        if (!FULL) {
+          // past the range p = 0, but the scale/min bytes are unwritten:
+          // select zeros so a stale NaN cannot reach the sums
+          const bool live = p0 + tile_token<CPG>(st, kg, i) < pe;
+          s_ = live ? s_ : 0.0f;
+          m_ = live ? m_ : 0.0f;
+        }
+        pp[i] = pv[i] * s_;
+        bias_v[v] += pv[i] * m_;
+      }
+      const h8 a = as_h8(pack_h2(pp[0], pp[1]), pack_h2(pp[2], pp[3]), pack_h2(pp[4], pp[5]),
+                         pack_h2(pp[6], pp[7]));
+      c_acc[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ones_b, c_acc[v], 0, 0, 0);
+      uint32_t w[8];  // word chunk + CPG*v of tokens tk(st, kg, i)
+      {
+        const uint32_t* vw = W + T::VW + chunk + CPG * v;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = vw[16 * tile_token<CPG>(st, kg, i)];
+      }
+#pragma unroll
+      for (int jj = 0; jj < T::NJJ; ++jj) {
+        const uint32_t sel = ln.selv[jj];
+        const h8 bv = as_h8(nib_pair(w[0], w[1], sel, ln.maskv), nib_pair(w[2], w[3], sel, ln.maskv),
+                            nib_pair(w[4], w[5], sel, ln.maskv), nib_pair(w[6], w[7], sel, ln.maskv));
+        o_acc[v * T::NJJ + jj] =
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv, o_acc[v * T::NJJ + jj], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 }
 
@@ -196,23 +469,20 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
                         const float* __restrict__ km, const uint32_t* __restrict__ vq,
                         const float* __restrict__ vs, const float* __restrict__ vm, int bs,
                         int g, int64_t nb, const int32_t* __restrict__ block_table,
-                        int64_t maxb, const int32_t* __restrict__ work,
+                        int64_t maxb, const int32_t* __restrict__ work, int64_t num_work,
                         float* __restrict__ ws_o, float* __restrict__ ws_ml) {
-  using L = TileLayout<CPG>;
-  constexpr int D = L::D;
-  constexpr int GT = L::GT;      // tokens per tile
-  constexpr int NJ = CPG / 2;    // score MFMAs per k-step (16 tokens each)
-  constexpr int SUB = 16 / CPG;  // tokens of one chunk inside one score MFMA
-  constexpr int NVG = L::NVG;    // PV column groups (one value group each)
-  constexpr int NJJ = CPG / 2;   // PV MFMAs per column group (NVG * NJJ == 8)
-  constexpr int PVS = CPG / 4;   // PV k-steps (32 tokens) per tile
+  using T = Tile<CPG>;
+  constexpr int D = T::D;
+  constexpr int GT = T::GT;
+  constexpr int NVG = T::NVG;
+  constexpr int NJJ = T::NJJ;
 
   extern __shared__ __align__(16) char lds_raw[];
-  const int wi = blockIdx.x;
-  const int h = blockIdx.y;
+  int wi, h;
+  if (!xcd_item_head(blockIdx.x, kvh, num_work, wi, h)) return;
   const int lane = threadIdx.x;
   const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
-  if (wk[3] != 0) return;  // kind-1 items belong to the generic kernel (uniform)
+  if (wk[3] != 0) return;  // kind-1 items belong to the tail kernel (uniform)
   const int b = wk[0];
   const int pb = wk[1];
   const int pe = wk[2];
@@ -221,25 +491,28 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   const int kg = lane >> 4;
   const int gpb = bs / g;
   const int ng = D / g;
+  const int wpd = bs / 8;
   const int32_t* bt = block_table + static_cast<int64_t>(b) * maxb;
 
-  // q of head n for the lane's dims d = 32*s + 4*i + kg, in the input dtype.
-  // Lanes past the GQA group read head 0's row (always valid) and zero it, so
-  // the 32 loads issue back to back instead of behind per-lane branches.
-  TQ qv[32];
+  // q of head n for dims 32*s4 + 4*ii + kg in the input dtype (the softmax
+  // scale is applied to the fp32 scores).  Lanes past the GQA group read head
+  // 0's row (always valid) and zero it.
+  QRegs<TQ> qv;
   {
     const bool live = n < rep;
     const TQ* qrow = query + (static_cast<int64_t>(b) * hq + h * rep + (live ? n : 0)) * D;
+    const TQ zero = from_f32<TQ>(0.0f);
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qv[8 * s4 + i] = qrow[32 * s4 + 4 * i + kg];
-    if (!live) {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) qv[i] = from_f32<TQ>(0.0f);
-    }
+      for (int p = 0; p < 4; ++p) {
+        const TQ lo = qrow[32 * s4 + 8 * p + kg];
+        const TQ hi = qrow[32 * s4 + 8 * p + 4 + kg];
+        qv.set(4 * s4 + p, live ? lo : zero, live ? hi : zero);
+      }
   }
-  const h8 ones_a = as_h8(kMagic, kMagic, kMagic, kMagic);
+  const LaneNib<CPG> ln(n, kg);
+  const LaneDma ld = lane_dma<CPG>(lane, wpd, kvh, gpb, ng, g);
 
   float m_run = -INFINITY;
   float l_run = 0.0f;
@@ -256,167 +529,39 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
 
   // page ids are clamped into [0, nb): the host validates live ids, the clamp
   // only guarantees that no DMA can leave the cache whatever the table holds
-  auto page = [&](int p) -> int64_t {
-    const int64_t blk = bt[p / bs];
-    return blk < 0 ? 0 : (blk >= nb ? nb - 1 : blk);
+  auto issue = [&](char* buf, int p) {
+    const int64_t b0 = bt[p / bs];
+    const int64_t blk = b0 < 0 ? 0 : (b0 >= nb ? nb - 1 : b0);
+    const int off0 = p % bs;
+    const int64_t krow = (blk * kvh + h) * D;
+    const int64_t vtok = (blk * bs + off0) * kvh + h;
+    issue_tile<CPG>(buf, ld, kq + krow * wpd + off0 / 8, wpd, vq + vtok * 16, kvh,
+                    ks + krow * gpb + off0 / g, km + krow * gpb + off0 / g, gpb, vs + vtok * ng,
+                    vm + vtok * ng, ng, g);
   };
-  // prologue: tile 0 into buffer 0
-  {
-    const int64_t blk = page(pb);
-    issue_tile<CPG>(lds_raw, lane, blk, pb % bs, (pb % bs) / g, h, kvh, bs, gpb, ng, kq, ks, km,
-                    vq, vs, vm);
-  }
+  issue(lds_raw, pb);  // prologue: tile 0 into buffer 0
   int cur = 0;
   for (int p0 = pb; p0 < pe; p0 += GT) {
     // prefetch tile p0 + GT into the other buffer, then wait for this tile only
     const int p1 = p0 + GT;
     if (p1 < pe) {
-      const int64_t blk1 = page(p1);
-      issue_tile<CPG>(lds_raw + (cur ^ 1) * L::BYTES, lane, blk1, p1 % bs, (p1 % bs) / g, h,
-                      kvh, bs, gpb, ng, kq, ks, km, vq, vs, vm);
-      wait_vmcnt<L::NINST>();
+      issue(lds_raw + (cur ^ 1) * T::BYTES, p1);
+      wait_vmcnt<T::NINST>();
     } else {
       wait_vmcnt<0>();
     }
-    const char* buf = lds_raw + cur * L::BYTES;
-    const float* sks = reinterpret_cast<const float*>(buf + L::KS);
-    const float* skm = reinterpret_cast<const float*>(buf + L::KM);
-    const uint32_t* skw = reinterpret_cast<const uint32_t*>(buf + L::KW);
-    const uint32_t* svw = reinterpret_cast<const uint32_t*>(buf + L::VW);
-    const float* svs = reinterpret_cast<const float*>(buf + L::VS);
-    const float* svm = reinterpret_cast<const float*>(buf + L::VM);
-
-    // ---- scores ------------------------------------------------------------
-    const int chunk = n % CPG;
-    const int sub = n / CPG;
-    float kb = 0.0f;
-    f4 sacc[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) sacc[j] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      uint32_t qh[4], ql[4];
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int d0 = 32 * s4 + 8 * p + kg;  // element 2p
-        const int d1 = d0 + 4;                // element 2p + 1
-        const float q0 = to_f32(qv[8 * s4 + 2 * p]) * qscale;
-        const float q1 = to_f32(qv[8 * s4 + 2 * p + 1]) * qscale;
-        _Float16 h0, l0, h1, l1;
-        split_h(q0 * sks[d0], h0, l0);
-        split_h(q1 * sks[d1], h1, l1);
-        qh[p] = h2_bits(h0, h1);
-        ql[p] = h2_bits(l0, l1);
-        kb += q0 * skm[d0] + q1 * skm[d1];
-      }
-      uint32_t w[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) w[i] = skw[(32 * s4 + 4 * i + kg) * CPG + chunk];
-      const h8 bq = as_h8(qh[0], qh[1], qh[2], qh[3]);
-      const h8 bl = as_h8(ql[0], ql[1], ql[2], ql[3]);
-#pragma unroll
-      for (int jm = 0; jm < NJ; ++jm) {
-        const uint32_t j = static_cast<uint32_t>(jm * SUB + sub);
-        const h8 a = as_h8(code_pair_exact(w[0], w[1], j), code_pair_exact(w[2], w[3], j),
-                           code_pair_exact(w[4], w[5], j), code_pair_exact(w[6], w[7], j));
-        sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, sacc[jm], 0, 0, 0);
-        sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, sacc[jm], 0, 0, 0);
-      }
-    }
-    kb = sum_kg(kb);
-    // lane holds head n, rows m' = 4*kg + r: token 8*(m' % CPG) + jm*SUB + m'/CPG
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int jm = 0; jm < NJ; ++jm) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int mr = 4 * kg + r;
-        const int pos = p0 + 8 * (mr % CPG) + jm * SUB + mr / CPG;
-        const float sv = pos < pe ? sacc[jm][r] + kb : -INFINITY;
-        sacc[jm][r] = sv;
-        tmax = fmaxf(tmax, sv);
-      }
-    }
-    tmax = max_kg(tmax);
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = m_run == -INFINITY ? 0.0f : exp2f(m_run - m_new);
-    float psum = 0.0f;
-#pragma unroll
-    for (int jm = 0; jm < NJ; ++jm) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pr = exp2f(sacc[jm][r] - m_new);
-        sacc[jm][r] = pr;
-        psum += pr;
-      }
-    }
-    l_run = l_run * alpha + sum_kg(psum);
-    m_run = m_new;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float ar = __shfl(alpha, 4 * kg + r, 64);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) o_acc[q][r] *= ar;
-#pragma unroll
-      for (int v = 0; v < NVG; ++v) c_acc[v][r] *= ar;
-    }
-#pragma unroll
-    for (int v = 0; v < NVG; ++v) bias_v[v] *= alpha;
-
-    // ---- PV ------------------------------------------------------------------
-#pragma unroll
-    for (int st = 0; st < PVS; ++st) {
-      int tk[8];
-      float pv[8];
-      bool live[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int jm = 2 * st + i / 4;
-        const int mr = 4 * kg + (i % 4);
-        tk[i] = 8 * (mr % CPG) + jm * SUB + mr / CPG;
-        pv[i] = sacc[jm][i % 4];
-        live[i] = p0 + tk[i] < pe;
-      }
-#pragma unroll
-      for (int v = 0; v < NVG; ++v) {
-        const int vgrp = (8 * CPG * v) / g;
-        float pp[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          // tokens past the range have p = 0 but unwritten scale/min bytes:
-          // select zeros so a stale NaN cannot leak into the sums (the reads
-          // stay inside the tile buffer, so they are unconditional)
-          const float sc_raw = svs[tk[i] * NVG + vgrp];
-          const float mn_raw = svm[tk[i] * NVG + vgrp];
-          const float sc = live[i] ? sc_raw : 0.0f;
-          const float mn = live[i] ? mn_raw : 0.0f;
-          pp[i] = pv[i] * sc;
-          bias_v[v] += pv[i] * mn;
-        }
-        const h8 a = as_h8(pack_h2(pp[0], pp[1]), pack_h2(pp[2], pp[3]), pack_h2(pp[4], pp[5]),
-                           pack_h2(pp[6], pp[7]));
-        c_acc[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ones_a, c_acc[v], 0, 0, 0);
-        const int vchunk = n % CPG + CPG * v;
-        uint32_t w[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = svw[tk[i] * 16 + vchunk];
-#pragma unroll
-        for (int jj = 0; jj < NJJ; ++jj) {
-          const uint32_t nib = static_cast<uint32_t>(jj * SUB + n / CPG);
-          const h8 bv = as_h8(code_pair(w[0], w[1], nib), code_pair(w[2], w[3], nib),
-                              code_pair(w[4], w[5], nib), code_pair(w[6], w[7], nib));
-          o_acc[v * NJJ + jj] =
-              __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv, o_acc[v * NJJ + jj], 0, 0, 0);
-        }
-      }
-    }
+    const uint32_t* W = reinterpret_cast<const uint32_t*>(lds_raw + cur * T::BYTES);
+    if (p0 + GT <= pe)
+      compute_tile<TQ, CPG, true>(W, p0, pe, n, kg, qv, qscale, ln, m_run, l_run, o_acc, c_acc, bias_v);
+    else
+      compute_tile<TQ, CPG, false>(W, p0, pe, n, kg, qv, qscale, ln, m_run, l_run, o_acc, c_acc, bias_v);
     // every LDS read of this buffer has been consumed before the next
     // iteration's DMA may overwrite it
     asm volatile("" ::: "memory");
     cur ^= 1;
   }
 
-  // ---- epilogue: remove the PV offset, add the value-minimum term --------
+  // ---- epilogue: remove the PV offset, undo the 16x columns, add the minima ----
 #pragma unroll
   for (int v = 0; v < NVG; ++v) bias_v[v] = sum_kg(bias_v[v]);
   const int64_t head0 = static_cast<int64_t>(wi) * hq + h * rep;
@@ -425,11 +570,13 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
     const int hh = 4 * kg + r;
 #pragma unroll
     for (int v = 0; v < NVG; ++v) {
-      const float bv = __shfl(bias_v[v], hh, 64) - c_acc[v][r];
+      const float bv = __shfl(bias_v[v], hh, 64);
 #pragma unroll
       for (int jj = 0; jj < NJJ; ++jj) {
-        const int dim = 8 * (n % CPG + CPG * v) + jj * SUB + n / CPG;
-        if (hh < rep) ws_o[(head0 + hh) * D + dim] = o_acc[v * NJJ + jj][r] + bv;
+        const int dim = 8 * (n % CPG + CPG * v) + jj * T::SUB + n / CPG;
+        if (hh < rep)
+          ws_o[(head0 + hh) * D + dim] =
+              (o_acc[v * NJJ + jj][r] - c_acc[v][r]) * ln.col_scale + bv;
       }
     }
   }
@@ -488,16 +635,16 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
   // tiles of 64 tokens (32 for G = 32): inside one key group and one page
   const int cpg = g >= 64 ? 8 : 4;
   if (bs % (8 * cpg)) return KVQ_OK;
-  const dim3 grid(static_cast<unsigned>(num_work), kvh);
+  const dim3 grid(static_cast<unsigned>(xcd_grid_size(num_work, kvh)));
   const dim3 block(64);
   const uint32_t* kqu = reinterpret_cast<const uint32_t*>(kq);
   const uint32_t* vqu = reinterpret_cast<const uint32_t*>(vq);
 #define KVQ_LAUNCH_MFMA(C)                                                                   \
   KVQ_DISPATCH_FLOAT(q_dtype, TQ,                                                           \
     hipLaunchKernelGGL((kivi_decode_mfma_kernel<TQ, C>), grid, block,                       \
-                       2 * TileLayout<C>::BYTES, s, static_cast<const TQ*>(query), hq, kvh, \
+                       2 * Tile<C>::BYTES, s, static_cast<const TQ*>(query), hq, kvh, \
                        qscale, kqu, ks, km, vqu, vs, vm, bs, g, nb, block_table, maxb, work,\
-                       ws_o, ws_ml))
+                       num_work, ws_o, ws_ml))
   if (cpg == 8) {
     KVQ_LAUNCH_MFMA(8);
   } else {

@@ -74,15 +74,15 @@ kivi_decode_tail_mfma_kernel(const T* __restrict__ query, int hq, int kvh, float
                              int g, int64_t nb, const int32_t* __restrict__ block_table,
                              int64_t maxb, const int32_t* __restrict__ seq_meta,
                              const int32_t* __restrict__ work, const T* __restrict__ ring_k,
-                             const T* __restrict__ ring_v, int ring_len,
+                             const T* __restrict__ ring_v, int ring_len, int64_t num_work,
                              float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   constexpr int D = kD;
   extern __shared__ __align__(16) char lds_raw[];
   uint16_t* sk = reinterpret_cast<uint16_t*>(lds_raw);  // [kTT][kKP]
   uint16_t* svt = sk + kTT * kKP;                        // [D][kVP]
 
-  const int wi = blockIdx.x;
-  const int h = blockIdx.y;
+  int wi, h;
+  if (!xcd_item_head(blockIdx.x, kvh, num_work, wi, h)) return;
   const int lane = threadIdx.x;
   const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
   if (wk[3] != 1) return;  // kind-0 items belong to the int4 MFMA kernel (uniform)
@@ -340,7 +340,7 @@ int launch_kivi_decode_tail_mfma(const void* query, int q_dtype, int hq, int kvh
   *launched = false;
   if (d != kD || hq / kvh > 16 || ring_dtype != q_dtype) return KVQ_OK;
   if (q_dtype != KVQ_DTYPE_BF16 && q_dtype != KVQ_DTYPE_F16) return KVQ_OK;
-  const dim3 grid(static_cast<unsigned>(num_work), kvh);
+  const dim3 grid(static_cast<unsigned>(xcd_grid_size(num_work, kvh)));
   const size_t lds = sizeof(uint16_t) * (kTT * kKP + kD * kVP);
   const uint32_t* kqu = reinterpret_cast<const uint32_t*>(kq);
   const uint32_t* vqu = reinterpret_cast<const uint32_t*>(vq);
@@ -349,13 +349,13 @@ int launch_kivi_decode_tail_mfma(const void* query, int q_dtype, int hq, int kvh
                        static_cast<const bf16*>(query), hq, kvh, qscale, kqu, ks, km, vqu, vs, vm,
                        bs, g, nb, block_table, maxb, seq_meta, work,
                        static_cast<const bf16*>(ring_k), static_cast<const bf16*>(ring_v),
-                       ring_len, ws_o, ws_ml);
+                       ring_len, num_work, ws_o, ws_ml);
   } else {
     hipLaunchKernelGGL((kivi_decode_tail_mfma_kernel<f16>), grid, dim3(64), lds, s,
                        static_cast<const f16*>(query), hq, kvh, qscale, kqu, ks, km, vqu, vs, vm,
                        bs, g, nb, block_table, maxb, seq_meta, work,
                        static_cast<const f16*>(ring_k), static_cast<const f16*>(ring_v),
-                       ring_len, ws_o, ws_ml);
+                       ring_len, num_work, ws_o, ws_ml);
   }
   KVQ_LAUNCH_CHECK();
   *launched = true;

@@ -7,6 +7,26 @@
 
 namespace kvq {
 
+// ---- XCD-aware grid mapping ------------------------------------------------
+// Workgroups are handed to the 8 XCDs round-robin (id % 8).  The kv heads of
+// one work item share HBM lines: a token's value words and value scales/mins
+// of all heads are contiguous.  Mapping id -> (item, head) so that every head
+// of an item lands on the same XCD lets that XCD's L2 serve each line once.
+constexpr int kXcds = 8;
+
+__host__ __device__ __forceinline__ int64_t xcd_grid_size(int64_t num_work, int kvh) {
+  return (num_work + kXcds - 1) / kXcds * kXcds * kvh;
+}
+
+__device__ __forceinline__ bool xcd_item_head(int64_t id, int kvh, int64_t num_work, int& item,
+                                              int& head) {
+  const int64_t j = id / kXcds;
+  const int64_t it = id % kXcds + kXcds * (j / kvh);
+  head = static_cast<int>(j % kvh);
+  item = static_cast<int>(it);
+  return it < num_work;
+}
+
 // Workspace: o [num_work, num_heads, D] fp32, then (m, l) [num_work, num_heads, 2].
 inline int64_t decode_workspace_bytes(int64_t num_work, int num_heads, int head_size) {
   return num_work * num_heads * (static_cast<int64_t>(head_size) + 2) *
