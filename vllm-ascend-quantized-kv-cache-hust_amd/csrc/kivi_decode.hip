@@ -11,12 +11,16 @@
 // Work items (built by the host from the request lengths, no device sync):
 //   kind 0: a range where keys and values both come from int4 pages -- the
 //           MFMA kernel of kivi_decode_mfma.hip;
-//   kind 1: any range (tails where one side is already in the ring, and
-//           geometries the MFMA kernel does not cover) -- the generic kernel
-//           below: one wave per (work item, kv head), the QK dot products
-//           lane-per-position, the PV accumulation lane-per-dim.
+//   kind 1: tails where one side is already in the ring -- the MFMA tail
+//           kernel of decode_tail_mfma.hip, on a side stream beside the
+//           kind-0 kernel.
+// Geometries either MFMA kernel does not cover go to the generic kernel
+// below: one wave per (work item, kv head), the QK dot products
+// lane-per-position, the PV accumulation lane-per-dim.
 // Each work item leaves (m, l, o[D]) per query head in the workspace (m in
-// the log2 domain); kvq_decode_combine merges a request's items.
+// the log2 domain); the combine kernel merges a request's items.
+#include <mutex>
+
 #include "kvq_common.h"
 #include "kvq_decode.h"
 
@@ -292,43 +296,120 @@ kivi_decode_generic_kernel(const TQ* __restrict__ query, int hq, int kvh, int d,
 
 namespace kvq {
 
-template <typename TO>
-__global__ void __launch_bounds__(64)
+// Side stream of each device for the tail items: the tail kernel and the int4
+// kernel write disjoint workspace rows, so the tail runs beside the int4
+// kernel.  Created on first use (default priority) and kept for the process;
+// fork_mutex() serializes the record/wait sequence between host threads.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t join = nullptr;
+};
+
+static std::mutex& fork_mutex() {
+  static std::mutex mu;
+  return mu;
+}
+
+// Caller holds fork_mutex().
+static hipError_t side_stream(SideStream** out) {
+  static SideStream side[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  SideStream& st = side[dev];
+  if (!st.stream) {
+    if ((e = hipEventCreateWithFlags(&st.fork, hipEventDisableTiming)) != hipSuccess) return e;
+    if ((e = hipEventCreateWithFlags(&st.join, hipEventDisableTiming)) != hipSuccess) return e;
+    if ((e = hipStreamCreateWithFlags(&st.stream, hipStreamNonBlocking)) != hipSuccess) return e;
+  }
+  *out = &st;
+  return hipSuccess;
+}
+
+// Log-sum-exp combine of a request's work items: one wave per (request, query
+// head), four heads per workgroup.  Lane s holds item s's (m, l) of the current
+// chunk of 64 items; the weights 2^(m_s - max) go to every lane through
+// readlane, and each lane accumulates columns lane + 64*k of sum_s w_s * o_s.
+// Items with m = -inf (no position) carry weight 0 and their o is never read.
+template <typename TO, int KD>
+__global__ void __launch_bounds__(256)
 decode_combine_kernel(int hq, int d, const int32_t* __restrict__ seq_meta, int meta_stride,
                       int first_col, const float* __restrict__ ws_o,
                       const float* __restrict__ ws_ml, TO* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int hh = blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (hh >= hq) return;  // whole wave: no workgroup barrier below
   const int b = blockIdx.x;
-  const int hh = blockIdx.y;
   const int32_t* sm = seq_meta + static_cast<int64_t>(meta_stride) * b;
   const int fw = sm[first_col];
   const int nw = sm[first_col + 1];
   float mx = -INFINITY;
-  for (int s = 0; s < nw; ++s) mx = fmaxf(mx, ws_ml[2 * (static_cast<int64_t>(fw + s) * hq + hh)]);
-  float wsum = 0.0f;
-  for (int s = 0; s < nw; ++s) {
-    const int64_t idx = static_cast<int64_t>(fw + s) * hq + hh;
-    const float ms = ws_ml[2 * idx];
-    if (ms != -INFINITY) wsum += exp2f(ms - mx) * ws_ml[2 * idx + 1];
+  for (int s0 = 0; s0 < nw; s0 += 64) {
+    const int s = s0 + lane;
+    if (s < nw) mx = fmaxf(mx, ws_ml[2 * (static_cast<int64_t>(fw + s) * hq + hh)]);
   }
-  const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
-  for (int c = threadIdx.x; c < d; c += blockDim.x) {
-    float o = 0.0f;
-    for (int s = 0; s < nw; ++s) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  float acc[KD];
+#pragma unroll
+  for (int k = 0; k < KD; ++k) acc[k] = 0.0f;
+  float wsum = 0.0f;
+  for (int s0 = 0; s0 < nw; s0 += 64) {
+    const int s = s0 + lane;
+    float wgt = 0.0f;
+    if (s < nw) {
       const int64_t idx = static_cast<int64_t>(fw + s) * hq + hh;
       const float ms = ws_ml[2 * idx];
-      if (ms != -INFINITY) o += exp2f(ms - mx) * ws_o[idx * d + c];
+      if (ms != -INFINITY) {
+        wgt = exp2f(ms - mx);
+        wsum += wgt * ws_ml[2 * idx + 1];
+      }
     }
-    out[(static_cast<int64_t>(b) * hq + hh) * d + c] = from_f32<TO>(o * inv);
+    const int cnt = nw - s0 < 64 ? nw - s0 : 64;
+    const float* row0 = ws_o + (static_cast<int64_t>(fw + s0) * hq + hh) * d;
+    const int64_t stride = static_cast<int64_t>(hq) * d;
+#pragma unroll 4
+    for (int j = 0; j < cnt; ++j) {
+      const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), j));
+      const float* row = row0 + j * stride;
+#pragma unroll
+      for (int k = 0; k < KD; ++k) {
+        const int c = lane + 64 * k;
+        const float x = row[c < d ? c : 0];  // columns past d are read in bounds, unused
+        acc[k] += wj != 0.0f ? wj * x : 0.0f;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) wsum += __shfl_xor(wsum, o, 64);
+  const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+  TO* orow = out + (static_cast<int64_t>(b) * hq + hh) * d;
+#pragma unroll
+  for (int k = 0; k < KD; ++k) {
+    const int c = lane + 64 * k;
+    if (c < d) orow[c] = from_f32<TO>(acc[k] * inv);
   }
 }
 
 int launch_decode_combine(int dtype, int64_t batch, int hq, int d, const int32_t* seq_meta,
                           int meta_stride, int first_col, const float* ws_o,
                           const float* ws_ml, void* out, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(batch), hq);
-  KVQ_DISPATCH_FLOAT(dtype, TO,
-    hipLaunchKernelGGL((decode_combine_kernel<TO>), grid, dim3(64), 0, s, hq, d, seq_meta,
-                       meta_stride, first_col, ws_o, ws_ml, static_cast<TO*>(out)));
+  if (d <= 0 || d > 256) return KVQ_ERR_GEOMETRY;
+  const dim3 grid(static_cast<unsigned>(batch), (hq + 3) / 4);
+  const int kd = (d + 63) / 64;
+#define KVQ_LAUNCH_COMBINE(KD)                                                              \
+  KVQ_DISPATCH_FLOAT(dtype, TO,                                                             \
+    hipLaunchKernelGGL((decode_combine_kernel<TO, KD>), grid, dim3(256), 0, s, hq, d,       \
+                       seq_meta, meta_stride, first_col, ws_o, ws_ml, static_cast<TO*>(out)))
+  switch (kd) {
+    case 1: KVQ_LAUNCH_COMBINE(1); break;
+    case 2: KVQ_LAUNCH_COMBINE(2); break;
+    case 3: KVQ_LAUNCH_COMBINE(3); break;
+    default: KVQ_LAUNCH_COMBINE(4); break;
+  }
+#undef KVQ_LAUNCH_COMBINE
   KVQ_LAUNCH_CHECK();
   return KVQ_OK;
 }
@@ -365,19 +446,32 @@ extern "C" int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batc
   float* ws_ml = ws_o + num_work * num_heads * head_size;
   const float qscale = scale * 1.4426950408889634f;  // fold log2(e): exp2 in the kernels
 
-  bool mfma = false;
-  int rc = kvq::launch_kivi_decode_mfma(query, q_dtype, num_heads, num_kv_heads, head_size,
-                                       qscale, k_quant, k_scale, k_mn, v_quant, v_scale, v_mn,
-                                       block_size, group_size, num_blocks, block_table,
-                                       max_blocks, seq_meta,
-                                       work, num_work, ws_o, ws_ml, s, &mfma);
-  if (rc != KVQ_OK) return rc;
+  // tail items (kind 1) on the side stream, int4 items (kind 0) on the
+  // caller's stream; the combine waits for both
+  std::lock_guard<std::mutex> lock(kvq::fork_mutex());
+  kvq::SideStream* side = nullptr;
+  hipError_t he = kvq::side_stream(&side);
+  if (he != hipSuccess) return static_cast<int>(he);
+  if ((he = hipEventRecord(side->fork, s)) != hipSuccess) return static_cast<int>(he);
+  if ((he = hipStreamWaitEvent(side->stream, side->fork, 0)) != hipSuccess)
+    return static_cast<int>(he);
   bool tail = false;
-  rc = kvq::launch_kivi_decode_tail_mfma(query, q_dtype, num_heads, num_kv_heads, head_size,
-                                         qscale, k_quant, k_scale, k_mn, v_quant, v_scale,
-                                         v_mn, block_size, group_size, num_blocks, block_table,
-                                         max_blocks, seq_meta, work, num_work, ring_k, ring_v,
-                                         ring_dtype, ring_len, ws_o, ws_ml, s, &tail);
+  int rc = kvq::launch_kivi_decode_tail_mfma(query, q_dtype, num_heads, num_kv_heads,
+                                             head_size, qscale, k_quant, k_scale, k_mn, v_quant,
+                                             v_scale, v_mn, block_size, group_size, num_blocks,
+                                             block_table, max_blocks, seq_meta, work, num_work,
+                                             ring_k, ring_v, ring_dtype, ring_len, ws_o, ws_ml,
+                                             side->stream, &tail);
+  // the join is recorded whatever happened, so the caller's stream never waits
+  // on a stale fork
+  if ((he = hipEventRecord(side->join, side->stream)) != hipSuccess) return static_cast<int>(he);
+  if (rc != KVQ_OK) return rc;
+  bool mfma = false;
+  rc = kvq::launch_kivi_decode_mfma(query, q_dtype, num_heads, num_kv_heads, head_size,
+                                   qscale, k_quant, k_scale, k_mn, v_quant, v_scale, v_mn,
+                                   block_size, group_size, num_blocks, block_table, max_blocks,
+                                   seq_meta, work, num_work, ws_o, ws_ml, s, &mfma);
+  if ((he = hipStreamWaitEvent(s, side->join, 0)) != hipSuccess) return static_cast<int>(he);
   if (rc != KVQ_OK) return rc;
   if (!mfma || !tail) {
     const dim3 grid(static_cast<unsigned>(num_work), num_kv_heads);
