@@ -656,14 +656,6 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
   return KVQ_OK;
 }
 
-int launch_int8_decode_mfma(const void*, int, int, int, int, float, const int8_t*, const int8_t*,
-                            int, const void*, const void*, const int32_t*, int64_t,
-                            const int32_t*, int64_t, float*, float*, hipStream_t,
-                            bool* launched) {
-  *launched = false;
-  return KVQ_OK;
-}
-
 }  // namespace kvq
 
 extern "C" int kvq_selftest_mfma_f16(const void* a, const void* b, float* d, void* stream) {

@@ -376,7 +376,8 @@ extern "C" int kvq_int8_decode_attn(const void* query, int dtype, int64_t batch,
   const float qscale = scale * 1.4426950408889634f;
   bool mfma = false;
   int rc = kvq::launch_int8_decode_mfma(query, dtype, num_heads, num_kv_heads, head_size, qscale,
-                                       key_cache, value_cache, block_size, k_aq, v_aq,
+                                       key_cache, value_cache, block_size, num_blocks,
+                                       k_aq, v_aq,
                                        block_table, max_blocks, work, num_work, ws_o, ws_ml, s,
                                        &mfma);
   if (rc != KVQ_OK) return rc;

@@ -58,7 +58,8 @@ int launch_kivi_decode_tail_mfma(const void* query, int q_dtype, int hq, int kvh
 
 // INT8 counterpart: kind-0 items (all positions in int8 pages) on MFMA.
 int launch_int8_decode_mfma(const void* query, int dtype, int hq, int kvh, int d, float qscale,
-                            const int8_t* kc, const int8_t* vc, int bs, const void* k_aq,
+                            const int8_t* kc, const int8_t* vc, int bs, int64_t nb,
+                            const void* k_aq,
                             const void* v_aq, const int32_t* block_table, int64_t maxb,
                             const int32_t* work, int64_t num_work, float* ws_o, float* ws_ml,
                             hipStream_t s, bool* launched);

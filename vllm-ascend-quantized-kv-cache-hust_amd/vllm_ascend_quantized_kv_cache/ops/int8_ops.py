@@ -142,6 +142,13 @@ def int8_decode_attention(
     if batch == 0:
         return out
     bt = block_table.to(torch.int32).contiguous()
+    if len(seq_lens) != batch or bt.shape[0] < batch:
+        raise ValueError("int8_decode_attention: seq_lens / block_table rows != batch")
+    if max(seq_lens) > bt.shape[1] * bs or min(seq_lens) < 0:
+        raise ValueError(
+            f"int8_decode_attention: a sequence length exceeds its block table "
+            f"({max(seq_lens)} > {bt.shape[1]} x {bs})"
+        )
     if plan is None:
         if split_tokens is None:
             split_tokens = choose_split_tokens(int(sum(seq_lens)), kvh)
