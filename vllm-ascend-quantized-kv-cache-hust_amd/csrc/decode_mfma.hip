@@ -54,10 +54,28 @@ __device__ __forceinline__ h8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t
   return __builtin_bit_cast(h8, v);
 }
 
-// (hi, lo) fp16 parts of x: hi = fp16(x), lo = fp16(x - hi).
-__device__ __forceinline__ void split_h(float x, _Float16& hi, _Float16& lo) {
-  hi = static_cast<_Float16>(x);
-  lo = static_cast<_Float16>(x - static_cast<float>(hi));
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+// x - (fp16 half of `pair`), exact in fp32: one v_fma_mix_f32 reading the
+// half directly (the compiler would convert and subtract in two steps).
+template <int HALF>
+__device__ __forceinline__ float sub_half(float x, uint32_t pair) {
+  float r;
+  if (HALF == 0)
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(x));
+  else
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=v"(r)
+        : "v"(pair), "v"(x));
+  return r;
+}
+
+// (hi, lo) fp16 pairs of x: hi = fp16(x), lo = fp16(x - hi), both round to
+// nearest; two lanes per v_cvt_pk_f16_f32.
+__device__ __forceinline__ void split_h2(f2 x, uint32_t& hi, uint32_t& lo) {
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
+  const f2 r = f2{sub_half<0>(x[0], hi), sub_half<1>(x[1], hi)};
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, h2));
 }
 
 __device__ __forceinline__ uint32_t h2_bits(_Float16 a, _Float16 b) {
@@ -65,11 +83,9 @@ __device__ __forceinline__ uint32_t h2_bits(_Float16 a, _Float16 b) {
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
 }
 
+// fp16 pair (lo, hi), round to nearest.
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
-  const _Float16 a = static_cast<_Float16>(lo);
-  const _Float16 b = static_cast<_Float16>(hi);
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{lo, hi}), h2));
 }
 
 // Selector putting byte u of `lo` in byte 0 and byte u of `hi` in byte 2.
@@ -316,10 +332,43 @@ struct QRegs<float> {
   __device__ __forceinline__ float hi(int i) const { return w[2 * i + 1]; }
 };
 
+// B operands of one key group: Q' = q * key_scale(dim, group) as hi/lo fp16
+// pairs for the 4 k-steps, and the minima term kb = sum_d q * mn (times the
+// softmax scale).  Shared by the group's tiles (two 64-token tiles at G = 128).
+struct QGroup {
+  h8 bq[4], bl[4];
+  float kb;
+};
+
+template <typename TQ, int CPG>
+__device__ __forceinline__ void prepare_group(const uint32_t* W, int kg, const QRegs<TQ>& qv,
+                                              float qscale, QGroup& qg) {
+#pragma clang fp contract(fast)
+  using T = Tile<CPG>;
+  float kb = 0.0f;
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) {
+    float sc[8], mn[8];
+    read8f(W + T::KS + (s4 * 4 + kg) * 8, sc);
+    read8f(W + T::KM + (s4 * 4 + kg) * 8, mn);
+    uint32_t qh[4], ql[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float q0 = qv.lo(4 * s4 + p);  // exact widening of the input
+      const float q1 = qv.hi(4 * s4 + p);
+      split_h2(f2{q0 * sc[2 * p], q1 * sc[2 * p + 1]}, qh[p], ql[p]);
+      kb += q0 * mn[2 * p] + q1 * mn[2 * p + 1];
+    }
+    qg.bq[s4] = as_h8(qh[0], qh[1], qh[2], qh[3]);
+    qg.bl[s4] = as_h8(ql[0], ql[1], ql[2], ql[3]);
+  }
+  qg.kb = sum_kg(kb) * qscale;
+}
+
 // One tile of scores, softmax update and PV.  FULL: every token < pe.
 template <typename TQ, int CPG, bool FULL>
 __device__ __forceinline__ void compute_tile(const uint32_t* W, int p0, int pe, int n, int kg,
-                                             const QRegs<TQ>& qv, float qscale,
+                                             const QGroup& qg, float qscale,
                                              const LaneNib<CPG>& ln, float& m_run, float& l_run, f4 (&o_acc)[8],
                                              f4 (&c_acc)[16 / CPG], float (&bias_v)[16 / CPG]) {
   // attention math is tolerance-checked: let mul+add fuse here (the library
@@ -329,35 +378,17 @@ __device__ __forceinline__ void compute_tile(const uint32_t* W, int p0, int pe, 
   const int chunk = n % CPG;
   const h8 ones_b = as_h8(kMagic, kMagic, kMagic, kMagic);
   // ---- scores ----------------------------------------------------------------
-  float kb = 0.0f;
   f4 sacc[T::NJ];
 #pragma unroll
   for (int j = 0; j < T::NJ; ++j) sacc[j] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s4 = 0; s4 < 4; ++s4) {
-    float sc[8], mn[8];
-    read8f(W + T::KS + (s4 * 4 + kg) * 8, sc);
-    read8f(W + T::KM + (s4 * 4 + kg) * 8, mn);
     uint32_t w[8];  // dims 32*s4 + 4*ii + kg of chunk `chunk`: pairs 32 words apart
     {
       const uint32_t* kw = W + T::KW + (32 * s4 + kg) * CPG + chunk;
 #pragma unroll
       for (int ii = 0; ii < 8; ++ii) w[ii] = kw[4 * ii * CPG];
     }
-    uint32_t qh[4], ql[4];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const float q0 = qv.lo(4 * s4 + p);  // exact widening of the input
-      const float q1 = qv.hi(4 * s4 + p);
-      _Float16 h0, l0, h1, l1;
-      split_h(q0 * sc[2 * p], h0, l0);
-      split_h(q1 * sc[2 * p + 1], h1, l1);
-      qh[p] = h2_bits(h0, h1);
-      ql[p] = h2_bits(l0, l1);
-      kb += q0 * mn[2 * p] + q1 * mn[2 * p + 1];
-    }
-    const h8 bq = as_h8(qh[0], qh[1], qh[2], qh[3]);
-    const h8 bl = as_h8(ql[0], ql[1], ql[2], ql[3]);
 #pragma unroll
     for (int jm = 0; jm < T::NJ; ++jm) {
       const uint32_t sel = ln.selk[jm];
@@ -365,12 +396,12 @@ __device__ __forceinline__ void compute_tile(const uint32_t* W, int p0, int pe, 
                          nib_pair_exact(w[2], w[3], sel, ln.maskk),
                          nib_pair_exact(w[4], w[5], sel, ln.maskk),
                          nib_pair_exact(w[6], w[7], sel, ln.maskk));
-      sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, sacc[jm], 0, 0, 0);
-      sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, sacc[jm], 0, 0, 0);
+      sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qg.bq[s4], sacc[jm], 0, 0, 0);
+      sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qg.bl[s4], sacc[jm], 0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the k-steps' live ranges apart
   }
-  kb = sum_kg(kb) * qscale;
+  const float kb = qg.kb;
   // softmax scale * log2(e), and 1/16 on the rows read as 16c
   const float rs = qscale * ln.row_scale;
   // lane holds head n, rows m' = 4*kg + r: token tk = tile_token(jm/2, kg, 4*(jm%2) + r)
@@ -541,6 +572,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   };
   issue(lds_raw, pb);  // prologue: tile 0 into buffer 0
   int cur = 0;
+  QGroup qg;
   for (int p0 = pb; p0 < pe; p0 += GT) {
     // prefetch tile p0 + GT into the other buffer, then wait for this tile only
     const int p1 = p0 + GT;
@@ -551,10 +583,13 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
       wait_vmcnt<0>();
     }
     const uint32_t* W = reinterpret_cast<const uint32_t*>(lds_raw + cur * T::BYTES);
+    // tiles are GT-aligned and GT divides g: a tile starts a key group or
+    // continues the previous tile's
+    if (p0 == pb || p0 % g == 0) prepare_group<TQ, CPG>(W, kg, qv, qscale, qg);
     if (p0 + GT <= pe)
-      compute_tile<TQ, CPG, true>(W, p0, pe, n, kg, qv, qscale, ln, m_run, l_run, o_acc, c_acc, bias_v);
+      compute_tile<TQ, CPG, true>(W, p0, pe, n, kg, qg, qscale, ln, m_run, l_run, o_acc, c_acc, bias_v);
     else
-      compute_tile<TQ, CPG, false>(W, p0, pe, n, kg, qv, qscale, ln, m_run, l_run, o_acc, c_acc, bias_v);
+      compute_tile<TQ, CPG, false>(W, p0, pe, n, kg, qg, qscale, ln, m_run, l_run, o_acc, c_acc, bias_v);
     // every LDS read of this buffer has been consumed before the next
     // iteration's DMA may overwrite it
     asm volatile("" ::: "memory");
