@@ -82,6 +82,59 @@ def test_pack_config1_bit_exact(gpu_device):
         assert torch.equal(a.view(torch.int32), b.cpu().view(torch.int32))
 
 
+def _boundary_values(shape, group_axis_len, seed):
+    """fp32 values whose KIVI quotients sit on the x.5 rounding boundaries.
+
+    Every group of ``group_axis_len`` entries along the last axis holds its
+    min, its max = min + 15 s, and entries min + (k + 0.5) s nudged by -1, 0
+    or +1 ulp, so (x - mn) / scale + 0.5 falls within a few ulps of an integer
+    (the cases the reciprocal fast path hands to the exact division).
+    """
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    x = np.empty(shape, dtype=np.float32)
+    flat = x.reshape(-1, group_axis_len)
+    for row in flat:
+        mn = np.float32(rng.normal())
+        s = np.float32(np.exp(rng.normal()) * 0.1)
+        k = rng.integers(0, 15, group_axis_len).astype(np.float32)
+        v = (mn + (k + np.float32(0.5)) * s).astype(np.float32)
+        nudge = rng.integers(-1, 2, group_axis_len)
+        v = np.where(nudge < 0, np.nextafter(v, np.float32(-np.inf)), v)
+        v = np.where(nudge > 0, np.nextafter(v, np.float32(np.inf)), v).astype(np.float32)
+        v[0] = mn
+        v[-1] = np.float32(mn + np.float32(15) * s)
+        row[:] = v
+    return torch.from_numpy(x)
+
+
+@pytest.mark.parametrize("d,kvh,g,bs", [(128, 8, 128, 128), (128, 4, 32, 64), (64, 2, 16, 32)])
+def test_pack_boundary_quotients_bit_exact(gpu_device, d, kvh, g, bs):
+    from vllm_ascend_quantized_kv_cache.ops.kivi_pack import (
+        kivi_pack_key_cache,
+        kivi_pack_value_cache,
+    )
+
+    n_groups = 4
+    t = n_groups * g
+    nb = t // bs + 2
+    # keys group over tokens: build [kvh, d, t] and move tokens first
+    key = _boundary_values((kvh, d, t), g, seed=d + g).permute(2, 0, 1).contiguous()
+    value = _boundary_values((t, kvh, d), g, seed=d + g + 1)
+    table = torch.randperm(nb, generator=torch.Generator().manual_seed(g)).to(torch.int32)
+    slots = slots_for(table, range(t), bs)
+    cpu = empty_kivi_caches(nb, bs, kvh, d, g)
+    gpu = to_dev(cpu, gpu_device)
+    ref.pack_key_cache(key, slots, *cpu[:3], g)
+    ref.pack_value_cache(value, slots, *cpu[3:], g)
+    kivi_pack_key_cache(key.to(gpu_device), slots.to(gpu_device), *gpu[:3], g)
+    kivi_pack_value_cache(value.to(gpu_device), slots.to(gpu_device), *gpu[3:], g)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("kq", "ks", "km", "vq", "vs", "vm"), cpu, gpu):
+        assert torch.equal(a.view(torch.int32), b.cpu().view(torch.int32)), f"{name} differs"
+
+
 @pytest.mark.parametrize("d,kvh,g,bs", GEOMS)
 def test_gather_bit_exact(gpu_device, d, kvh, g, bs):
     from vllm_ascend_quantized_kv_cache.ops.kivi_gather import kivi_dequant_gather_cache

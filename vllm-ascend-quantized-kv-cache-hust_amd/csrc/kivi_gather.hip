@@ -138,8 +138,9 @@ kivi_gather_kernel(const int32_t* __restrict__ kq, const float* __restrict__ ks,
         const int gi = (w * 8) / g;
         const float sc = vs[vrow * ng + gi];
         const float mn = vm[vrow * ng + gi];
+        nibbles_f32(word, x);
 #pragma unroll
-        for (int l = 0; l < 8; ++l) x[l] = kivi_dequant((word >> (4 * l)) & 0xfu, sc, mn);
+        for (int l = 0; l < 8; ++l) x[l] = __fadd_rn(__fmul_rn(x[l], sc), mn);
       }
       store8(out_v + (row0 + p) * hd + h * d + w * 8, x);
     }

@@ -13,6 +13,8 @@
 //   One thread per output word (8 consecutive dims of one token-head row,
 //   a 16-byte load).  The head-dim group's min/max is a butterfly over the
 //   group's G/8 adjacent lanes (DPP/swizzle through __shfl_xor).
+#include <mutex>
+
 #include "kvq_common.h"
 
 namespace {
@@ -97,12 +99,10 @@ kivi_pack_key_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __restri
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int c = dv * 8 + j;
-      const float sc = s_scale[c];
-      const float mn = s_min[c];
-      uint32_t word = 0;
+      float col[8];
 #pragma unroll
-      for (int l = 0; l < 8; ++l) word |= kivi_quantize(x[l][j], mn, sc) << (4 * l);
-      s_words[c * nchunk + tc] = word;
+      for (int l = 0; l < 8; ++l) col[l] = x[l][j];
+      s_words[c * nchunk + tc] = kivi_pack_word(col, s_min[c], s_scale[c]);
     }
   }
   __syncthreads();
@@ -175,9 +175,7 @@ kivi_pack_value_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __rest
   const int64_t slot = ld_index(slots, t);
   if (slot < 0) return;
   const float sc = kivi_group_scale(mn, mx);
-  uint32_t word = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) word |= kivi_quantize(x[i], mn, sc) << (4 * i);
+  const uint32_t word = kivi_pack_word(x, mn, sc);
   const int64_t blk = slot / bs;
   const int64_t off = slot - blk * bs;
   const int64_t orow = (blk * bs + off) * kvh + h;
@@ -208,6 +206,249 @@ ring_write_kernel(const TS* __restrict__ src, const int64_t* __restrict__ src_ro
   store8(ring + dst_rows[i] * row_elems + c, x);
 }
 
+// ---- wave-pipelined pack kernels --------------------------------------------
+// Both walk their work in single-wave items with a register double buffer: the
+// next item's source rows are in flight while the current one is reduced,
+// quantized and stored, so the loads of one item overlap the arithmetic of the
+// previous one instead of every wave of the chip loading, then computing, then
+// storing in lockstep.
+
+// Key pack: item = (key group, kv head, slice of 8 * DV dims), DV = 64 / NCH.
+// Lane (tc, dv) holds tokens 8*tc .. 8*tc + 7 of the group for dims
+// 8*(slice*DV + dv) .. + 7; the group min/max per dim is a butterfly over the
+// NCH chunk lanes (lane bits above DV), so no LDS and no barrier.  Each lane
+// then writes its 8 words (one per dim, its 8 tokens) and, in chunk 0, the
+// 8 scales and mins.
+template <typename T, typename I, int NCH>
+__global__ void __launch_bounds__(64)
+kivi_pack_key_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __restrict__ src_b,
+                          const int64_t* __restrict__ src_index, const I* __restrict__ slots,
+                          int kvh, int d, int g, int bs, int slices, int64_t items,
+                          int32_t* __restrict__ kq, float* __restrict__ ks,
+                          float* __restrict__ km) {
+  constexpr int DV = 64 / NCH;
+  const int lane = threadIdx.x;
+  const int tc = lane / DV;
+  const int dv = lane % DV;
+  const int64_t nw = gridDim.x;
+  const int64_t row_elems = static_cast<int64_t>(kvh) * d;
+  const int wpd = bs / 8;
+  const int gpb = bs / g;
+
+  struct Item {
+    int64_t grp;
+    int h, dim0;
+    bool active;
+  };
+  auto decode = [&](int64_t item) {
+    Item it;
+    const int64_t hg = item / slices;
+    const int slice = static_cast<int>(item - hg * slices);
+    it.grp = hg / kvh;
+    it.h = static_cast<int>(hg - it.grp * kvh);
+    it.dim0 = (slice * DV + dv) * 8;
+    it.active = it.dim0 < d;
+    if (!it.active) it.dim0 = d - 8;  // idle lanes read a valid column
+    return it;
+  };
+  auto load = [&](Raw8<T> (&r)[8], int64_t item) {
+    const Item it = decode(item);
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const int64_t t = it.grp * g + tc * 8 + l;
+      const int64_t row = src_index ? src_index[t] : t;
+      r[l].load(src_row(src_a, n_a, src_b, row, row_elems) + it.h * d + it.dim0);
+    }
+  };
+  auto compute = [&](const Raw8<T> (&r)[8], int64_t item) {
+    const Item it = decode(item);
+    const int64_t first = ld_index(slots, it.grp * g);
+    if (first < 0) return;  // uniform: padding groups are skipped
+    const int64_t blk = first / bs;
+    const int off = static_cast<int>(first - blk * bs);
+    // widened from the raw registers where used (keeps 64 fp32 copies out of
+    // the register file)
+    float mn[8], mx[8];
+    {
+      float x[8];
+      r[0].get(x);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mn[j] = mx[j] = x[j];
+#pragma unroll
+      for (int l = 1; l < 8; ++l) {
+        r[l].get(x);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          mn[j] = fminf(mn[j], x[j]);
+          mx[j] = fmaxf(mx[j], x[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (DV <= 1) { mn[j] = fminf(mn[j], lane_xor<1>(mn[j])); mx[j] = fmaxf(mx[j], lane_xor<1>(mx[j])); }
+      if (DV <= 2) { mn[j] = fminf(mn[j], lane_xor<2>(mn[j])); mx[j] = fmaxf(mx[j], lane_xor<2>(mx[j])); }
+      if (DV <= 4) { mn[j] = fminf(mn[j], lane_xor<4>(mn[j])); mx[j] = fmaxf(mx[j], lane_xor<4>(mx[j])); }
+      if (DV <= 8) { mn[j] = fminf(mn[j], lane_xor<8>(mn[j])); mx[j] = fmaxf(mx[j], lane_xor<8>(mx[j])); }
+      if (DV <= 16) { mn[j] = fminf(mn[j], lane_xor<16>(mn[j])); mx[j] = fmaxf(mx[j], lane_xor<16>(mx[j])); }
+      if (DV <= 32) { mn[j] = fminf(mn[j], lane_xor<32>(mn[j])); mx[j] = fmaxf(mx[j], lane_xor<32>(mx[j])); }
+    }
+    if (!it.active) return;
+    const int64_t row_base = (blk * kvh + it.h) * static_cast<int64_t>(d) + it.dim0;
+    uint32_t* out = reinterpret_cast<uint32_t*>(kq);
+    float x[8][8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) r[l].get(x[l]);
+    float sc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sc[j] = kivi_group_scale(mn[j], mx[j]);
+      float col[8];
+#pragma unroll
+      for (int l = 0; l < 8; ++l) col[l] = x[l][j];
+      out[(row_base + j) * wpd + off / 8 + tc] = kivi_pack_word(col, mn[j], sc[j]);
+      if (tc == 0) {
+        const int64_t sidx = (row_base + j) * gpb + off / g;
+        ks[sidx] = sc[j];
+        km[sidx] = mn[j];
+      }
+    }
+  };
+
+  Raw8<T> ra[8], rb[8];
+  int64_t item = blockIdx.x;
+  if (item < items) load(ra, item);
+  for (; item < items; item += 2 * nw) {
+    if (item + nw < items) load(rb, item + nw);
+    compute(ra, item);
+    if (item + nw >= items) break;
+    if (item + 2 * nw < items) load(ra, item + 2 * nw);
+    compute(rb, item + nw);
+  }
+}
+
+// Value pack: the flat (token-head row, word) index space in units of one
+// wave (64 lanes = 64 / WPR rows, WPR = head_size / 8 words per row).  Each
+// wave takes U consecutive units per step and keeps the next step's U units
+// in flight; the head-dim group min/max is a butterfly over its g / 8 adjacent
+// lanes.  row -> token goes through a host-built FastDiv (no 64-bit division).
+template <typename T, typename I, int WPR>
+__global__ void __launch_bounds__(256)
+kivi_pack_value_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __restrict__ src_b,
+                            const int64_t* __restrict__ src_index, const I* __restrict__ slots,
+                            int32_t rows, FastDiv kvh_div, int g, int bs,
+                            int32_t* __restrict__ vq, float* __restrict__ vs,
+                            float* __restrict__ vm) {
+  constexpr int RPU = 64 / WPR;  // rows per unit
+  constexpr int U = 4;           // units per step
+  constexpr int D = 8 * WPR;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6);
+  const int64_t nw = static_cast<int64_t>(gridDim.x) * (blockDim.x / 64);
+  const int kvh = static_cast<int>(kvh_div.d);
+  const int gw = g / 8;
+  const int ng = D / g;
+  const int w = lane % WPR;
+  const int64_t row_elems = static_cast<int64_t>(kvh) * D;
+  const int64_t units = (static_cast<int64_t>(rows) + RPU - 1) / RPU;
+
+  struct Buf {
+    Raw8<T> x[U];
+    int64_t slot[U];
+  };
+  auto load = [&](Buf& b, int64_t u0) {
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      int32_t r = static_cast<int32_t>((u0 + k) * RPU) + lane / WPR;
+      r = r < rows ? r : rows - 1;  // rows past the end read the last row, store nothing
+      const uint32_t t = kvh_div.div(static_cast<uint32_t>(r));
+      if (src_index) {
+        const int h = r - static_cast<int32_t>(t) * kvh;
+        b.x[k].load(src_row(src_a, n_a, src_b, src_index[t], row_elems) + h * D + w * 8);
+      } else {
+        // rows of src_a are the (token, head) rows in order: row r starts at r * D
+        b.x[k].load(src_a + static_cast<int64_t>(r) * D + w * 8);
+      }
+      b.slot[k] = ld_index(slots, static_cast<int64_t>(t));
+    }
+  };
+  auto compute = [&](const Buf& b, int64_t u0) {
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int64_t r = (u0 + k) * RPU + lane / WPR;
+      float x[8];
+      b.x[k].get(x);
+      float mn = x[0], mx = x[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) {
+        mn = fminf(mn, x[i]);
+        mx = fmaxf(mx, x[i]);
+      }
+      // butterfly over the group's gw lanes: every step runs, steps at or past
+      // gw keep the lane's value (a uniform select, no branch)
+#define KVQ_GROUP_STEP(O)                                               \
+      {                                                                 \
+        const float pn = fminf(mn, lane_xor<O>(mn));                    \
+        const float px = fmaxf(mx, lane_xor<O>(mx));                    \
+        mn = gw > O ? pn : mn;                                          \
+        mx = gw > O ? px : mx;                                          \
+      }
+      if (WPR > 1) KVQ_GROUP_STEP(1)
+      if (WPR > 2) KVQ_GROUP_STEP(2)
+      if (WPR > 4) KVQ_GROUP_STEP(4)
+      if (WPR > 8) KVQ_GROUP_STEP(8)
+      if (WPR > 16) KVQ_GROUP_STEP(16)
+      if (WPR > 32) KVQ_GROUP_STEP(32)
+#undef KVQ_GROUP_STEP
+      const int64_t slot = b.slot[k];
+      if (r >= rows || slot < 0) continue;
+      const float sc = kivi_group_scale(mn, mx);
+      const uint32_t word = kivi_pack_word(x, mn, sc);
+      const uint32_t t = kvh_div.div(static_cast<uint32_t>(r));
+      const int h = static_cast<int>(r) - static_cast<int>(t) * kvh;
+      const int64_t orow = slot * kvh + h;  // page row (blk * bs + off) of head h
+      reinterpret_cast<uint32_t*>(vq)[orow * WPR + w] = word;
+      if (w % gw == 0) {
+        const int64_t sidx = orow * ng + w / gw;
+        vs[sidx] = sc;
+        vm[sidx] = mn;
+      }
+    }
+  };
+
+  Buf ba, bb;
+  int64_t u = wave * U;
+  const int64_t step = nw * U;
+  if (u < units) load(ba, u);
+  for (; u < units; u += 2 * step) {
+    if (u + step < units) load(bb, u + step);
+    compute(ba, u);
+    if (u + step >= units) break;
+    if (u + 2 * step < units) load(ba, u + 2 * step);
+    compute(bb, u + step);
+  }
+}
+
+// Workgroups of `kernel` that fit the device at once (CUs x occupancy),
+// cached per kernel and device; 0 on error.
+template <typename K>
+int64_t resident_blocks(K* kernel, int threads) {
+  static std::mutex mu;
+  static int64_t cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] == 0) {
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void*>(kernel),
+                                                     threads, 0) != hipSuccess)
+      return 0;
+    cache[dev] = static_cast<int64_t>(cus) * (per > 0 ? per : 1);
+  }
+  return cache[dev];
+}
+
 bool kivi_geometry_ok(int kvh, int d, int g, int bs) {
   return kvh > 0 && d > 0 && g > 0 && bs > 0 && g % 8 == 0 && d % 8 == 0 && d % g == 0 &&
          bs % g == 0;
@@ -230,13 +471,44 @@ extern "C" int kvq_kivi_pack_key(const void* src_a, int64_t n_a, const void* src
     return KVQ_ERR_GEOMETRY;
   if (num_tokens % group_size) return KVQ_ERR_INVALID;
   if (!src_index && n_a < num_tokens) return KVQ_ERR_INVALID;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nch = group_size / 8;
+  if (nch <= 64 && (nch & (nch - 1)) == 0) {
+    // wave-pipelined kernel: items of (group, head, 8 * (64 / nch) dims)
+    const int span = 8 * (64 / nch);
+    const int slices = (head_size + span - 1) / span;
+    const int64_t items = (num_tokens / group_size) * num_kv_heads * slices;
+#define KVQ_LAUNCH_KEY_WAVE(NCH)                                                              \
+    KVQ_DISPATCH_FLOAT(src_dtype, T,                                                        \
+      KVQ_DISPATCH_INDEX(slot_index_type, I,                                                \
+        const int64_t fit = resident_blocks(kivi_pack_key_wave_kernel<T, I, NCH>, 64);      \
+        if (fit <= 0) return KVQ_ERR_INVALID;                                               \
+        const int64_t waves = items < fit ? items : fit;                                    \
+        hipLaunchKernelGGL((kivi_pack_key_wave_kernel<T, I, NCH>),                          \
+                           dim3(static_cast<unsigned>(waves)), dim3(64), 0, s,               \
+                           static_cast<const T*>(src_a), n_a, static_cast<const T*>(src_b),  \
+                           src_index, static_cast<const I*>(slot_mapping), num_kv_heads,     \
+                           head_size, group_size, block_size, slices, items, k_quant,        \
+                           k_scale, k_mn)))
+    switch (nch) {
+      case 1: KVQ_LAUNCH_KEY_WAVE(1); break;
+      case 2: KVQ_LAUNCH_KEY_WAVE(2); break;
+      case 4: KVQ_LAUNCH_KEY_WAVE(4); break;
+      case 8: KVQ_LAUNCH_KEY_WAVE(8); break;
+      case 16: KVQ_LAUNCH_KEY_WAVE(16); break;
+      case 32: KVQ_LAUNCH_KEY_WAVE(32); break;
+      default: KVQ_LAUNCH_KEY_WAVE(64); break;
+    }
+#undef KVQ_LAUNCH_KEY_WAVE
+    KVQ_LAUNCH_CHECK();
+    return KVQ_OK;
+  }
   const int tiles = (group_size / 8) * (head_size / 8);
   if (tiles > 1024) return KVQ_ERR_GEOMETRY;
   const int threads = ((tiles + 63) / 64) * 64;
   const size_t lds = sizeof(float) * (3 * (group_size / 8) * head_size + 2 * head_size);
   if (lds > 160 * 1024) return KVQ_ERR_GEOMETRY;
   const dim3 grid(static_cast<unsigned>(num_tokens / group_size), num_kv_heads);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   KVQ_DISPATCH_FLOAT(src_dtype, T,
     KVQ_DISPATCH_INDEX(slot_index_type, I,
       hipLaunchKernelGGL((kivi_pack_key_kernel<T, I>), grid, dim3(threads), lds, s,
@@ -259,11 +531,45 @@ extern "C" int kvq_kivi_pack_value(const void* src_a, int64_t n_a, const void* s
   if (!kivi_geometry_ok(num_kv_heads, head_size, group_size, block_size))
     return KVQ_ERR_GEOMETRY;
   if (!src_index && n_a < num_tokens) return KVQ_ERR_INVALID;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int wpr = head_size / 8;
+  const int gw = group_size / 8;
+  const int64_t rows = num_tokens * num_kv_heads;
+  if (64 % wpr == 0 && (gw & (gw - 1)) == 0 && rows < 0x7fffffff) {
+    // wave-pipelined kernel over units of 64 / wpr rows, 4 units per step
+    const int64_t units = (rows + (64 / wpr) - 1) / (64 / wpr);
+    const int64_t steps = (units + 3) / 4;
+    const int64_t want = (steps + 3) / 4;  // workgroups of 4 waves, one step each
+    const FastDiv kdiv = FastDiv::make(static_cast<uint32_t>(num_kv_heads));
+#define KVQ_LAUNCH_VALUE_WAVE(WPR)                                                            \
+    KVQ_DISPATCH_FLOAT(src_dtype, T,                                                        \
+      KVQ_DISPATCH_INDEX(slot_index_type, I,                                                \
+        const int64_t fit = resident_blocks(kivi_pack_value_wave_kernel<T, I, WPR>, 256);   \
+        if (fit <= 0) return KVQ_ERR_INVALID;                                               \
+        const int64_t blocks = want < fit ? want : fit;                                     \
+        hipLaunchKernelGGL((kivi_pack_value_wave_kernel<T, I, WPR>),                        \
+                           dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s,             \
+                           static_cast<const T*>(src_a), n_a, static_cast<const T*>(src_b),  \
+                           src_index, static_cast<const I*>(slot_mapping),                   \
+                           static_cast<int32_t>(rows), kdiv, group_size, block_size,         \
+                           v_quant, v_scale, v_mn)))
+    switch (wpr) {
+      case 1: KVQ_LAUNCH_VALUE_WAVE(1); break;
+      case 2: KVQ_LAUNCH_VALUE_WAVE(2); break;
+      case 4: KVQ_LAUNCH_VALUE_WAVE(4); break;
+      case 8: KVQ_LAUNCH_VALUE_WAVE(8); break;
+      case 16: KVQ_LAUNCH_VALUE_WAVE(16); break;
+      case 32: KVQ_LAUNCH_VALUE_WAVE(32); break;
+      default: KVQ_LAUNCH_VALUE_WAVE(64); break;
+    }
+#undef KVQ_LAUNCH_VALUE_WAVE
+    KVQ_LAUNCH_CHECK();
+    return KVQ_OK;
+  }
   const int64_t total = num_tokens * num_kv_heads * (head_size / 8);
   const int threads = 256;
   const int64_t blocks = (total + threads - 1) / threads;
   if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   KVQ_DISPATCH_FLOAT(src_dtype, T,
     KVQ_DISPATCH_INDEX(slot_index_type, I,
       hipLaunchKernelGGL((kivi_pack_value_kernel<T, I>), dim3(static_cast<unsigned>(blocks)),

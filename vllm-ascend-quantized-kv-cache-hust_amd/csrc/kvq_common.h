@@ -75,12 +75,19 @@ __device__ __forceinline__ void store8(float* p, const float (&x)[8]) {
   *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
   *reinterpret_cast<float4*>(p + 4) = make_float4(x[4], x[5], x[6], x[7]);
 }
+// bf16 pairs through v_cvt_pk_bf16_f32 (round to nearest even, the same bits
+// as f32_to_bf16_bits for every non-NaN input).
+__device__ __forceinline__ uint32_t bf16x2_bits(float lo, float hi) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2v __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v{lo, hi}), b2v));
+}
 __device__ __forceinline__ void store8(bf16* p, const float (&x)[8]) {
   uint4 v;
-  v.x = f32_to_bf16_bits(x[0]) | (static_cast<uint32_t>(f32_to_bf16_bits(x[1])) << 16);
-  v.y = f32_to_bf16_bits(x[2]) | (static_cast<uint32_t>(f32_to_bf16_bits(x[3])) << 16);
-  v.z = f32_to_bf16_bits(x[4]) | (static_cast<uint32_t>(f32_to_bf16_bits(x[5])) << 16);
-  v.w = f32_to_bf16_bits(x[6]) | (static_cast<uint32_t>(f32_to_bf16_bits(x[7])) << 16);
+  v.x = bf16x2_bits(x[0], x[1]);
+  v.y = bf16x2_bits(x[2], x[3]);
+  v.z = bf16x2_bits(x[4], x[5]);
+  v.w = bf16x2_bits(x[6], x[7]);
   *reinterpret_cast<uint4*>(p) = v;
 }
 __device__ __forceinline__ void store8(f16* p, const float (&x)[8]) {
@@ -107,6 +114,60 @@ __device__ __forceinline__ uint32_t kivi_quantize(float x, float mn, float scale
   return static_cast<uint32_t>(t);
 }
 
+// One packed word (8 codes, code i at bits 4i) with the codes of
+// kivi_quantize but no division per element.  With d = x - mn (rounded as
+// there) and rcp = v_rcp_f32(scale) (1 ulp), v = d * rcp lies within 3e-6 of
+// d / scale for quotients below 16 (2^-23 * 16 from rcp, half an ulp of 16 from
+// the product), and the reference's floor(RN(RN(d / scale) + 0.5)) sits
+// within another 2e-6 of floor(d / scale + 0.5).  So rndne(v) -- which
+// differs from rounding half up only at a tie -- is the reference's code
+// whenever v is more than 1e-5 away from k + 0.5 (codes from 16 up clamp to
+// 15 on both sides).  A word holding a v within 1e-5 of a tie (about 2e-5 of
+// the elements) is redone with the exact division.
+__device__ __forceinline__ uint32_t kivi_pack_word(const float (&x)[8], float mn, float scale) {
+  const float rcp = __builtin_amdgcn_rcpf(scale);
+  uint32_t word = 0;
+  float worst = 0.0f;  // max |v - rndne(v)|: 0.5 at a tie
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float v = (x[i] - mn) * rcp;
+    const float r = __builtin_rintf(v);
+    worst = fmaxf(worst, fabsf(v - r));
+    word |= static_cast<uint32_t>(fminf(r, 15.0f)) << (4 * i);
+  }
+  if (!(worst <= 0.49999f)) {
+    word = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) word |= kivi_quantize(x[i], mn, scale) << (4 * i);
+  }
+  return word;
+}
+
+// The 8 nibbles of a packed word as floats (nibble i -> c[i]): one mask per
+// parity, then v_cvt_f32_ubyte{0..3} on each byte (the compiler would
+// extract every nibble on its own).
+template <int B>
+__device__ __forceinline__ float ubyte_f32(uint32_t v) {
+  float r;
+  if (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+  if (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+  if (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+  if (B == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+__device__ __forceinline__ void nibbles_f32(uint32_t w, float (&c)[8]) {
+  const uint32_t ev = w & 0x0f0f0f0fu;         // nibbles 0, 2, 4, 6 in bytes 0..3
+  const uint32_t od = (w >> 4) & 0x0f0f0f0fu;  // nibbles 1, 3, 5, 7
+  c[0] = ubyte_f32<0>(ev);
+  c[1] = ubyte_f32<0>(od);
+  c[2] = ubyte_f32<1>(ev);
+  c[3] = ubyte_f32<1>(od);
+  c[4] = ubyte_f32<2>(ev);
+  c[5] = ubyte_f32<2>(od);
+  c[6] = ubyte_f32<3>(ev);
+  c[7] = ubyte_f32<3>(od);
+}
+
 // KIVI dequant: q * scale, then + mn, as two separate fp32 roundings.
 __device__ __forceinline__ float kivi_dequant(uint32_t q, float scale, float mn) {
   return __fadd_rn(__fmul_rn(static_cast<float>(q), scale), mn);
@@ -119,6 +180,81 @@ template <typename I>
 __device__ __forceinline__ int64_t ld_index(const I* p, int64_t i) {
   return static_cast<int64_t>(p[i]);
 }
+
+// Value of lane (lane ^ MASK) in the wave: DPP quad permutes for masks 1 and
+// 2, ds_swizzle's xor mode inside 32-lane halves, ds_bpermute across them.
+template <int MASK>
+__device__ __forceinline__ float lane_xor(float v) {
+  static_assert(MASK > 0 && MASK < 64 && (MASK & (MASK - 1)) == 0, "power-of-two mask");
+  const int b = __float_as_int(v);
+  int r;
+  if (MASK == 1)
+    r = __builtin_amdgcn_update_dpp(b, b, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  else if (MASK == 2)
+    r = __builtin_amdgcn_update_dpp(b, b, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  else if (MASK < 32)
+    r = __builtin_amdgcn_ds_swizzle(b, (MASK << 10) | 0x1F);  // and 0x1f, or 0, xor MASK
+  else
+    r = __builtin_amdgcn_ds_bpermute(static_cast<int>((threadIdx.x ^ MASK) & 63) << 2, b);
+  return __int_as_float(r);
+}
+
+// Division by a launch constant d >= 1 for 0 <= n < 2^31 (Granlund-Montgomery):
+// n / d = (umulhi(n, m) + n) >> s with s = ceil(log2 d) and
+// m = floor(2^32 (2^s - d) / d) + 1, computed on the host.
+struct FastDiv {
+  uint32_t d, m, s;
+  static FastDiv make(uint32_t d) {
+    uint32_t s = 0;
+    while ((1ull << s) < d) ++s;
+    const uint64_t m = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
+    return FastDiv{d, static_cast<uint32_t>(m), s};
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    return (__umulhi(n, m) + n) >> s;
+  }
+};
+
+// Eight consecutive elements kept in their storage type (loaded early, widened
+// to fp32 when used).
+template <typename T>
+struct Raw8;
+template <>
+struct Raw8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const float4*>(p);
+    b = *reinterpret_cast<const float4*>(p + 4);
+  }
+  __device__ __forceinline__ void get(float (&x)[8]) const {
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  }
+};
+template <>
+struct Raw8<bf16> {
+  uint4 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ void get(float (&x)[8]) const {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+};
+template <>
+struct Raw8<f16> {
+  uint4 v;
+  __device__ __forceinline__ void load(const f16* p) { v = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ void get(float (&x)[8]) const {
+    typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+    const h8v h = __builtin_bit_cast(h8v, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(h[i]);
+  }
+};
 
 }  // namespace kvq
 
