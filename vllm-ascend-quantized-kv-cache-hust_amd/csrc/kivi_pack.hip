@@ -10,9 +10,15 @@
 //   as [dim][chunk] and written back in address order.
 //
 // Value pack (reference: pkg/ops/triton/kivi_pack.py:61-131)
-//   One thread per output word (8 consecutive dims of one token-head row,
-//   a 16-byte load).  The head-dim group's min/max is a butterfly over the
-//   group's G/8 adjacent lanes (DPP/swizzle through __shfl_xor).
+//   One lane per output word (8 consecutive dims of one token-head row, a
+//   16-byte load); waves walk units of 64 lanes, four at a time with the next
+//   four in flight.  The head-dim group's min/max is a butterfly over the
+//   group's G/8 adjacent lanes (DPP quad permutes and ds_swizzle).  Head sizes
+//   whose rows do not tile a wave keep the one-thread-per-word kernel.
+//
+// Both quantize with kivi_pack_word: a reciprocal per group and a
+// round-to-nearest per element, falling back to the exact division for the
+// rare word with a quotient at a rounding tie, so codes stay bit-exact.
 #include <mutex>
 
 #include "kvq_common.h"
@@ -206,126 +212,11 @@ ring_write_kernel(const TS* __restrict__ src, const int64_t* __restrict__ src_ro
   store8(ring + dst_rows[i] * row_elems + c, x);
 }
 
-// ---- wave-pipelined pack kernels --------------------------------------------
-// Both walk their work in single-wave items with a register double buffer: the
-// next item's source rows are in flight while the current one is reduced,
-// quantized and stored, so the loads of one item overlap the arithmetic of the
-// previous one instead of every wave of the chip loading, then computing, then
-// storing in lockstep.
-
-// Key pack: item = (key group, kv head, slice of 8 * DV dims), DV = 64 / NCH.
-// Lane (tc, dv) holds tokens 8*tc .. 8*tc + 7 of the group for dims
-// 8*(slice*DV + dv) .. + 7; the group min/max per dim is a butterfly over the
-// NCH chunk lanes (lane bits above DV), so no LDS and no barrier.  Each lane
-// then writes its 8 words (one per dim, its 8 tokens) and, in chunk 0, the
-// 8 scales and mins.
-template <typename T, typename I, int NCH>
-__global__ void __launch_bounds__(64)
-kivi_pack_key_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __restrict__ src_b,
-                          const int64_t* __restrict__ src_index, const I* __restrict__ slots,
-                          int kvh, int d, int g, int bs, int slices, int64_t items,
-                          int32_t* __restrict__ kq, float* __restrict__ ks,
-                          float* __restrict__ km) {
-  constexpr int DV = 64 / NCH;
-  const int lane = threadIdx.x;
-  const int tc = lane / DV;
-  const int dv = lane % DV;
-  const int64_t nw = gridDim.x;
-  const int64_t row_elems = static_cast<int64_t>(kvh) * d;
-  const int wpd = bs / 8;
-  const int gpb = bs / g;
-
-  struct Item {
-    int64_t grp;
-    int h, dim0;
-    bool active;
-  };
-  auto decode = [&](int64_t item) {
-    Item it;
-    const int64_t hg = item / slices;
-    const int slice = static_cast<int>(item - hg * slices);
-    it.grp = hg / kvh;
-    it.h = static_cast<int>(hg - it.grp * kvh);
-    it.dim0 = (slice * DV + dv) * 8;
-    it.active = it.dim0 < d;
-    if (!it.active) it.dim0 = d - 8;  // idle lanes read a valid column
-    return it;
-  };
-  auto load = [&](Raw8<T> (&r)[8], int64_t item) {
-    const Item it = decode(item);
-#pragma unroll
-    for (int l = 0; l < 8; ++l) {
-      const int64_t t = it.grp * g + tc * 8 + l;
-      const int64_t row = src_index ? src_index[t] : t;
-      r[l].load(src_row(src_a, n_a, src_b, row, row_elems) + it.h * d + it.dim0);
-    }
-  };
-  auto compute = [&](const Raw8<T> (&r)[8], int64_t item) {
-    const Item it = decode(item);
-    const int64_t first = ld_index(slots, it.grp * g);
-    if (first < 0) return;  // uniform: padding groups are skipped
-    const int64_t blk = first / bs;
-    const int off = static_cast<int>(first - blk * bs);
-    // widened from the raw registers where used (keeps 64 fp32 copies out of
-    // the register file)
-    float mn[8], mx[8];
-    {
-      float x[8];
-      r[0].get(x);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) mn[j] = mx[j] = x[j];
-#pragma unroll
-      for (int l = 1; l < 8; ++l) {
-        r[l].get(x);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          mn[j] = fminf(mn[j], x[j]);
-          mx[j] = fmaxf(mx[j], x[j]);
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (DV <= 1) { mn[j] = fminf(mn[j], lane_xor<1>(mn[j])); mx[j] = fmaxf(mx[j], lane_xor<1>(mx[j])); }
-      if (DV <= 2) { mn[j] = fminf(mn[j], lane_xor<2>(mn[j])); mx[j] = fmaxf(mx[j], lane_xor<2>(mx[j])); }
-      if (DV <= 4) { mn[j] = fminf(mn[j], lane_xor<4>(mn[j])); mx[j] = fmaxf(mx[j], lane_xor<4>(mx[j])); }
-      if (DV <= 8) { mn[j] = fminf(mn[j], lane_xor<8>(mn[j])); mx[j] = fmaxf(mx[j], lane_xor<8>(mx[j])); }
-      if (DV <= 16) { mn[j] = fminf(mn[j], lane_xor<16>(mn[j])); mx[j] = fmaxf(mx[j], lane_xor<16>(mx[j])); }
-      if (DV <= 32) { mn[j] = fminf(mn[j], lane_xor<32>(mn[j])); mx[j] = fmaxf(mx[j], lane_xor<32>(mx[j])); }
-    }
-    if (!it.active) return;
-    const int64_t row_base = (blk * kvh + it.h) * static_cast<int64_t>(d) + it.dim0;
-    uint32_t* out = reinterpret_cast<uint32_t*>(kq);
-    float x[8][8];
-#pragma unroll
-    for (int l = 0; l < 8; ++l) r[l].get(x[l]);
-    float sc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      sc[j] = kivi_group_scale(mn[j], mx[j]);
-      float col[8];
-#pragma unroll
-      for (int l = 0; l < 8; ++l) col[l] = x[l][j];
-      out[(row_base + j) * wpd + off / 8 + tc] = kivi_pack_word(col, mn[j], sc[j]);
-      if (tc == 0) {
-        const int64_t sidx = (row_base + j) * gpb + off / g;
-        ks[sidx] = sc[j];
-        km[sidx] = mn[j];
-      }
-    }
-  };
-
-  Raw8<T> ra[8], rb[8];
-  int64_t item = blockIdx.x;
-  if (item < items) load(ra, item);
-  for (; item < items; item += 2 * nw) {
-    if (item + nw < items) load(rb, item + nw);
-    compute(ra, item);
-    if (item + nw >= items) break;
-    if (item + 2 * nw < items) load(ra, item + 2 * nw);
-    compute(rb, item + nw);
-  }
-}
+// ---- wave-pipelined value pack ---------------------------------------------
+// Waves walk their units with a register double buffer: the next units'
+// source rows are in flight while the current ones are reduced, quantized and
+// stored, so loads overlap the arithmetic instead of every wave of the chip
+// loading, then computing, then storing in lockstep.
 
 // Value pack: the flat (token-head row, word) index space in units of one
 // wave (64 lanes = 64 / WPR rows, WPR = head_size / 8 words per row).  Each
@@ -472,37 +363,6 @@ extern "C" int kvq_kivi_pack_key(const void* src_a, int64_t n_a, const void* src
   if (num_tokens % group_size) return KVQ_ERR_INVALID;
   if (!src_index && n_a < num_tokens) return KVQ_ERR_INVALID;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int nch = group_size / 8;
-  if (nch <= 64 && (nch & (nch - 1)) == 0) {
-    // wave-pipelined kernel: items of (group, head, 8 * (64 / nch) dims)
-    const int span = 8 * (64 / nch);
-    const int slices = (head_size + span - 1) / span;
-    const int64_t items = (num_tokens / group_size) * num_kv_heads * slices;
-#define KVQ_LAUNCH_KEY_WAVE(NCH)                                                              \
-    KVQ_DISPATCH_FLOAT(src_dtype, T,                                                        \
-      KVQ_DISPATCH_INDEX(slot_index_type, I,                                                \
-        const int64_t fit = resident_blocks(kivi_pack_key_wave_kernel<T, I, NCH>, 64);      \
-        if (fit <= 0) return KVQ_ERR_INVALID;                                               \
-        const int64_t waves = items < fit ? items : fit;                                    \
-        hipLaunchKernelGGL((kivi_pack_key_wave_kernel<T, I, NCH>),                          \
-                           dim3(static_cast<unsigned>(waves)), dim3(64), 0, s,               \
-                           static_cast<const T*>(src_a), n_a, static_cast<const T*>(src_b),  \
-                           src_index, static_cast<const I*>(slot_mapping), num_kv_heads,     \
-                           head_size, group_size, block_size, slices, items, k_quant,        \
-                           k_scale, k_mn)))
-    switch (nch) {
-      case 1: KVQ_LAUNCH_KEY_WAVE(1); break;
-      case 2: KVQ_LAUNCH_KEY_WAVE(2); break;
-      case 4: KVQ_LAUNCH_KEY_WAVE(4); break;
-      case 8: KVQ_LAUNCH_KEY_WAVE(8); break;
-      case 16: KVQ_LAUNCH_KEY_WAVE(16); break;
-      case 32: KVQ_LAUNCH_KEY_WAVE(32); break;
-      default: KVQ_LAUNCH_KEY_WAVE(64); break;
-    }
-#undef KVQ_LAUNCH_KEY_WAVE
-    KVQ_LAUNCH_CHECK();
-    return KVQ_OK;
-  }
   const int tiles = (group_size / 8) * (head_size / 8);
   if (tiles > 1024) return KVQ_ERR_GEOMETRY;
   const int threads = ((tiles + 63) / 64) * 64;
