@@ -37,6 +37,19 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 METRIC = "INT4 pack/gather-dequant GB/s (% HBM peak); fused INT4 decode attn µs/layer"
 
 
+def recorded_traffic(name: str) -> int | None:
+    """HBM bytes per call recorded under profiles/ from the FETCH_SIZE /
+    WRITE_SIZE counter runs (counters cannot be read inside a timed run)."""
+    path = ROOT / "profiles" / "decode_hbm_traffic_pmc.md"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith(f"traffic_bytes_per_call {name}:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -460,6 +473,9 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-config5", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 512 MiB device-to-device 5 times (the known-size "
+                         "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -476,6 +492,15 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        n = 512 << 20
+        a = torch.ones(n, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 5}), flush=True)
+        return 0
 
     b, hq, kvh, d, g, r, bs = 32, 40, 8, 128, 128, 128, 128
     gen = torch.Generator().manual_seed(0)
@@ -541,7 +566,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(main_res["decode_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": recorded_traffic("config3"),
             "kernel": "kvq_kivi_decode_attn (fused INT4 decode + combine)",
             "algorithmic_bytes_per_launch": int(main_res["decode_bytes"]),
         },

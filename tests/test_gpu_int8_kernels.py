@@ -110,3 +110,27 @@ def test_int8_decode_matches_oracle(gpu_device, rep, kvh, d, bs):
             v_aq.to(gpu_device), table.to(gpu_device), lens, scale, split_tokens=split,
         )
         torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
+
+
+def test_int8_decode_empty_request_is_zero(gpu_device):
+    """A request with no cached tokens gets an empty work item: its output is
+    zero and the other requests still match the oracle."""
+    from vllm_ascend_quantized_kv_cache.ops.int8_ops import int8_decode_attention
+
+    dtype = torch.bfloat16
+    kvh, d, bs, rep = 8, 128, 128, 4
+    lens = [300, 0, 129]
+    table, kc, vc, k_inv, v_inv, k_aq, v_aq = _int8_state(gpu_device, 3, lens, kvh, d, bs, dtype, 5)
+    hq = kvh * rep
+    q = torch.randn(len(lens), hq, d, generator=torch.Generator().manual_seed(4)).to(dtype)
+    scale = d ** -0.5
+    got = int8_decode_attention(
+        q.to(gpu_device), kc.to(gpu_device), vc.to(gpu_device), k_aq.to(gpu_device),
+        v_aq.to(gpu_device), table.to(gpu_device), lens, scale,
+    ).float().cpu()
+    assert torch.equal(got[1], torch.zeros_like(got[1]))
+    live = [0, 2]
+    dk, dv = ref.int8_paged_dequant(kc, vc, table[live], [lens[i] for i in live], torch.float32,
+                                    k_inv, v_inv)
+    want = ref.attention(q[live], dk, dv, [1, 1], [lens[i] for i in live], scale, causal=True)
+    torch.testing.assert_close(got[live], want, atol=1e-2, rtol=1e-2)

@@ -228,13 +228,22 @@ int8_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   const int h = blockIdx.x - wi * kvh;
   const int lane = threadIdx.x;
   const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
-  if (wk[3] != 0) return;  // empty requests belong to the generic kernel
   const int b = wk[0];
   const int pb = wk[1];
   const int pe = wk[2];
   const int rep = hq / kvh;
   const int n = lane & 15;
   const int g = lane >> 4;
+  if (wk[3] != 0) {
+    // an empty request's item: m = -inf, l = 0 (the combine gives it weight 0
+    // and writes zeros when a request has nothing else)
+    if (lane < rep) {
+      const int64_t hh = static_cast<int64_t>(wi) * hq + static_cast<int64_t>(h) * rep + lane;
+      ws_ml[2 * hh] = -INFINITY;
+      ws_ml[2 * hh + 1] = 0.0f;
+    }
+    return;
+  }
 
   // ---- Q' = q * k_aq for head n, dims 32g + 8s + i, scaled by 2^e ----
   float qf[32];

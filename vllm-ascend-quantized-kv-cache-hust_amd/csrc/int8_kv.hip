@@ -168,12 +168,11 @@ int8_decode_generic_kernel(const T* __restrict__ query, int hq, int kvh, int d, 
                            const T* __restrict__ k_aq, const T* __restrict__ v_aq,
                            const int32_t* __restrict__ block_table, int64_t maxb,
                            const int32_t* __restrict__ work, float* __restrict__ ws_o,
-                           float* __restrict__ ws_ml, int skip_kind0) {
+                           float* __restrict__ ws_ml) {
   const int wi = blockIdx.x;
   const int h = blockIdx.y;
   const int lane = threadIdx.x;
   const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
-  if (skip_kind0 && wk[3] == 0) return;
   const int b = wk[0], pb = wk[1], pe = wk[2];
   const int rep = hq / kvh;
   const int dpl = (d + 63) / 64;
@@ -381,14 +380,16 @@ extern "C" int kvq_int8_decode_attn(const void* query, int dtype, int64_t batch,
                                        block_table, max_blocks, work, num_work, ws_o, ws_ml, s,
                                        &mfma);
   if (rc != KVQ_OK) return rc;
-  const dim3 grid(static_cast<unsigned>(num_work), num_kv_heads);
-  KVQ_DISPATCH_FLOAT(dtype, T,
-    hipLaunchKernelGGL((int8_decode_generic_kernel<T>), grid, dim3(64), 0, s,
-                       static_cast<const T*>(query), num_heads, num_kv_heads, head_size, qscale,
-                       key_cache, value_cache, block_size, static_cast<const T*>(k_aq),
-                       static_cast<const T*>(v_aq), block_table, max_blocks, work, ws_o, ws_ml,
-                       mfma ? 1 : 0));
-  KVQ_LAUNCH_CHECK();
+  if (!mfma) {  // the MFMA kernel covers every item (empty ones included) when it runs
+    const dim3 grid(static_cast<unsigned>(num_work), num_kv_heads);
+    KVQ_DISPATCH_FLOAT(dtype, T,
+      hipLaunchKernelGGL((int8_decode_generic_kernel<T>), grid, dim3(64), 0, s,
+                         static_cast<const T*>(query), num_heads, num_kv_heads, head_size,
+                         qscale, key_cache, value_cache, block_size,
+                         static_cast<const T*>(k_aq), static_cast<const T*>(v_aq), block_table,
+                         max_blocks, work, ws_o, ws_ml));
+    KVQ_LAUNCH_CHECK();
+  }
   return kvq::launch_decode_combine(dtype, batch, num_heads, head_size, seq_meta, 4, 1, ws_o,
                                     ws_ml, out, s);
 }
