@@ -12,8 +12,12 @@
  *   - Return 0 on success; KVQ_ERR_* (< 0) for rejected arguments; a positive
  *     hipError_t if the launch failed.  Nothing is launched when an argument
  *     is rejected.
- *   - Calls are asynchronous on `stream` and reentrant (no global mutable
- *     state).
+ *   - Calls are asynchronous on `stream` and thread-safe.  The only state
+ *     the library keeps is per device and created on first use: cached
+ *     device limits (LDS per workgroup, resident workgroups per kernel) and,
+ *     for kvq_kivi_decode_attn, a side stream with two events onto which the
+ *     tail items fork from `stream` and from which `stream` joins back before
+ *     the combine (the fork/join is serialized by a mutex).
  *
  * Reference paths are relative to /root/reference with
  * pkg/ = src/vllm_ascend_quantized_kv_cache/; each entry point names the
@@ -118,8 +122,11 @@ int kvq_kivi_gather_dequant(const int32_t* k_quant, const float* k_scale, const 
  *               positions < k_hist (v_hist) read int4 keys (values); the
  *               others read ring lane (first_lane + p - hist) % ring_len
  *   work        int32 [num_work, 4] = {request, pos_begin, pos_end, kind}
- *               kind 0: both sides int4 over the whole range (MFMA path);
- *               kind 1: any mix of sources (generic path)
+ *               kind 0: both sides int4 over the whole range (int4 MFMA
+ *                       kernel, 128-aligned ranges);
+ *               kind 1: any mix of sources (MFMA tail kernel on the side
+ *                       stream; the generic kernel for geometries neither
+ *                       MFMA kernel covers)
  *   workspace   >= kvq_kivi_decode_workspace_bytes(num_work, num_heads, D)
  *   block_table int32 [batch, max_blocks]
  * Replaces the decode branch: _forward_kivi_paged_decode_attention
