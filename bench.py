@@ -13,8 +13,8 @@ timed region; the timed region is the device work only.
 ``value`` = algorithmic bytes of the step / step time (GB/s).  ``roofline``
 covers the fused decode attention (the dominant kernel), timed with HIP
 events on its stream.  ``extra`` carries the other BASELINE configs: INT4
-pack and gather-dequant (config 4), INT8 decode (config 2), long-context INT4
-decode (config 5) and the config 1 round trip.  ``cpu_baseline`` times the
+pack, gather-dequant and the chunk's causal attention (config 4), INT8 decode
+(config 2) and long-context INT4 decode (config 5).  ``cpu_baseline`` times the
 CPU oracle (the reference algorithm restated in torch) on a bounded sample.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-extras] [--no-cpu]
@@ -34,6 +34,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "vllm-ascend-quantized-kv-cache-hust_amd"))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 METRIC = "INT4 pack/gather-dequant GB/s (% HBM peak); fused INT4 decode attn µs/layer"
 
 
@@ -399,13 +400,40 @@ def bench_pack_gather(torch, dev, *, reps=10, seed=0):
     hist = sum(q.k_hist + q.v_hist for q in seqs)
     res_t = sum(2 * q.seq_len - q.k_hist - q.v_hist for q in seqs)
     gather_bytes = hist * kvh * (s + 2 * d) + res_t * kvh * d * 4
-    del st, key, value
+
+    # causal MFMA attention of the 2048-token chunk (kv positions 8192..10239)
+    # over the gathered 10240-token K/V of each request
+    from vllm_ascend_quantized_kv_cache.ops.attention import prefill_attention
+
+    hq = 40
+    dk, dv = gather()
+    q = torch.randn((b * chunk, hq, d), generator=gdev, device=dev).to(torch.bfloat16)
+    q_lens, kv_lens = [chunk] * b, list(lens)
+    attn_out = torch.empty_like(q)
+
+    def attend():
+        prefill_attention(q, dk, dv, q_lens, kv_lens, d ** -0.5, True, out=attn_out)
+
+    attend()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        attend()
+    e1.record()
+    torch.cuda.synchronize()
+    attn_ms = e0.elapsed_time(e1) / reps
+    # causally valid (query, key) pairs x heads x (QK + PV) x 2 flops x D
+    pairs = sum(sum(range(n - m + 1, n + 1)) for m, n in zip(q_lens, kv_lens))
+    attn_flops = 4 * d * hq * pairs
+    del st, key, value, dk, dv, q, attn_out
     torch.cuda.empty_cache()
     return {
         "pack_ms": pack_ms,
         "pack_gbs": pack_bytes / pack_ms / 1e6,
         "gather_ms": gather_ms,
         "gather_gbs": gather_bytes / gather_ms / 1e6,
+        "attn_ms": attn_ms,
+        "attn_tflops": attn_flops / attn_ms / 1e9,
     }
 
 
@@ -521,7 +549,11 @@ def main() -> int:
         extra["config4_gather"] = {"ms": round(pg["gather_ms"], 4),
                                    "gbs": round(pg["gather_gbs"], 1),
                                    "frac": round(pg["gather_gbs"] / HBM_PEAK_GBS, 4)}
-        log(f"config4: pack {pg['pack_gbs']:.0f} GB/s, gather {pg['gather_gbs']:.0f} GB/s")
+        extra["config4_prefill_attn"] = {"ms": round(pg["attn_ms"], 4),
+                                         "tflops": round(pg["attn_tflops"], 1),
+                                         "frac": round(pg["attn_tflops"] / MFMA_PEAK_TFLOPS, 4)}
+        log(f"config4: pack {pg['pack_gbs']:.0f} GB/s, gather {pg['gather_gbs']:.0f} GB/s, "
+            f"attention {pg['attn_tflops']:.0f} TFLOP/s")
         i8 = bench_int8_decode(torch, dev)
         extra["config2_int8_decode"] = {k: round(v, 4) for k, v in i8.items()}
         log(f"config2: int8 decode {i8['us_per_layer']:.1f} us ({i8['gbs']:.0f} GB/s)")

@@ -10,7 +10,10 @@
 // position lk - lq + i; with `causal`, key positions past it are masked
 // (pkg/methods/kivi_int4/semantics.py:285-299).
 //
-// One workgroup = 4 waves = 64 query rows of one query head; each wave owns
+// bf16/fp16 inputs with head_size 64 or 128 run prefill_attn_fa_kernel
+// (64-key blocks, DMA-staged K, transposed V, described at the kernel).  The
+// kernel below covers the rest (fp32 inputs, head_size 32 and 256):
+// one workgroup = 4 waves = 64 query rows of one query head; each wave owns
 // 16 rows.  Keys/values stream through LDS in 32-token blocks.
 //   S^T = K * Q^T   (v_mfma_f32_16x16x32_{bf16,f16}): A = K rows from LDS
 //                   (16-byte reads), B = Q^T from registers (loaded once).
@@ -224,6 +227,272 @@ prefill_attn_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
     for (int r = 0; r < 4; ++r) orow[16 * j + 4 * kg + r] = from_f32<T>(o[j][r] * inv);
 }
 
+// ---- 64-key-block kernel for 16-bit inputs, D in {64, 128} ------------------
+// One workgroup = 4 waves x 32 query rows (two 16-row MFMA column groups) of one
+// query head; key/value blocks of 64 tokens, double-buffered in LDS with one
+// barrier per block:
+//   K  [64][D]    written by global_load_lds (16-byte lanes); the 16-byte
+//                 column of each row is XOR-swizzled by the row so that the
+//                 16 rows one score MFMA reads sit in different banks;
+//   V^T [D][64+4] written from registers: a thread loads 4 keys x 8 dims and
+//                 stores each dim's 4 keys as one 8-byte word, so the PV
+//                 operand (4 consecutive keys of one dim) is an 8-byte read.
+// While block i is computed, block i+1's K is in flight (DMA) and its V sits in
+// registers until the compute is done.
+//   S^T = K * Q^T: A = 16 keys x 32 dims (one 16-byte read per lane), B = the
+//                  wave's Q^T (registers), each A feeding both column groups.
+//   O^T += V^T * P^T: B = P^T straight from the S^T registers (the lane's
+//                  keys 16*(2ks + i/4) + 4*kg + i%4 of its query column),
+//                  A = the same 8 keys of one dim from V^T (two 8-byte reads).
+// The rescale needs no shuffles: S^T and O^T both put the lane's query in
+// its column.
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)(lds), 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(0) with expcnt/lgkmcnt left at their maxima (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+__device__ __forceinline__ void wait_vmcnt0() {
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+
+constexpr int kFaRows = 32;   // query rows per wave
+constexpr int kFaWaves = 4;
+constexpr int kFaBlock = 64;  // keys per block
+constexpr int kFaVPitch = kFaBlock + 4;
+
+template <int D>
+struct FaLds {
+  static constexpr int K_BYTES = kFaBlock * D * 2;
+  static constexpr int V_BYTES = D * kFaVPitch * 2;
+  static constexpr int BUF = K_BYTES + V_BYTES;
+  static constexpr int BYTES = 2 * BUF;
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                       const T* __restrict__ v, const int32_t* __restrict__ cu_q,
+                       const int32_t* __restrict__ cu_k, int hq, int kvh, float qscale,
+                       int causal, int qblocks, T* __restrict__ out) {
+  using O = typename Op<T>::type;
+  using L = FaLds<D>;
+  constexpr int KS = D / 32;      // score k-steps
+  constexpr int DB = D / 16;      // output dim blocks
+  constexpr int PPR = D / 8;      // 16-byte pieces per row
+  constexpr int RPI = 64 / PPR;   // K rows per DMA instruction
+  constexpr int KINST = kFaBlock / RPI / kFaWaves;  // DMA instructions per wave per block
+  constexpr int VTASKS = (kFaBlock / 4) * PPR;      // (key quad, piece) tasks per block
+  static_assert(KINST >= 1 && kFaBlock % (RPI * kFaWaves) == 0, "K DMA split");
+  static_assert(VTASKS <= 256, "one V task per thread");
+  extern __shared__ __align__(16) char lds[];
+
+  // heavy query blocks first: block x = qblocks - 1 - blockIdx.x
+  const int qb = qblocks - 1 - static_cast<int>(blockIdx.x);
+  const int head = blockIdx.y;
+  const int b = blockIdx.z;
+  const int kvhead = head / (hq / kvh);
+  const int q_start = cu_q[b];
+  const int lq = cu_q[b + 1] - q_start;
+  const int k_start = cu_k[b];
+  const int lk = cu_k[b + 1] - k_start;
+  const int row0 = qb * (kFaRows * kFaWaves);
+  if (row0 >= lq || lk <= 0) return;  // uniform over the workgroup
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int n = lane & 15;
+  const int kg = lane >> 4;
+  const int wrow0 = row0 + wave * kFaRows;
+  const int last_row = min(row0 + kFaRows * kFaWaves, lq) - 1;
+  const int kv_end = causal ? min(lk, lk - lq + last_row + 1) : lk;
+  const int nblk = (kv_end + kFaBlock - 1) / kFaBlock;
+  const int wave_last = min(wrow0 + kFaRows, lq) - 1;  // < wrow0 when the wave has no rows
+  const int wave_last_pos = lk - lq + wave_last;
+
+  // Q^T operands: group g2, k-step s: query row wrow0 + 16*g2 + n, dims 32s + 8kg + i
+  u8v qop[2][KS];
+  int my_pos[2];
+  bool live[2];
+#pragma unroll
+  for (int g2 = 0; g2 < 2; ++g2) {
+    const int row = wrow0 + 16 * g2 + n;
+    live[g2] = row < lq;
+    my_pos[g2] = lk - lq + row;
+    const T* qrow = q + (static_cast<int64_t>(q_start + (live[g2] ? row : 0)) * hq + head) * D;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u8v x = load_op8(qrow + 32 * s + 8 * kg);
+      if (!live[g2]) x = u8v{0, 0, 0, 0, 0, 0, 0, 0};
+      qop[g2][s] = x;
+    }
+  }
+
+  // ---- staging ----
+  const T* kbase = k + (static_cast<int64_t>(k_start) * kvh + kvhead) * D;
+  const T* vbase = v + (static_cast<int64_t>(k_start) * kvh + kvhead) * D;
+  const int64_t row_stride = static_cast<int64_t>(kvh) * D;
+  auto issue_k = [&](char* buf, int kb) {
+#pragma unroll
+    for (int i = 0; i < KINST; ++i) {
+      const int inst = wave * KINST + i;
+      const int r = inst * RPI + lane / PPR;  // block row of this lane
+      const int slot = lane % PPR;
+      const int piece = slot ^ (r % PPR);      // swizzled column
+      int pos = kb + r;
+      pos = pos < lk ? pos : lk - 1;           // rows past the end: a valid row, masked later
+      dma16(kbase + pos * row_stride + 8 * piece, buf + 1024 * inst);
+    }
+  };
+  // V task of this thread: key quad j, piece c (dims 8c .. 8c + 7)
+  const int vj = tid / PPR;
+  const int vc = tid % PPR;
+  const bool vtask = tid < VTASKS;
+  uint4 vr[4];
+  auto load_v = [&](int kb) {
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      int pos = kb + 4 * vj + l;
+      pos = pos < lk ? pos : lk - 1;
+      if (vtask) vr[l] = *reinterpret_cast<const uint4*>(vbase + pos * row_stride + 8 * vc);
+    }
+  };
+  auto store_vt = [&](char* buf) {
+    if (!vtask) return;
+    uint16_t* vt = reinterpret_cast<uint16_t*>(buf + L::K_BYTES);
+    const uint32_t w0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
+    const uint32_t w1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
+    const uint32_t w2[4] = {vr[2].x, vr[2].y, vr[2].z, vr[2].w};
+    const uint32_t w3[4] = {vr[3].x, vr[3].y, vr[3].z, vr[3].w};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      // dim 8c + 2w: low halves of keys 0..3; dim 8c + 2w + 1: high halves
+      uint2 lo, hi;
+      lo.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x05040100u);
+      lo.y = __builtin_amdgcn_perm(w3[w], w2[w], 0x05040100u);
+      hi.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u);
+      hi.y = __builtin_amdgcn_perm(w3[w], w2[w], 0x07060302u);
+      *reinterpret_cast<uint2*>(vt + (8 * vc + 2 * w) * kFaVPitch + 4 * vj) = lo;
+      *reinterpret_cast<uint2*>(vt + (8 * vc + 2 * w + 1) * kFaVPitch + 4 * vj) = hi;
+    }
+  };
+
+  float m_run[2] = {-INFINITY, -INFINITY};
+  float l_run[2] = {0.0f, 0.0f};
+  f4 o[DB][2];
+#pragma unroll
+  for (int j = 0; j < DB; ++j) o[j][0] = o[j][1] = f4{0.f, 0.f, 0.f, 0.f};
+
+  // prologue: block 0
+  issue_k(lds, 0);
+  load_v(0);
+  wait_vmcnt0();  // K landed in LDS, V in registers
+  store_vt(lds);
+  __syncthreads();
+
+  for (int i = 0; i < nblk; ++i) {
+    const int kb = i * kFaBlock;
+    char* cur = lds + (i & 1) * L::BUF;
+    char* nxt = lds + ((i + 1) & 1) * L::BUF;
+    const bool more = i + 1 < nblk;
+    if (more) {
+      issue_k(nxt, kb + kFaBlock);
+      load_v(kb + kFaBlock);
+    }
+    // waves whose rows all precede this block under the causal mask skip it
+    if (wrow0 <= wave_last && !(causal && kb > wave_last_pos)) {
+      const uint16_t* sk = reinterpret_cast<const uint16_t*>(cur);
+      const uint16_t* svt = reinterpret_cast<const uint16_t*>(cur + L::K_BYTES);
+      // ---- S^T = K * Q^T ----
+      f4 sacc[4][2];
+#pragma unroll
+      for (int kb2 = 0; kb2 < 4; ++kb2) sacc[kb2][0] = sacc[kb2][1] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb2 = 0; kb2 < 4; ++kb2) {
+        const int r = 16 * kb2 + n;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const int piece = (4 * s + kg) ^ (r % PPR);
+          const u8v a = *reinterpret_cast<const u8v*>(sk + r * D + 8 * piece);
+          sacc[kb2][0] = mfma16(a, qop[0][s], sacc[kb2][0], O{});
+          sacc[kb2][1] = mfma16(a, qop[1][s], sacc[kb2][1], O{});
+        }
+      }
+      // ---- online softmax per query column ----
+      u8v pop[2][2];  // [g2][ks]
+#pragma unroll
+      for (int g2 = 0; g2 < 2; ++g2) {
+        float sv[16];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int kb2 = 0; kb2 < 4; ++kb2)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int pos = kb + 16 * kb2 + 4 * kg + r;
+            const bool ok = pos < lk && (!causal || pos <= my_pos[g2]);
+            const float x = ok ? sacc[kb2][g2][r] * qscale : -INFINITY;
+            sv[4 * kb2 + r] = x;
+            tmax = fmaxf(tmax, x);
+          }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = fmaxf(m_run[g2], tmax);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = m_run[g2] == -INFINITY ? 0.0f : exp2f(m_run[g2] - m_use);
+        float psum = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int i8 = 0; i8 < 8; ++i8) {
+            const float p = exp2f(sv[4 * (2 * ks + i8 / 4) + (i8 % 4)] - m_use);  // exp2(-inf) = 0
+            const uint16_t bits = op_bits(p, O{});
+            pop[g2][ks][i8] = bits;
+            psum += op_to_f32(bits, O{});  // normalise by what the MFMA sees
+          }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        l_run[g2] = l_run[g2] * alpha + psum;
+        m_run[g2] = m_new;
+#pragma unroll
+        for (int j = 0; j < DB; ++j) o[j][g2] *= alpha;
+      }
+      // ---- O^T += V^T * P^T ----
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int j = 0; j < DB; ++j) {
+          const uint16_t* row = svt + (16 * j + n) * kFaVPitch + 32 * ks + 4 * kg;
+          const uint2 lo = *reinterpret_cast<const uint2*>(row);
+          const uint2 hi = *reinterpret_cast<const uint2*>(row + 16);
+          const u8v a = __builtin_bit_cast(u8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
+          o[j][0] = mfma16(a, pop[0][ks], o[j][0], O{});
+          o[j][1] = mfma16(a, pop[1][ks], o[j][1], O{});
+        }
+    }
+    if (more) {
+      wait_vmcnt0();  // next K landed in LDS, next V in registers
+      store_vt(nxt);
+    }
+    __syncthreads();
+  }
+
+  // o[j][g2][r] = O^T[dim 16j + 4kg + r][query 16*g2 + n]
+#pragma unroll
+  for (int g2 = 0; g2 < 2; ++g2) {
+    if (!live[g2]) continue;
+    const float inv = l_run[g2] > 0.0f ? 1.0f / l_run[g2] : 0.0f;
+    T* orow = out + (static_cast<int64_t>(q_start + wrow0 + 16 * g2 + n) * hq + head) * D;
+#pragma unroll
+    for (int j = 0; j < DB; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) orow[16 * j + 4 * kg + r] = from_f32<T>(o[j][g2][r] * inv);
+  }
+}
+
 }  // namespace
 
 extern "C" int kvq_prefill_attn(const void* query, const void* key, const void* value, int dtype,
@@ -238,11 +507,46 @@ extern "C" int kvq_prefill_attn(const void* query, const void* key, const void* 
   if (num_kv_heads <= 0 || num_heads % num_kv_heads) return KVQ_ERR_GEOMETRY;
   if (head_size != 64 && head_size != 128 && head_size != 256 && head_size != 32)
     return KVQ_ERR_GEOMETRY;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const float qscale = scale * 1.4426950408889634f;
+  // LDS one workgroup may use on this device (cached per device)
+  static int64_t lds_cache[64] = {};
+  int dev = 0;
+  hipError_t he = hipGetDevice(&dev);
+  if (he != hipSuccess) return static_cast<int>(he);
+  if (dev >= 0 && dev < 64 && lds_cache[dev] == 0) {
+    int vmax = 0;
+    he = hipDeviceGetAttribute(&vmax, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (he != hipSuccess) return static_cast<int>(he);
+    lds_cache[dev] = vmax;
+  }
+  const int64_t lds_max = dev >= 0 && dev < 64 ? lds_cache[dev] : 0;
+  const int64_t fa_lds = head_size == 64 ? FaLds<64>::BYTES : FaLds<128>::BYTES;
+  if ((dtype == KVQ_DTYPE_BF16 || dtype == KVQ_DTYPE_F16) &&
+      (head_size == 64 || head_size == 128) && fa_lds <= lds_max) {
+    const int64_t fab = (max_q_len + kFaRows * kFaWaves - 1) / (kFaRows * kFaWaves);
+    if (fab > 0x7fffffff) return KVQ_ERR_INVALID;
+    const dim3 fgrid(static_cast<unsigned>(fab), num_heads, static_cast<unsigned>(batch));
+#define KVQ_PREFILL_FA(TT, DD)                                                              \
+    hipLaunchKernelGGL((prefill_attn_fa_kernel<TT, DD>), fgrid, dim3(256),                  \
+                       FaLds<DD>::BYTES, s, static_cast<const TT*>(query),                 \
+                       static_cast<const TT*>(key), static_cast<const TT*>(value),         \
+                       cu_seqlens_q, cu_seqlens_k, num_heads, num_kv_heads, qscale, causal, \
+                       static_cast<int>(fab), static_cast<TT*>(out))
+    if (dtype == KVQ_DTYPE_BF16) {
+      if (head_size == 64) KVQ_PREFILL_FA(kvq::bf16, 64);
+      else KVQ_PREFILL_FA(kvq::bf16, 128);
+    } else {
+      if (head_size == 64) KVQ_PREFILL_FA(kvq::f16, 64);
+      else KVQ_PREFILL_FA(kvq::f16, 128);
+    }
+#undef KVQ_PREFILL_FA
+    KVQ_LAUNCH_CHECK();
+    return KVQ_OK;
+  }
   const int64_t qblocks = (max_q_len + 63) / 64;
   if (qblocks > 0x7fffffff) return KVQ_ERR_INVALID;
   const dim3 grid(static_cast<unsigned>(qblocks), num_heads, static_cast<unsigned>(batch));
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const float qscale = scale * 1.4426950408889634f;
 #define KVQ_PREFILL(DD)                                                                  \
   KVQ_DISPATCH_FLOAT(dtype, T,                                                           \
     hipLaunchKernelGGL((prefill_attn_kernel<T, DD>), grid, dim3(256), 0, s,              \
