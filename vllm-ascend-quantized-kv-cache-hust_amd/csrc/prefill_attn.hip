@@ -61,6 +61,22 @@ __device__ __forceinline__ float op_to_f32(uint16_t bits, f16) {
   return static_cast<float>(__builtin_bit_cast(_Float16, bits));
 }
 
+// Two fp32 values as an operand pair (round to nearest even), and back.
+__device__ __forceinline__ uint32_t pack_op2(float lo, float hi, bf16) { return bf16x2_bits(lo, hi); }
+__device__ __forceinline__ uint32_t pack_op2(float lo, float hi, f16) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v{lo, hi}), h2v));
+}
+__device__ __forceinline__ float op_lo_f32(uint32_t w, bf16) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float op_hi_f32(uint32_t w, bf16) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float op_lo_f32(uint32_t w, f16) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w)));
+}
+__device__ __forceinline__ float op_hi_f32(uint32_t w, f16) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+}
+
 __device__ __forceinline__ f4 mfma16(u8v a, u8v b, f4 c, bf16) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, a), __builtin_bit_cast(b8, b),
                                                  c, 0, 0, 0);
@@ -423,6 +439,9 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
         }
       }
       // ---- online softmax per query column ----
+      // the max runs over raw scores (qscale > 0), the exponent is one fma:
+      // p = 2^(qscale * s - qscale * m)
+      const bool full = kb + kFaBlock <= lk && (!causal || kb + kFaBlock - 1 <= lk - lq + wrow0);
       u8v pop[2][2];  // [g2][ks]
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
@@ -432,33 +451,45 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
         for (int kb2 = 0; kb2 < 4; ++kb2)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int pos = kb + 16 * kb2 + 4 * kg + r;
-            const bool ok = pos < lk && (!causal || pos <= my_pos[g2]);
-            const float x = ok ? sacc[kb2][g2][r] * qscale : -INFINITY;
+            float x = sacc[kb2][g2][r];
+            if (!full) {
+              const int pos = kb + 16 * kb2 + 4 * kg + r;
+              x = (pos < lk && (!causal || pos <= my_pos[g2])) ? x : -INFINITY;
+            }
             sv[4 * kb2 + r] = x;
             tmax = fmaxf(tmax, x);
           }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run[g2], tmax);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = m_run[g2] == -INFINITY ? 0.0f : exp2f(m_run[g2] - m_use);
+        const float m_new = fmaxf(m_run[g2], tmax);  // raw-score units
+        const float m_off = m_new == -INFINITY ? 0.0f : -qscale * m_new;
+        const float alpha = m_run[g2] == -INFINITY
+                                ? 0.0f
+                                : __builtin_amdgcn_exp2f(__builtin_fmaf(qscale, m_run[g2], m_off));
         float psum = 0.0f;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        for (int ks = 0; ks < 2; ++ks) {
+          uint32_t w[4];
 #pragma unroll
-          for (int i8 = 0; i8 < 8; ++i8) {
-            const float p = exp2f(sv[4 * (2 * ks + i8 / 4) + (i8 % 4)] - m_use);  // exp2(-inf) = 0
-            const uint16_t bits = op_bits(p, O{});
-            pop[g2][ks][i8] = bits;
-            psum += op_to_f32(bits, O{});  // normalise by what the MFMA sees
+          for (int h = 0; h < 4; ++h) {
+            const int i0 = 2 * h, i1 = 2 * h + 1;
+            const float p0 = __builtin_amdgcn_exp2f(
+                __builtin_fmaf(qscale, sv[4 * (2 * ks + i0 / 4) + (i0 % 4)], m_off));
+            const float p1 = __builtin_amdgcn_exp2f(
+                __builtin_fmaf(qscale, sv[4 * (2 * ks + i1 / 4) + (i1 % 4)], m_off));
+            w[h] = pack_op2(p0, p1, O{});
+            psum += op_lo_f32(w[h], O{}) + op_hi_f32(w[h], O{});  // what the MFMA sees
           }
+          pop[g2][ks] = __builtin_bit_cast(u8v, make_uint4(w[0], w[1], w[2], w[3]));
+        }
         psum += __shfl_xor(psum, 16, 64);
         psum += __shfl_xor(psum, 32, 64);
         l_run[g2] = l_run[g2] * alpha + psum;
         m_run[g2] = m_new;
+        if (__any(alpha != 1.0f)) {
 #pragma unroll
-        for (int j = 0; j < DB; ++j) o[j][g2] *= alpha;
+          for (int j = 0; j < DB; ++j) o[j][g2] *= alpha;
+        }
       }
       // ---- O^T += V^T * P^T ----
 #pragma unroll
