@@ -570,19 +570,22 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
                     ks + krow * gpb + off0 / g, km + krow * gpb + off0 / g, gpb, vs + vtok * ng,
                     vm + vtok * ng, ng, g);
   };
-  issue(lds_raw, pb);  // prologue: tile 0 into buffer 0
-  int cur = 0;
+  // One tile step: DMA of tile p0 + GT into `nxt`, then compute tile p0 from
+  // `cur`.  Both buffers are __restrict__ within the step, which tells the
+  // compiler's wait-count pass that the reads of `cur` cannot alias the DMA
+  // in flight into `nxt`: without it the pass puts vmcnt(0) -- a wait for the
+  // next tile -- in front of the first LDS read and the double buffer never
+  // overlaps.  The wait for tile p0 itself is explicit.
   QGroup qg;
-  for (int p0 = pb; p0 < pe; p0 += GT) {
-    // prefetch tile p0 + GT into the other buffer, then wait for this tile only
+  auto step = [&](const char* __restrict__ cur, char* __restrict__ nxt, int p0) {
     const int p1 = p0 + GT;
     if (p1 < pe) {
-      issue(lds_raw + (cur ^ 1) * T::BYTES, p1);
+      issue(nxt, p1);
       wait_vmcnt<T::NINST>();
     } else {
       wait_vmcnt<0>();
     }
-    const uint32_t* W = reinterpret_cast<const uint32_t*>(lds_raw + cur * T::BYTES);
+    const uint32_t* W = reinterpret_cast<const uint32_t*>(cur);
     // tiles are GT-aligned and GT divides g: a tile starts a key group or
     // continues the previous tile's
     if (p0 == pb || p0 % g == 0) prepare_group<TQ, CPG>(W, kg, qv, qscale, qg);
@@ -590,6 +593,11 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
       compute_tile<TQ, CPG, true>(W, p0, pe, n, kg, qg, qscale, ln, m_run, l_run, o_acc, c_acc, bias_v);
     else
       compute_tile<TQ, CPG, false>(W, p0, pe, n, kg, qg, qscale, ln, m_run, l_run, o_acc, c_acc, bias_v);
+  };
+  issue(lds_raw, pb);  // prologue: tile 0 into buffer 0
+  int cur = 0;
+  for (int p0 = pb; p0 < pe; p0 += GT) {
+    step(lds_raw + cur * T::BYTES, lds_raw + (cur ^ 1) * T::BYTES, p0);
     // every LDS read of this buffer has been consumed before the next
     // iteration's DMA may overwrite it
     asm volatile("" ::: "memory");

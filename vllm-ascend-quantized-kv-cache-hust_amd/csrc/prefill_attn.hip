@@ -251,8 +251,10 @@ prefill_attn_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
 //                 column of each row is XOR-swizzled by the row so that the
 //                 16 rows one score MFMA reads sit in different banks;
 //   V^T [D][64+4] written from registers: a thread loads 4 keys x 8 dims and
-//                 stores each dim's 4 keys as one 8-byte word, so the PV
-//                 operand (4 consecutive keys of one dim) is an 8-byte read.
+//                 stores each dim's 4 keys as one 8-byte word (neighbouring
+//                 lanes hold neighbouring key quads: conflict-free stores), so
+//                 the PV operand (4 consecutive keys of one dim) is an 8-byte
+//                 read.
 // While block i is computed, block i+1's K is in flight (DMA) and its V sits in
 // registers until the compute is done.
 //   S^T = K * Q^T: A = 16 keys x 32 dims (one 16-byte read per lane), B = the
@@ -364,9 +366,11 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
       dma16(kbase + pos * row_stride + 8 * piece, buf + 1024 * inst);
     }
   };
-  // V task of this thread: key quad j, piece c (dims 8c .. 8c + 7)
-  const int vj = tid / PPR;
-  const int vc = tid % PPR;
+  // V task of this thread: key quad j, piece c (dims 8c .. 8c + 7).  Lanes
+  // next to each other take consecutive key quads, so a quarter-wave's
+  // transposed stores (row 8c + i, keys 4j .. 4j + 3) are 128 contiguous bytes.
+  const int vj = tid % 16;
+  const int vc = tid / 16;
   const bool vtask = tid < VTASKS;
   uint4 vr[4];
   auto load_v = [&](int kb) {
@@ -410,10 +414,13 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   store_vt(lds);
   __syncthreads();
 
-  for (int i = 0; i < nblk; ++i) {
+  // One block step: staging of block i + 1 into `nxt` and compute of block i
+  // from `cur`.  The two buffers are __restrict__ within the step, so the
+  // compiler's wait-count pass knows the LDS reads of `cur` cannot alias the
+  // DMA in flight into `nxt` (otherwise it waits for that DMA before the
+  // first read and the double buffer never overlaps).
+  auto step = [&](const char* __restrict__ cur, char* __restrict__ nxt, int i) {
     const int kb = i * kFaBlock;
-    char* cur = lds + (i & 1) * L::BUF;
-    char* nxt = lds + ((i + 1) & 1) * L::BUF;
     const bool more = i + 1 < nblk;
     if (more) {
       issue_k(nxt, kb + kFaBlock);
@@ -429,13 +436,20 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
       for (int kb2 = 0; kb2 < 4; ++kb2) sacc[kb2][0] = sacc[kb2][1] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb2 = 0; kb2 < 4; ++kb2) {
+        // all k-steps' K operands of this 16-key block first, then the MFMAs:
+        // the LDS reads overlap instead of each waiting for the one before
         const int r = 16 * kb2 + n;
+        u8v a[KS];
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
           const int piece = (4 * s + kg) ^ (r % PPR);
-          const u8v a = *reinterpret_cast<const u8v*>(sk + r * D + 8 * piece);
-          sacc[kb2][0] = mfma16(a, qop[0][s], sacc[kb2][0], O{});
-          sacc[kb2][1] = mfma16(a, qop[1][s], sacc[kb2][1], O{});
+          a[s] = *reinterpret_cast<const u8v*>(sk + r * D + 8 * piece);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          sacc[kb2][0] = mfma16(a[s], qop[0][s], sacc[kb2][0], O{});
+          sacc[kb2][1] = mfma16(a[s], qop[1][s], sacc[kb2][1], O{});
         }
       }
       // ---- online softmax per query column ----
@@ -493,21 +507,30 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
       }
       // ---- O^T += V^T * P^T ----
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < 2; ++ks) {
+        u8v a[DB];  // every dim block's V^T operand of this k-step, then the MFMAs
 #pragma unroll
         for (int j = 0; j < DB; ++j) {
           const uint16_t* row = svt + (16 * j + n) * kFaVPitch + 32 * ks + 4 * kg;
           const uint2 lo = *reinterpret_cast<const uint2*>(row);
           const uint2 hi = *reinterpret_cast<const uint2*>(row + 16);
-          const u8v a = __builtin_bit_cast(u8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
-          o[j][0] = mfma16(a, pop[0][ks], o[j][0], O{});
-          o[j][1] = mfma16(a, pop[1][ks], o[j][1], O{});
+          a[j] = __builtin_bit_cast(u8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
         }
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+        for (int j = 0; j < DB; ++j) {
+          o[j][0] = mfma16(a[j], pop[0][ks], o[j][0], O{});
+          o[j][1] = mfma16(a[j], pop[1][ks], o[j][1], O{});
+        }
+      }
     }
     if (more) {
       wait_vmcnt0();  // next K landed in LDS, next V in registers
       store_vt(nxt);
     }
+  };
+  for (int i = 0; i < nblk; ++i) {
+    step(lds + (i & 1) * L::BUF, lds + ((i + 1) & 1) * L::BUF, i);
     __syncthreads();
   }
 
