@@ -354,16 +354,27 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   const T* kbase = k + (static_cast<int64_t>(k_start) * kvh + kvhead) * D;
   const T* vbase = v + (static_cast<int64_t>(k_start) * kvh + kvhead) * D;
   const int64_t row_stride = static_cast<int64_t>(kvh) * D;
+  // per-lane element offsets of the K rows this lane moves (row r of the
+  // block, swizzled piece), relative to the block's first row
+  int64_t koff[KINST];
+  int krow[KINST];
+#pragma unroll
+  for (int i = 0; i < KINST; ++i) {
+    const int inst = wave * KINST + i;
+    const int r = inst * RPI + lane / PPR;  // block row of this lane
+    const int piece = (lane % PPR) ^ (r % PPR);  // swizzled column
+    krow[i] = r;
+    koff[i] = r * row_stride + 8 * piece;
+  }
   auto issue_k = [&](char* buf, int kb) {
+    const bool whole = kb + kFaBlock <= lk;  // uniform: only the last block clamps
 #pragma unroll
     for (int i = 0; i < KINST; ++i) {
       const int inst = wave * KINST + i;
-      const int r = inst * RPI + lane / PPR;  // block row of this lane
-      const int slot = lane % PPR;
-      const int piece = slot ^ (r % PPR);      // swizzled column
-      int pos = kb + r;
-      pos = pos < lk ? pos : lk - 1;           // rows past the end: a valid row, masked later
-      dma16(kbase + pos * row_stride + 8 * piece, buf + 1024 * inst);
+      const T* src = kbase + kb * row_stride + koff[i];
+      if (!whole && kb + krow[i] >= lk)  // rows past the end: a valid row, masked later
+        src = kbase + static_cast<int64_t>(lk - 1) * row_stride + (koff[i] - krow[i] * row_stride);
+      dma16(src, buf + 1024 * inst);
     }
   };
   // V task of this thread: key quad j, piece c (dims 8c .. 8c + 7).  Lanes
@@ -373,12 +384,20 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   const int vc = tid / 16;
   const bool vtask = tid < VTASKS;
   uint4 vr[4];
+  const T* vlane = vbase + (4 * vj) * row_stride + 8 * vc;
   auto load_v = [&](int kb) {
+    if (!vtask) return;
+    if (kb + kFaBlock <= lk) {  // uniform: only the last block clamps
+      const T* src = vlane + kb * row_stride;
 #pragma unroll
-    for (int l = 0; l < 4; ++l) {
-      int pos = kb + 4 * vj + l;
-      pos = pos < lk ? pos : lk - 1;
-      if (vtask) vr[l] = *reinterpret_cast<const uint4*>(vbase + pos * row_stride + 8 * vc);
+      for (int l = 0; l < 4; ++l) vr[l] = *reinterpret_cast<const uint4*>(src + l * row_stride);
+    } else {
+#pragma unroll
+      for (int l = 0; l < 4; ++l) {
+        int pos = kb + 4 * vj + l;
+        pos = pos < lk ? pos : lk - 1;
+        vr[l] = *reinterpret_cast<const uint4*>(vbase + pos * row_stride + 8 * vc);
+      }
     }
   };
   auto store_vt = [&](char* buf) {
@@ -402,10 +421,15 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   };
 
   float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.0f, 0.0f};
+  // l_acc[g2]: every row holds the running sum of the (rounded) P of query
+  // column n, accumulated by an MFMA with an all-ones A, so it is the exact sum
+  // of what the PV MFMAs saw and rescales together with o
+  f4 l_acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
   f4 o[DB][2];
 #pragma unroll
   for (int j = 0; j < DB; ++j) o[j][0] = o[j][1] = f4{0.f, 0.f, 0.f, 0.f};
+  const uint16_t one = op_bits(1.0f, O{});
+  const u8v ones = u8v{one, one, one, one, one, one, one, one};
 
   // prologue: block 0
   issue_k(lds, 0);
@@ -480,7 +504,6 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
         const float alpha = m_run[g2] == -INFINITY
                                 ? 0.0f
                                 : __builtin_amdgcn_exp2f(__builtin_fmaf(qscale, m_run[g2], m_off));
-        float psum = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           uint32_t w[4];
@@ -492,15 +515,12 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
             const float p1 = __builtin_amdgcn_exp2f(
                 __builtin_fmaf(qscale, sv[4 * (2 * ks + i1 / 4) + (i1 % 4)], m_off));
             w[h] = pack_op2(p0, p1, O{});
-            psum += op_lo_f32(w[h], O{}) + op_hi_f32(w[h], O{});  // what the MFMA sees
           }
           pop[g2][ks] = __builtin_bit_cast(u8v, make_uint4(w[0], w[1], w[2], w[3]));
         }
-        psum += __shfl_xor(psum, 16, 64);
-        psum += __shfl_xor(psum, 32, 64);
-        l_run[g2] = l_run[g2] * alpha + psum;
         m_run[g2] = m_new;
         if (__any(alpha != 1.0f)) {
+          l_acc[g2] *= alpha;
 #pragma unroll
           for (int j = 0; j < DB; ++j) o[j][g2] *= alpha;
         }
@@ -522,6 +542,8 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
           o[j][0] = mfma16(a[j], pop[0][ks], o[j][0], O{});
           o[j][1] = mfma16(a[j], pop[1][ks], o[j][1], O{});
         }
+        l_acc[0] = mfma16(ones, pop[0][ks], l_acc[0], O{});
+        l_acc[1] = mfma16(ones, pop[1][ks], l_acc[1], O{});
       }
     }
     if (more) {
@@ -538,7 +560,8 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
 #pragma unroll
   for (int g2 = 0; g2 < 2; ++g2) {
     if (!live[g2]) continue;
-    const float inv = l_run[g2] > 0.0f ? 1.0f / l_run[g2] : 0.0f;
+    const float l = l_acc[g2][0];
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     T* orow = out + (static_cast<int64_t>(q_start + wrow0 + 16 * g2 + n) * hq + head) * D;
 #pragma unroll
     for (int j = 0; j < DB; ++j)
