@@ -12,12 +12,10 @@
  *   - Return 0 on success; KVQ_ERR_* (< 0) for rejected arguments; a positive
  *     hipError_t if the launch failed.  Nothing is launched when an argument
  *     is rejected.
- *   - Calls are asynchronous on `stream` and thread-safe.  The only state
- *     the library keeps is per device and created on first use: cached
- *     device limits (LDS per workgroup, resident workgroups per kernel) and,
- *     for kvq_kivi_decode_attn, a side stream with two events onto which the
- *     tail items fork from `stream` and from which `stream` joins back before
- *     the combine (the fork/join is serialized by a mutex).
+ *   - Calls are asynchronous on `stream`, run entirely on it, and are
+ *     thread-safe.  The only state the library keeps is per device: cached
+ *     device limits (LDS per workgroup, resident workgroups per kernel),
+ *     filled on first use.
  *
  * Reference paths are relative to /root/reference with
  * pkg/ = src/vllm_ascend_quantized_kv_cache/; each entry point names the

@@ -255,6 +255,39 @@ def test_decode_attention_matches_oracle(gpu_device, d, kvh, g, bs, rep):
         torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("kvh,g,bs,rep", [
+    (8, 32, 64, 8),     # workgroup kernel, 32-token tiles, 4 value groups per token
+    (16, 64, 128, 2),   # two workgroups per item (head groups 0-7, 8-15)
+    (8, 128, 256, 7),
+    (8, 128, 128, 12),  # GQA group above 8: per-wave kernel (two score MFMAs)
+    (4, 64, 128, 8),    # kv heads not a multiple of 8: per-wave kernel
+])
+def test_decode_head_group_geometries(gpu_device, kvh, g, bs, rep):
+    """Decode over the workgroup (shared value rows) and per-wave kernel forms."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import DecodeSeq, kivi_decode_attention
+
+    d = 128
+    r_len = 2 * g if g <= 64 else g
+    lens = [r_len * 9 + 3, r_len + 5, r_len * 5]
+    cpu, table, ring_k, ring_v, seqs, wk, wv, _, _ = _ring_case(
+        gpu_device, d, kvh, g, bs, r_len, lens, seed=21, ring_dtype=torch.bfloat16
+    )
+    hq = kvh * rep
+    q = torch.randn(len(lens), hq, d, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    scale = d ** -0.5
+    dk, dv = ref.dequant_gather(*cpu, table, torch.tensor(lens), torch.float32, g)
+    dk = ref.overlay_residual(dk, lens, wk)
+    dv = ref.overlay_residual(dv, lens, wv)
+    want = ref.attention(q, dk, dv, [1] * len(lens), lens, scale, causal=True)
+    dseqs = [DecodeSeq(n, hk, hv, row, ks_, vs_) for (n, hk, hv, row, ks_, vs_) in seqs]
+    for split in (None, 256):
+        got = kivi_decode_attention(
+            q.to(gpu_device), to_dev(cpu, gpu_device), table.to(gpu_device), dseqs,
+            ring_k.to(gpu_device), ring_v.to(gpu_device), scale, g, split_tokens=split,
+        )
+        torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
+
+
 def test_mfma_lane_layout(gpu_device):
     """The 16x16x32 f16 MFMA lane mapping the decode kernels assume."""
     from vllm_ascend_quantized_kv_cache.ops import _native

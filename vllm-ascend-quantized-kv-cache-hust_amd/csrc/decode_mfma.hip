@@ -34,6 +34,7 @@
 //   (value minima) is accumulated in fp32 and added at the end.
 // Online softmax in the log2 domain; each work item leaves (m, l, o) per head
 // for the log-sum-exp combine.
+#include "decode_tail.h"
 #include "kvq_common.h"
 #include "kvq_decode.h"
 
@@ -160,10 +161,11 @@ struct Tile {
   static constexpr int NJJ = CPG / 2;   // PV MFMAs per column group (NVG * NJJ == 8)
   static constexpr int PVS = CPG / 4;   // PV k-steps (32 tokens) per tile
   static constexpr int KW = 0;
-  static constexpr int VW = KW + D * CPG;
-  static constexpr int KS = VW + GT * 16;
+  static constexpr int KS = KW + D * CPG;
   static constexpr int KM = KS + D;
-  static constexpr int VS = KM + D;
+  static constexpr int KEY_WORDS = KM + D;  // the key part: a wave's own region
+  static constexpr int VW = KEY_WORDS;
+  static constexpr int VS = VW + GT * 16;
   static constexpr int VM = VS + PVS * NVG * 32;
   static constexpr int WORDS = VM + PVS * NVG * 32;
   static constexpr int BYTES = 4 * WORDS;
@@ -176,12 +178,22 @@ struct Tile {
   static_assert(NINST < 64, "vmcnt range");
 };
 
+// tk = tile_token(st, kg, i): the token of PV slot 8*kg + i in k-step st, the
+// one whose p the lane already holds from the score layout (score row
+// mr = 4*kg + i%4 of MFMA jm = 2*st + i/4 is token 8*(mr % CPG) + jm*SUB +
+// mr / CPG).  With i%4 < 4 <= CPG the row splits into a lane part and a
+// constant part, so LDS reads at tk take one lane base and immediate offsets.
+template <int CPG>
+__device__ __forceinline__ int tile_token_lane(int kg) {
+  return 8 * ((4 * kg) % CPG) + (4 * kg) / CPG;
+}
+template <int CPG>
+__device__ __forceinline__ constexpr int tile_token_const(int st, int i) {
+  return 8 * (i % 4) + (2 * st + i / 4) * (16 / CPG);
+}
 template <int CPG>
 __device__ __forceinline__ int tile_token(int st, int kg, int i) {
-  constexpr int SUB = 16 / CPG;
-  const int jm = 2 * st + i / 4;
-  const int mr = 4 * kg + (i % 4);
-  return 8 * (mr % CPG) + jm * SUB + mr / CPG;
+  return tile_token_lane<CPG>(kg) + tile_token_const<CPG>(st, i);
 }
 
 // Offsets of DMA lane e = 64*i + lane for the gathered scale/min regions.
@@ -215,35 +227,47 @@ __device__ __forceinline__ LaneDma lane_dma(int lane, int wpd, int kvh, int gpb,
   return ld;
 }
 
-// DMA of one tile.  kq_t, vq_t, ks_t, km_t, vs_t, vm_t point at the tile's
-// first word/scale of kv head h (page blk, token offset off0, key group grp);
-// every lane address stays inside the tile's rows of that page.
+// DMA of one tile's key words and key scale/min for kv head h into the
+// wave's key region `buf`.  kq_t, ks_t, km_t point at the tile's first word /
+// scale (page blk, token offset off0, key group grp); every lane address stays
+// inside the tile's rows of that page.
 template <int CPG>
-__device__ __forceinline__ void issue_tile(char* buf, const LaneDma& ld, const uint32_t* kq_t,
-                                           int wpd, const uint32_t* vq_t, int kvh,
-                                           const float* ks_t, const float* km_t, int gpb,
-                                           const float* vs_t, const float* vm_t, int ng, int g) {
+__device__ __forceinline__ void issue_keys(char* buf, const LaneDma& ld, const uint32_t* kq_t,
+                                           int wpd, const float* ks_t, const float* km_t,
+                                           int gpb) {
   using T = Tile<CPG>;
   constexpr int LPR = CPG / 4;
   constexpr int DPI = 64 / LPR;  // key dim rows per instruction
   const char* kb = reinterpret_cast<const char*>(kq_t);
-  const char* vb = reinterpret_cast<const char*>(vq_t);
   const char* sb = reinterpret_cast<const char*>(ks_t);
   const char* mb = reinterpret_cast<const char*>(km_t);
-  const char* vsb = reinterpret_cast<const char*>(vs_t);
-  const char* vmb = reinterpret_cast<const char*>(vm_t);
 #pragma unroll
   for (int i = 0; i < T::KW_INST; ++i)
     dma16(kb + 4 * (i * DPI * wpd) + ld.k, buf + 4 * T::KW + 1024 * i);
-#pragma unroll
-  for (int i = 0; i < T::VW_INST; ++i)
-    dma16(vb + 4 * (16 * i * kvh * 16) + ld.v, buf + 4 * T::VW + 1024 * i);
 #pragma unroll
   for (int i = 0; i < T::KS_INST; ++i) {
     const int o = 4 * key_scale_off<CPG>(64 * i, gpb);
     dma4(sb + o + ld.ks, buf + 4 * (T::KS + 64 * i));
     dma4(mb + o + ld.ks, buf + 4 * (T::KM + 64 * i));
   }
+}
+
+// DMA of one whole tile (keys and the gathered value operands) for kv head h
+// into the wave's tile buffer; vq_t, vs_t, vm_t point at the tile's first value
+// word / scale of head h.
+template <int CPG>
+__device__ __forceinline__ void issue_tile(char* buf, const LaneDma& ld, const uint32_t* kq_t,
+                                           int wpd, const uint32_t* vq_t, int kvh,
+                                           const float* ks_t, const float* km_t, int gpb,
+                                           const float* vs_t, const float* vm_t, int ng, int g) {
+  using T = Tile<CPG>;
+  issue_keys<CPG>(buf, ld, kq_t, wpd, ks_t, km_t, gpb);
+  const char* vb = reinterpret_cast<const char*>(vq_t);
+  const char* vsb = reinterpret_cast<const char*>(vs_t);
+  const char* vmb = reinterpret_cast<const char*>(vm_t);
+#pragma unroll
+  for (int i = 0; i < T::VW_INST; ++i)
+    dma16(vb + 4 * (16 * i * kvh * 16) + ld.v, buf + 4 * T::VW + 1024 * i);
 #pragma unroll
   for (int i = 0; i < T::VS_INST; ++i) {
     const int o = 4 * value_scale_off<CPG>(64 * i, kvh, ng, g);
@@ -264,6 +288,29 @@ __device__ __forceinline__ void read8f(const uint32_t* p, float (&f)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) f[i] = __uint_as_float(w[i]);
 }
+
+// The value operands of one tile as the PV step reads them: the wave's
+// gathered copy (VW [token][16 words]; VS, VM in PV-slot order, 8 consecutive
+// floats per lane and step), resolved to the lane (kg, chunk) once so that
+// each read is a base plus an immediate offset.
+template <int CPG>
+struct WaveValues {
+  const uint32_t* vw;  // VW + 16 * tile_token_lane(kg) + chunk
+  const uint32_t* sm;  // the tile + 8 * kg
+  __device__ __forceinline__ WaveValues(const uint32_t* W, int kg, int chunk)
+      : vw(W + Tile<CPG>::VW + 16 * tile_token_lane<CPG>(kg) + chunk), sm(W + 8 * kg) {}
+  __device__ __forceinline__ void scales(int st, int v, float (&sc)[8], float (&mn)[8]) const {
+    using T = Tile<CPG>;
+    const int base = (st * T::NVG + v) * 32;
+    read8f(sm + T::VS + base, sc);
+    read8f(sm + T::VM + base, mn);
+  }
+  __device__ __forceinline__ void words(int st, int v, uint32_t (&w)[8]) const {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = vw[16 * tile_token_const<CPG>(st, i) + CPG * v];
+  }
+};
+
 
 // fp16 pair of nibbles from two words: byte `sel` of lo and of hi, the nibble
 // picked by `mask` (0x000f000f: low nibble -> 1024 + c; 0x00f000f0: high
@@ -307,6 +354,9 @@ struct LaneNib {
 
 // The lane's 32 query values (dims 32*s4 + 4*ii + kg) kept as 16 packed
 // pairs for 16-bit inputs (pair 4*s4 + p = elements 2p, 2p+1 of k-step s4).
+// The widening is volatile asm: it stays where the values are used (once per
+// key group) instead of being hoisted out of the tile loop as 32 live fp32
+// registers.
 template <typename TQ>
 struct QRegs {
   uint32_t w[16];
@@ -314,13 +364,35 @@ struct QRegs {
     w[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
   }
-  __device__ __forceinline__ float lo(int i) const {
-    return to_f32(__builtin_bit_cast(TQ, static_cast<uint16_t>(w[i] & 0xffffu)));
-  }
-  __device__ __forceinline__ float hi(int i) const {
-    return to_f32(__builtin_bit_cast(TQ, static_cast<uint16_t>(w[i] >> 16)));
-  }
+  __device__ __forceinline__ float lo(int i) const;
+  __device__ __forceinline__ float hi(int i) const;
 };
+template <>
+__device__ __forceinline__ float QRegs<bf16>::lo(int i) const {
+  float r;
+  asm volatile("v_lshlrev_b32 %0, 16, %1" : "=v"(r) : "v"(w[i]));
+  return r;
+}
+template <>
+__device__ __forceinline__ float QRegs<bf16>::hi(int i) const {
+  float r;
+  asm volatile("v_and_b32 %0, 0xffff0000, %1" : "=v"(r) : "v"(w[i]));
+  return r;
+}
+template <>
+__device__ __forceinline__ float QRegs<f16>::lo(int i) const {
+  float r;  // fp16 -> fp32 is exact: x * 1.0 + 0.0 in the mixed-precision fma
+  asm volatile("v_fma_mix_f32 %0, %1, 1.0, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w[i]));
+  return r;
+}
+template <>
+__device__ __forceinline__ float QRegs<f16>::hi(int i) const {
+  float r;
+  asm volatile("v_fma_mix_f32 %0, %1, 1.0, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+               : "=v"(r)
+               : "v"(w[i]));
+  return r;
+}
 template <>
 struct QRegs<float> {
   float w[32];
@@ -335,14 +407,19 @@ struct QRegs<float> {
 // B operands of one key group: Q' = q * key_scale(dim, group) as hi/lo fp16
 // pairs for the 4 k-steps, and the minima term kb = sum_d q * mn (times the
 // softmax scale).  Shared by the group's tiles (two 64-token tiles at G = 128).
+//
+// Folded form (GQA groups of at most 8 heads): columns n and n + 8 both carry
+// head n % 8, column n < 8 with the hi part and column n + 8 with the lo part
+// in bq, so one MFMA per k-step gives both partial scores and a rotate-by-8
+// add within each 16-lane row sums them (bl unused).
 struct QGroup {
   h8 bq[4], bl[4];
   float kb;
 };
 
-template <typename TQ, int CPG>
-__device__ __forceinline__ void prepare_group(const uint32_t* W, int kg, const QRegs<TQ>& qv,
-                                              float qscale, QGroup& qg) {
+template <typename TQ, int CPG, bool FOLD>
+__device__ __forceinline__ void prepare_group(const uint32_t* W, int n, int kg,
+                                              const QRegs<TQ>& qv, float qscale, QGroup& qg) {
 #pragma clang fp contract(fast)
   using T = Tile<CPG>;
   float kb = 0.0f;
@@ -359,15 +436,29 @@ __device__ __forceinline__ void prepare_group(const uint32_t* W, int kg, const Q
       split_h2(f2{q0 * sc[2 * p], q1 * sc[2 * p + 1]}, qh[p], ql[p]);
       kb += q0 * mn[2 * p] + q1 * mn[2 * p + 1];
     }
-    qg.bq[s4] = as_h8(qh[0], qh[1], qh[2], qh[3]);
-    qg.bl[s4] = as_h8(ql[0], ql[1], ql[2], ql[3]);
+    if (FOLD) {
+      const bool lo_col = n >= 8;
+      qg.bq[s4] = as_h8(lo_col ? ql[0] : qh[0], lo_col ? ql[1] : qh[1], lo_col ? ql[2] : qh[2],
+                        lo_col ? ql[3] : qh[3]);
+    } else {
+      qg.bq[s4] = as_h8(qh[0], qh[1], qh[2], qh[3]);
+      qg.bl[s4] = as_h8(ql[0], ql[1], ql[2], ql[3]);
+    }
   }
   qg.kb = sum_kg(kb) * qscale;
 }
 
-// One tile of scores, softmax update and PV.  FULL: every token < pe.
-template <typename TQ, int CPG, bool FULL>
-__device__ __forceinline__ void compute_tile(const uint32_t* W, int p0, int pe, int n, int kg,
+// x + (x of lane n ^ 8 in the same 16-lane row): v_add_f32 with a DPP
+// row_ror:8 operand.
+__device__ __forceinline__ float add_ror8(float x) {
+  const int y = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false);
+  return x + __int_as_float(y);
+}
+
+// One tile of scores, softmax update and PV.  FULL: every token < pe.  W is
+// the wave's key region; `vals` reads the tile's value operands.
+template <typename TQ, int CPG, bool FULL, bool FOLD, typename VALS>
+__device__ __forceinline__ void compute_tile(const uint32_t* W, const VALS& vals, int p0, int pe, int n, int kg,
                                              const QGroup& qg, float qscale,
                                              const LaneNib<CPG>& ln, float& m_run, float& l_run, f4 (&o_acc)[8],
                                              f4 (&c_acc)[16 / CPG], float (&bias_v)[16 / CPG]) {
@@ -397,9 +488,16 @@ __device__ __forceinline__ void compute_tile(const uint32_t* W, int p0, int pe, 
                          nib_pair_exact(w[4], w[5], sel, ln.maskk),
                          nib_pair_exact(w[6], w[7], sel, ln.maskk));
       sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qg.bq[s4], sacc[jm], 0, 0, 0);
-      sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qg.bl[s4], sacc[jm], 0, 0, 0);
+      if (!FOLD)
+        sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qg.bl[s4], sacc[jm], 0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the k-steps' live ranges apart
+  }
+  if (FOLD) {
+#pragma unroll
+    for (int jm = 0; jm < T::NJ; ++jm)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sacc[jm][r] = add_ror8(sacc[jm][r]);
   }
   const float kb = qg.kb;
   // softmax scale * log2(e), and 1/16 on the rows read as 16c
@@ -453,10 +551,8 @@ __device__ __forceinline__ void compute_tile(const uint32_t* W, int p0, int pe, 
     for (int i = 0; i < 8; ++i) pv[i] = sacc[2 * st + i / 4][i % 4];
 #pragma unroll
     for (int v = 0; v < T::NVG; ++v) {
-      const int base = ((st * T::NVG + v) * 4 + kg) * 8;
       float sc[8], mn[8];
-      read8f(W + T::VS + base, sc);
-      read8f(W + T::VM + base, mn);
+      vals.scales(st, v, sc, mn);
       float pp[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -475,11 +571,7 @@ __device__ __forceinline__ void compute_tile(const uint32_t* W, int p0, int pe, 
                          pack_h2(pp[6], pp[7]));
       c_acc[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ones_b, c_acc[v], 0, 0, 0);
       uint32_t w[8];  // word chunk + CPG*v of tokens tk(st, kg, i)
-      {
-        const uint32_t* vw = W + T::VW + chunk + CPG * v;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = vw[16 * tile_token<CPG>(st, kg, i)];
-      }
+      vals.words(st, v, w);
 #pragma unroll
       for (int jj = 0; jj < T::NJJ; ++jj) {
         const uint32_t sel = ln.selv[jj];
@@ -493,27 +585,148 @@ __device__ __forceinline__ void compute_tile(const uint32_t* W, int p0, int pe, 
   }
 }
 
-template <typename TQ, int CPG>
+// q of head n (n % 8 when folded) of kv head h's GQA group for dims 32*s4 + 4*ii + kg, in the
+// input dtype (the softmax scale is applied to the fp32 scores).  Lanes past
+// the group read head 0's row (always valid) and zero it.
+template <typename TQ, bool FOLD>
+__device__ __forceinline__ QRegs<TQ> load_q(const TQ* __restrict__ query, int b, int hq, int h,
+                                            int rep, int n, int kg) {
+  constexpr int D = 128;
+  QRegs<TQ> qv;
+  const int hn = FOLD ? (n & 7) : n;  // folded: columns n and n + 8 carry head n % 8
+  const bool live = hn < rep;
+  const TQ* qrow = query + (static_cast<int64_t>(b) * hq + h * rep + (live ? hn : 0)) * D;
+  const TQ zero = from_f32<TQ>(0.0f);
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const TQ lo = qrow[32 * s4 + 8 * p + kg];
+      const TQ hi = qrow[32 * s4 + 8 * p + 4 + kg];
+      qv.set(4 * s4 + p, live ? lo : zero, live ? hi : zero);
+    }
+  return qv;
+}
+
+// The item's page ids, one per lane (lane i: page pg0 + i), loaded once per
+// 64 pages rather than read from the table in front of every tile's DMA.  Page
+// ids are clamped into [0, nb): the host validates live ids, the clamp only
+// guarantees that no DMA can leave the cache whatever the table holds.
+struct PageIds {
+  const int32_t* bt;
+  int64_t maxb, nb;
+  int bs, pg0, pg_last, lane, vec;
+  __device__ __forceinline__ PageIds(const int32_t* bt_, int64_t maxb_, int64_t nb_, int bs_,
+                                     int pb, int pe, int lane_)
+      : bt(bt_), maxb(maxb_), nb(nb_), bs(bs_), pg0(pb / bs_), pg_last((pe - 1) / bs_),
+        lane(lane_), vec(0) {
+    if (pb < pe) vec = load();
+  }
+  __device__ __forceinline__ int load() const {
+    const int pg = pg0 + lane;
+    const int64_t b0 = pg <= pg_last && pg < maxb ? bt[pg] : 0;
+    return static_cast<int>(b0 < 0 ? 0 : (b0 >= nb ? nb - 1 : b0));
+  }
+  // page of position p; positions only move forward, one tile (<= one page)
+  // at a time
+  __device__ __forceinline__ int64_t page(int p) {
+    if (p / bs - pg0 >= 64) {  // uniform; only items longer than 64 pages get here
+      pg0 += 64;
+      vec = load();
+    }
+    return __builtin_amdgcn_readlane(vec, p / bs - pg0);
+  }
+};
+
+// Running state of one wave: softmax max / sum (log2 domain), the PV
+// accumulators (codes read as 1024 + c or 1024 + 16c), the constant-B MFMA
+// sums that remove the 1024 offset, and the value-minima term per column group.
+template <int CPG>
+struct WaveAcc {
+  static constexpr int NVG = 16 / CPG;
+  float m_run, l_run;
+  f4 o_acc[8];
+  f4 c_acc[NVG];
+  float bias_v[NVG];
+  __device__ __forceinline__ void init() {
+    m_run = -INFINITY;
+    l_run = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) o_acc[q] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < NVG; ++v) {
+      c_acc[v] = f4{0.f, 0.f, 0.f, 0.f};
+      bias_v[v] = 0.0f;
+    }
+  }
+  // Epilogue: remove the PV offset, undo the 16x columns, add the minima, and
+  // write the item's (o, m, l) for heads 0..rep-1 of the group.
+  __device__ __forceinline__ void store(const LaneNib<CPG>& ln, int wi, int hq, int h, int rep,
+                                        int n, int kg, float* __restrict__ ws_o,
+                                        float* __restrict__ ws_ml) {
+    constexpr int D = 128;
+    constexpr int NJJ = CPG / 2;
+    constexpr int SUB = 16 / CPG;
+#pragma unroll
+    for (int v = 0; v < NVG; ++v) bias_v[v] = sum_kg(bias_v[v]);
+    const int64_t head0 = static_cast<int64_t>(wi) * hq + h * rep;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int hh = 4 * kg + r;
+#pragma unroll
+      for (int v = 0; v < NVG; ++v) {
+        const float bv = __shfl(bias_v[v], hh, 64);
+#pragma unroll
+        for (int jj = 0; jj < NJJ; ++jj) {
+          const int dim = 8 * (n % CPG + CPG * v) + jj * SUB + n / CPG;
+          if (hh < rep)
+            ws_o[(head0 + hh) * D + dim] =
+                (o_acc[v * NJJ + jj][r] - c_acc[v][r]) * ln.col_scale + bv;
+        }
+      }
+    }
+    if (kg == 0 && n < rep) {
+      ws_ml[2 * (head0 + n)] = m_run;
+      ws_ml[2 * (head0 + n) + 1] = l_run;
+    }
+  }
+};
+
+// TAIL: the grid covers the work items twice; the first pass takes the int4
+// (kind-0) items, the second the tail (kind-1) items, so every tail wave is
+// dispatched after every int4 wave and runs in the slots the shorter int4
+// items free, with no second stream or event between the two.
+template <typename TQ, int CPG, bool FOLD, bool TAIL>
 __global__ void __launch_bounds__(64, 2)
 kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qscale,
                         const uint32_t* __restrict__ kq, const float* __restrict__ ks,
                         const float* __restrict__ km, const uint32_t* __restrict__ vq,
                         const float* __restrict__ vs, const float* __restrict__ vm, int bs,
                         int g, int64_t nb, const int32_t* __restrict__ block_table,
-                        int64_t maxb, const int32_t* __restrict__ work, int64_t num_work,
-                        float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+                        int64_t maxb, const int32_t* __restrict__ seq_meta,
+                        const int32_t* __restrict__ work, int64_t num_work,
+                        const TQ* __restrict__ ring_k, const TQ* __restrict__ ring_v,
+                        int ring_len, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   using T = Tile<CPG>;
   constexpr int D = T::D;
   constexpr int GT = T::GT;
-  constexpr int NVG = T::NVG;
-  constexpr int NJJ = T::NJJ;
 
   extern __shared__ __align__(16) char lds_raw[];
   int wi, h;
-  if (!xcd_item_head(blockIdx.x, kvh, num_work, wi, h)) return;
+  const int64_t pass_len = xcd_grid_size(num_work, kvh);
+  const int pass = TAIL && blockIdx.x >= pass_len ? 1 : 0;
+  if (!xcd_item_head(blockIdx.x - pass * pass_len, kvh, num_work, wi, h)) return;
   const int lane = threadIdx.x;
   const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
-  if (wk[3] != 0) return;  // kind-1 items belong to the tail kernel (uniform)
+  if (wk[3] != pass) return;  // the other pass (or the tail kernel) owns it (uniform)
+  if constexpr (TAIL) {
+    if (pass == 1) {
+      tail::tail_item<TQ>(lds_raw, query, hq, kvh, qscale, kq, ks, km, vq, vs, vm, bs, g, nb,
+                          block_table, maxb, seq_meta, wk, wi, h, ring_k, ring_v, ring_len,
+                          ws_o, ws_ml);
+      return;
+    }
+  }
   const int b = wk[0];
   const int pb = wk[1];
   const int pe = wk[2];
@@ -523,46 +736,16 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   const int gpb = bs / g;
   const int ng = D / g;
   const int wpd = bs / 8;
-  const int32_t* bt = block_table + static_cast<int64_t>(b) * maxb;
 
-  // q of head n for dims 32*s4 + 4*ii + kg in the input dtype (the softmax
-  // scale is applied to the fp32 scores).  Lanes past the GQA group read head
-  // 0's row (always valid) and zero it.
-  QRegs<TQ> qv;
-  {
-    const bool live = n < rep;
-    const TQ* qrow = query + (static_cast<int64_t>(b) * hq + h * rep + (live ? n : 0)) * D;
-    const TQ zero = from_f32<TQ>(0.0f);
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4)
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const TQ lo = qrow[32 * s4 + 8 * p + kg];
-        const TQ hi = qrow[32 * s4 + 8 * p + 4 + kg];
-        qv.set(4 * s4 + p, live ? lo : zero, live ? hi : zero);
-      }
-  }
+  const QRegs<TQ> qv = load_q<TQ, FOLD>(query, b, hq, h, rep, n, kg);
   const LaneNib<CPG> ln(n, kg);
   const LaneDma ld = lane_dma<CPG>(lane, wpd, kvh, gpb, ng, g);
 
-  float m_run = -INFINITY;
-  float l_run = 0.0f;
-  f4 o_acc[8];
-  f4 c_acc[NVG];
-  float bias_v[NVG];
-#pragma unroll
-  for (int q = 0; q < 8; ++q) o_acc[q] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int v = 0; v < NVG; ++v) {
-    c_acc[v] = f4{0.f, 0.f, 0.f, 0.f};
-    bias_v[v] = 0.0f;
-  }
-
-  // page ids are clamped into [0, nb): the host validates live ids, the clamp
-  // only guarantees that no DMA can leave the cache whatever the table holds
+  WaveAcc<CPG> acc;
+  acc.init();
+  PageIds pages(block_table + static_cast<int64_t>(b) * maxb, maxb, nb, bs, pb, pe, lane);
   auto issue = [&](char* buf, int p) {
-    const int64_t b0 = bt[p / bs];
-    const int64_t blk = b0 < 0 ? 0 : (b0 >= nb ? nb - 1 : b0);
+    const int64_t blk = pages.page(p);
     const int off0 = p % bs;
     const int64_t krow = (blk * kvh + h) * D;
     const int64_t vtok = (blk * bs + off0) * kvh + h;
@@ -588,13 +771,16 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
     const uint32_t* W = reinterpret_cast<const uint32_t*>(cur);
     // tiles are GT-aligned and GT divides g: a tile starts a key group or
     // continues the previous tile's
-    if (p0 == pb || p0 % g == 0) prepare_group<TQ, CPG>(W, kg, qv, qscale, qg);
+    if (p0 == pb || p0 % g == 0) prepare_group<TQ, CPG, FOLD>(W, n, kg, qv, qscale, qg);
+    const WaveValues<CPG> vals(W, kg, n % CPG);
     if (p0 + GT <= pe)
-      compute_tile<TQ, CPG, true>(W, p0, pe, n, kg, qg, qscale, ln, m_run, l_run, o_acc, c_acc, bias_v);
+      compute_tile<TQ, CPG, true, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run, acc.l_run,
+                                  acc.o_acc, acc.c_acc, acc.bias_v);
     else
-      compute_tile<TQ, CPG, false>(W, p0, pe, n, kg, qg, qscale, ln, m_run, l_run, o_acc, c_acc, bias_v);
+      compute_tile<TQ, CPG, false, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run, acc.l_run,
+                                   acc.o_acc, acc.c_acc, acc.bias_v);
   };
-  issue(lds_raw, pb);  // prologue: tile 0 into buffer 0
+  if (pb < pe) issue(lds_raw, pb);  // prologue: tile 0 into buffer 0
   int cur = 0;
   for (int p0 = pb; p0 < pe; p0 += GT) {
     step(lds_raw + cur * T::BYTES, lds_raw + (cur ^ 1) * T::BYTES, p0);
@@ -603,30 +789,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
     asm volatile("" ::: "memory");
     cur ^= 1;
   }
-
-  // ---- epilogue: remove the PV offset, undo the 16x columns, add the minima ----
-#pragma unroll
-  for (int v = 0; v < NVG; ++v) bias_v[v] = sum_kg(bias_v[v]);
-  const int64_t head0 = static_cast<int64_t>(wi) * hq + h * rep;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int hh = 4 * kg + r;
-#pragma unroll
-    for (int v = 0; v < NVG; ++v) {
-      const float bv = __shfl(bias_v[v], hh, 64);
-#pragma unroll
-      for (int jj = 0; jj < NJJ; ++jj) {
-        const int dim = 8 * (n % CPG + CPG * v) + jj * T::SUB + n / CPG;
-        if (hh < rep)
-          ws_o[(head0 + hh) * D + dim] =
-              (o_acc[v * NJJ + jj][r] - c_acc[v][r]) * ln.col_scale + bv;
-      }
-    }
-  }
-  if (kg == 0 && n < rep) {
-    ws_ml[2 * (head0 + n)] = m_run;
-    ws_ml[2 * (head0 + n) + 1] = l_run;
-  }
+  acc.store(ln, wi, hq, h, rep, n, kg, ws_o, ws_ml);
 }
 
 // Copies 1 KiB with 16-byte DMA lanes and 256 B with 4-byte DMA lanes through
@@ -669,33 +832,54 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
                             const int32_t* kq, const float* ks, const float* km,
                             const int32_t* vq, const float* vs, const float* vm, int bs, int g,
                             int64_t nb, const int32_t* block_table, int64_t maxb,
-                            const int32_t* seq_meta,
-                            const int32_t* work, int64_t num_work, float* ws_o, float* ws_ml,
-                            hipStream_t s, bool* launched) {
-  (void)seq_meta;
+                            const int32_t* seq_meta, const int32_t* work, int64_t num_work,
+                            const void* ring_k, const void* ring_v, int ring_dtype, int ring_len,
+                            float* ws_o, float* ws_ml, hipStream_t s, bool* launched,
+                            bool* tail_done) {
   *launched = false;
+  *tail_done = false;
   if (d != 128 || hq / kvh > 16 || g % 8 || d % g || g < 32 || g > 128) return KVQ_OK;
   // tiles of 64 tokens (32 for G = 32): inside one key group and one page
   const int cpg = g >= 64 ? 8 : 4;
   if (bs % (8 * cpg)) return KVQ_OK;
-  const dim3 grid(static_cast<unsigned>(xcd_grid_size(num_work, kvh)));
-  const dim3 block(64);
   const uint32_t* kqu = reinterpret_cast<const uint32_t*>(kq);
   const uint32_t* vqu = reinterpret_cast<const uint32_t*>(vq);
-#define KVQ_LAUNCH_MFMA(C)                                                                   \
-  KVQ_DISPATCH_FLOAT(q_dtype, TQ,                                                           \
-    hipLaunchKernelGGL((kivi_decode_mfma_kernel<TQ, C>), grid, block,                       \
-                       2 * Tile<C>::BYTES, s, static_cast<const TQ*>(query), hq, kvh, \
-                       qscale, kqu, ks, km, vqu, vs, vm, bs, g, nb, block_table, maxb, work,\
-                       num_work, ws_o, ws_ml))
-  if (cpg == 8) {
-    KVQ_LAUNCH_MFMA(8);
-  } else {
-    KVQ_LAUNCH_MFMA(4);
+  const int64_t pass_len = xcd_grid_size(num_work, kvh);
+  const bool tail = tail_path_applies(q_dtype, hq, kvh, d, ring_dtype);
+  if ((tail ? 2 : 1) * pass_len > 0x7fffffff) return KVQ_ERR_INVALID;
+  const dim3 grid(static_cast<unsigned>((tail ? 2 : 1) * pass_len));
+  const dim3 block(64);
+  // GQA groups of at most 8 heads fold the hi/lo score parts into one MFMA
+  const bool fold = hq / kvh <= 8;
+  const size_t lds_int4 = 2 * static_cast<size_t>(cpg == 8 ? Tile<8>::BYTES : Tile<4>::BYTES);
+  const size_t lds_tail = static_cast<size_t>(tail::kLdsBytes);
+  const size_t lds = tail && lds_tail > lds_int4 ? lds_tail : lds_int4;
+#define KVQ_LAUNCH_MFMA(TQ, C, F, TL)                                                         \
+  hipLaunchKernelGGL((kivi_decode_mfma_kernel<TQ, C, F, TL>), grid, block, lds, s,           \
+                     static_cast<const TQ*>(query), hq, kvh, qscale, kqu, ks, km, vqu, vs, vm,\
+                     bs, g, nb, block_table, maxb, seq_meta, work, num_work,                 \
+                     static_cast<const TQ*>(ring_k), static_cast<const TQ*>(ring_v),         \
+                     ring_len, ws_o, ws_ml)
+#define KVQ_LAUNCH_MFMA_CF(TQ, TL)                                                            \
+  if (cpg == 8) {                                                                             \
+    if (fold) KVQ_LAUNCH_MFMA(TQ, 8, true, TL); else KVQ_LAUNCH_MFMA(TQ, 8, false, TL);      \
+  } else {                                                                                    \
+    if (fold) KVQ_LAUNCH_MFMA(TQ, 4, true, TL); else KVQ_LAUNCH_MFMA(TQ, 4, false, TL);      \
   }
+  if (tail && q_dtype == KVQ_DTYPE_BF16) {
+    KVQ_LAUNCH_MFMA_CF(bf16, true);
+  } else if (tail) {
+    KVQ_LAUNCH_MFMA_CF(f16, true);
+  } else {
+    // without the tail pass the ring pointers are never read; they fill the
+    // parameters in the query dtype
+    KVQ_DISPATCH_FLOAT(q_dtype, TQ, KVQ_LAUNCH_MFMA_CF(TQ, false));
+  }
+#undef KVQ_LAUNCH_MFMA_CF
 #undef KVQ_LAUNCH_MFMA
   KVQ_LAUNCH_CHECK();
   *launched = true;
+  *tail_done = tail;
   return KVQ_OK;
 }
 

@@ -1,0 +1,345 @@
+// SPDX-License-Identifier: Apache-2.0
+// Decode attention over the mixed-source tail of one request (a kind-1 work
+// item), for one kv head, on one wave: the tail path of the int4 decode kernel.
+//
+// A request's tail is the positions past min(k_hist, v_hist): keys there are
+// int4 (below k_hist) or residual-ring rows, values are ring rows.  The wave
+// walks its item (at most 64 positions) in sub-tiles of kTT = 32 positions:
+//   * stages the sub-tile's K as [token][dim] in the activation dtype T: int4
+//     history is dequantized (q*scale then +mn in fp32, the reference's gather
+//     arithmetic, pkg/methods/kivi_int4/attention_backend.py:849-935) and kept
+//     as two T parts, hi = T(k) and lo = T(k - hi); ring rows are copied with
+//     lo = 0.  A key rounded to bf16 alone moves the score of an outlier
+//     channel (key scale ~20) by ~1e-2, which the softmax carries into the
+//     output, while hi + lo keeps ~16 bits;
+//   * S^T = (K_hi + K_lo) * Q^T with v_mfma_f32_16x16x32_{bf16,f16} on the raw
+//     query (exact products, fp32 accumulation; the softmax scale and log2(e)
+//     are applied to the fp32 scores);
+//   * then stages V transposed as [dim][token] over the same LDS (the keys are
+//     consumed by then) and computes O = P * V with P split into two T parts
+//     (hi + lo), so p keeps ~16 bits;
+//   * leaves (m, l, o) per head in the split-K workspace for the combine.
+// LDS: 2 * kTT * kKP * 2 bytes = 17 KiB, inside the int4 path's 20 KiB per wave.
+#pragma once
+
+#include "kvq_common.h"
+#include "kvq_decode.h"
+
+namespace kvq {
+namespace tail {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u8v __attribute__((ext_vector_type(8)));
+typedef uint16_t u4s __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4 mfma16(u8v a, u8v b, f4 c, bf16) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, a),
+                                                 __builtin_bit_cast(b8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f4 mfma16(u8v a, u8v b, f4 c, f16) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a),
+                                                __builtin_bit_cast(h8, b), c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ uint16_t bits_of(float x) {
+  const T v = from_f32<T>(x);
+  return __builtin_bit_cast(uint16_t, v);
+}
+
+__device__ __forceinline__ float sum_kg(float v) {  // over the 4 lane groups of 16
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+__device__ __forceinline__ float max_kg(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
+__device__ __forceinline__ int64_t clamp_page(const int32_t* __restrict__ bt, int p, int bs,
+                                              int64_t nb) {
+  const int64_t blk = bt[p / bs];
+  return blk < 0 ? 0 : (blk >= nb ? nb - 1 : blk);  // never leave the cache
+}
+
+constexpr int kD = 128;
+constexpr int kTT = 32;          // positions per sub-tile
+constexpr int kKP = kD + 8;      // K row pitch (elements): rows stay 16-byte aligned
+constexpr int kVP = kTT + 4;     // V^T row pitch (elements): 8-byte aligned token quads
+constexpr int kKW = kTT / 8 + 1;  // key words of one dim covering a sub-tile (8-aligned start)
+constexpr int kLdsBytes = 2 * kTT * kKP * 2;
+static_assert(kD * kVP <= 2 * kTT * kKP, "V^T fits the key region it reuses");
+
+// Work item wi (kind 1) for kv head h.  lds_raw: at least kLdsBytes.
+template <typename T>
+__device__ __forceinline__ void tail_item(char* __restrict__ lds_raw, const T* __restrict__ query,
+                                          int hq, int kvh, float qscale,
+                                          const uint32_t* __restrict__ kq,
+                                          const float* __restrict__ ks,
+                                          const float* __restrict__ km,
+                                          const uint32_t* __restrict__ vq,
+                                          const float* __restrict__ vs,
+                                          const float* __restrict__ vm, int bs, int g, int64_t nb,
+                                          const int32_t* __restrict__ block_table, int64_t maxb,
+                                          const int32_t* __restrict__ seq_meta,
+                                          const int32_t* __restrict__ wk, int wi, int h,
+                                          const T* __restrict__ ring_k,
+                                          const T* __restrict__ ring_v, int ring_len,
+                                          float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+  constexpr int D = kD;
+  uint16_t* sk = reinterpret_cast<uint16_t*>(lds_raw);  // [kTT][kKP] key hi parts
+  uint16_t* skl = sk + kTT * kKP;                        // [kTT][kKP] key lo parts
+  uint16_t* svt = sk;                                    // [D][kVP], after the scores
+  const int lane = threadIdx.x & 63;
+  const int b = wk[0];
+  const int pb = wk[1];
+  const int pe = wk[2];
+  const int32_t* sm = seq_meta + 8 * static_cast<int64_t>(b);
+  const int khist = sm[1], vhist = sm[2], row = sm[3], kfirst = sm[4], vfirst = sm[5];
+  const int rep = hq / kvh;
+  const int n = lane & 15;
+  const int kg = lane >> 4;
+  const int gpb = bs / g;
+  const int wpd = bs / 8;
+  const int32_t* bt = block_table + static_cast<int64_t>(b) * maxb;
+  const int64_t ring_row0 = static_cast<int64_t>(row) * ring_len;
+
+  // B operand of QK: q[head n][32*s4 + 8*kg + i], raw (the scale is applied in fp32)
+  u8v qb[4];
+  {
+    const bool live = n < rep;
+    const T* qrow = query + (static_cast<int64_t>(b) * hq + h * rep + (live ? n : 0)) * D;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qrow + 32 * s4 + 8 * kg);
+      qb[s4] = __builtin_bit_cast(u8v, live ? v : make_uint4(0, 0, 0, 0));
+    }
+  }
+
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
+  f4 o_acc[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) o_acc[q] = f4{0.f, 0.f, 0.f, 0.f};
+
+  for (int p0 = pb; p0 < pe; p0 += kTT) {
+    const int nt = (pe - p0) < kTT ? (pe - p0) : kTT;
+    // one wave: its LDS accesses take effect in program order, so the previous
+    // sub-tile's reads are done before these writes
+    // ---- K rows -------------------------------------------------------------
+    {
+      const int mk = khist - p0 < 0 ? 0 : (khist - p0 < nt ? khist - p0 : nt);  // int4 keys
+      if (mk > 0) {
+        // lane = dim: the <= kKW words of the dim covering positions [p0, p0+mk)
+        const int first = p0 & ~7;
+        for (int c = lane; c < D; c += 64) {
+          uint32_t w[kKW];
+          float sc[kKW], mn[kKW];
+#pragma unroll
+          for (int k = 0; k < kKW; ++k) {
+            // clamped into [p0, p0 + mk): every load is valid and unconditional
+            const int p = first + 8 * k;
+            const int pp = p < p0 ? p0 : (p < p0 + mk ? p : p0 + mk - 1);
+            const int64_t r = (clamp_page(bt, pp, bs, nb) * kvh + h) * D + c;
+            const int off = pp % bs;
+            w[k] = kq[r * wpd + off / 8];
+            sc[k] = ks[r * gpb + off / g];
+            mn[k] = km[r * gpb + off / g];
+          }
+#pragma unroll
+          for (int k = 0; k < kKW; ++k) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const int t = first + 8 * k + j - p0;
+              if (t >= 0 && t < mk) {
+                const float x = kivi_dequant((w[k] >> (4 * j)) & 0xfu, sc[k], mn[k]);
+                const T hi = from_f32<T>(x);
+                sk[t * kKP + c] = __builtin_bit_cast(uint16_t, hi);
+                skl[t * kKP + c] = bits_of<T>(x - to_f32(hi));
+              }
+            }
+          }
+        }
+      }
+      // ring keys: task = (position, 16-byte chunk), copied as is
+      const int tasks = (nt - mk) * (D / 8);
+      for (int t0 = 0; t0 < tasks; t0 += 64 * 4) {
+        uint4 x[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int t0k = t0 + 64 * k + lane;
+          const int t = t0k < tasks ? t0k : tasks - 1;  // clamped: unconditional load
+          const int pi = mk + t / (D / 8);
+          const int rl = (kfirst + (p0 + pi - khist)) % ring_len;
+          x[k] = *reinterpret_cast<const uint4*>(ring_k + ((ring_row0 + rl) * kvh + h) * D +
+                                                 8 * (t % (D / 8)));
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int t = t0 + 64 * k + lane;
+          if (t < tasks) {
+            const int pi = mk + t / (D / 8);
+            *reinterpret_cast<uint4*>(sk + pi * kKP + 8 * (t % (D / 8))) = x[k];
+            *reinterpret_cast<uint4*>(skl + pi * kKP + 8 * (t % (D / 8))) = make_uint4(0, 0, 0, 0);
+          }
+        }
+      }
+    }
+    // ---- scores: S^T[token][head] for kTT/16 x 16 tokens ------------------------
+    f4 sacc[kTT / 16];
+#pragma unroll
+    for (int jm = 0; jm < kTT / 16; ++jm) {
+      sacc[jm] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int o = (16 * jm + n) * kKP + 32 * s4 + 8 * kg;
+        const u8v a = *reinterpret_cast<const u8v*>(sk + o);
+        const u8v al = *reinterpret_cast<const u8v*>(skl + o);
+        sacc[jm] = mfma16(a, qb[s4], sacc[jm], T{});
+        sacc[jm] = mfma16(al, qb[s4], sacc[jm], T{});
+      }
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int jm = 0; jm < kTT / 16; ++jm) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pos = p0 + 16 * jm + 4 * kg + r;
+        const float sv = pos < pe ? sacc[jm][r] * qscale : -INFINITY;
+        sacc[jm][r] = sv;
+        tmax = fmaxf(tmax, sv);
+      }
+    }
+    tmax = max_kg(tmax);
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = m_run == -INFINITY ? 0.0f : exp2f(m_run - m_new);
+    float psum = 0.0f;
+#pragma unroll
+    for (int jm = 0; jm < kTT / 16; ++jm) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pr = exp2f(sacc[jm][r] - m_new);
+        sacc[jm][r] = pr;
+        psum += pr;
+      }
+    }
+    l_run = l_run * alpha + sum_kg(psum);
+    m_run = m_new;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float ar = __shfl(alpha, 4 * kg + r, 64);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o_acc[q][r] *= ar;
+    }
+
+    // ---- V rows, stored transposed ----------------------------------------------
+    {
+      const int mv = vhist - p0 < 0 ? 0 : (vhist - p0 < nt ? vhist - p0 : nt);  // int4 values
+      const int nd = D / 8;
+      for (int t0 = 0; t0 < mv * nd; t0 += 64 * 4) {
+        uint32_t w[4];
+        float sc[4], mn[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int t0k = t0 + 64 * k + lane;
+          const int t = t0k < mv * nd ? t0k : mv * nd - 1;  // clamped: unconditional load
+          const int p = p0 + t / nd;
+          const int dv = t % nd;
+          const int64_t vrow = (clamp_page(bt, p, bs, nb) * bs + p % bs) * kvh + h;
+          w[k] = vq[vrow * nd + dv];
+          sc[k] = vs[vrow * (D / g) + (8 * dv) / g];
+          mn[k] = vm[vrow * (D / g) + (8 * dv) / g];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int t = t0 + 64 * k + lane;
+          if (t < mv * nd) {
+            const int pi = t / nd;
+            const int dv = t % nd;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              svt[(8 * dv + i) * kVP + pi] =
+                  bits_of<T>(kivi_dequant((w[k] >> (4 * i)) & 0xfu, sc[k], mn[k]));
+          }
+        }
+      }
+      const int tasks = (nt - mv) * nd;
+      for (int t0 = 0; t0 < tasks; t0 += 64 * 4) {
+        uint4 x[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int t0k = t0 + 64 * k + lane;
+          const int t = t0k < tasks ? t0k : tasks - 1;  // clamped: unconditional load
+          const int pi = mv + t / nd;
+          const int rl = (vfirst + (p0 + pi - vhist)) % ring_len;
+          x[k] = *reinterpret_cast<const uint4*>(ring_v + ((ring_row0 + rl) * kvh + h) * D +
+                                                 8 * (t % nd));
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int t = t0 + 64 * k + lane;
+          if (t < tasks) {
+            const int pi = mv + t / nd;
+            const int dv = t % nd;
+            const uint32_t e[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              svt[(8 * dv + 2 * i) * kVP + pi] = static_cast<uint16_t>(e[i] & 0xffffu);
+              svt[(8 * dv + 2 * i + 1) * kVP + pi] = static_cast<uint16_t>(e[i] >> 16);
+            }
+          }
+        }
+      }
+      // positions past the item: p = 0 there, and zero V keeps 0 * V exact
+      for (int e = lane; e < (kTT - nt) * D; e += 64) {
+        const int d = e / (kTT - nt);
+        const int pi = nt + e % (kTT - nt);
+        svt[d * kVP + pi] = 0;
+      }
+    }
+
+    // ---- O += P V: slot i of lane group kg is token 32*st + 16*(i/4) + 4*kg + i%4
+#pragma unroll
+    for (int st = 0; st < kTT / 32; ++st) {
+      u8v ahi, alo;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p = sacc[2 * st + i / 4][i % 4];
+        const float hi = to_f32(from_f32<T>(p));
+        ahi[i] = bits_of<T>(p);
+        alo[i] = bits_of<T>(p - hi);
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint16_t* vrow = svt + (16 * q + n) * kVP + 32 * st + 4 * kg;
+        const u4s v0 = *reinterpret_cast<const u4s*>(vrow);
+        const u4s v1 = *reinterpret_cast<const u4s*>(vrow + 16);
+        const u8v bv = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        o_acc[q] = mfma16(ahi, bv, o_acc[q], T{});
+        o_acc[q] = mfma16(alo, bv, o_acc[q], T{});
+      }
+    }
+  }
+
+  // ---- epilogue: o_acc[q][r] = O[head 4*kg + r][dim 16*q + n] ------------------
+  const int64_t head0 = static_cast<int64_t>(wi) * hq + h * rep;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int hh = 4 * kg + r;
+    if (hh < rep) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) ws_o[(head0 + hh) * D + 16 * q + n] = o_acc[q][r];
+    }
+  }
+  if (kg == 0 && n < rep) {
+    ws_ml[2 * (head0 + n)] = m_run;
+    ws_ml[2 * (head0 + n) + 1] = l_run;
+  }
+}
+
+}  // namespace tail
+}  // namespace kvq

@@ -10,17 +10,16 @@
 //
 // Work items (built by the host from the request lengths, no device sync):
 //   kind 0: a range where keys and values both come from int4 pages -- the
-//           MFMA kernel of kivi_decode_mfma.hip;
-//   kind 1: tails where one side is already in the ring -- the MFMA tail
-//           kernel of decode_tail_mfma.hip, on a side stream beside the
-//           kind-0 kernel.
-// Geometries either MFMA kernel does not cover go to the generic kernel
-// below: one wave per (work item, kv head), the QK dot products
-// lane-per-position, the PV accumulation lane-per-dim.
+//           MFMA kernel of decode_mfma.hip;
+//   kind 1: tails where one side is already in the ring -- the tail path of
+//           decode_tail.h, run by the same launch in a second pass of its
+//           grid (after every kind-0 wave), or by the standalone tail kernel
+//           when the int4 kernel does not apply.
+// Everything runs on the caller's stream.  Geometries neither MFMA path
+// covers go to the generic kernel below: one wave per (work item, kv head),
+// the QK dot products lane-per-position, the PV accumulation lane-per-dim.
 // Each work item leaves (m, l, o[D]) per query head in the workspace (m in
 // the log2 domain); the combine kernel merges a request's items.
-#include <mutex>
-
 #include "kvq_common.h"
 #include "kvq_decode.h"
 
@@ -296,48 +295,20 @@ kivi_decode_generic_kernel(const TQ* __restrict__ query, int hq, int kvh, int d,
 
 namespace kvq {
 
-// Side stream of each device for the tail items: the tail kernel and the int4
-// kernel write disjoint workspace rows, so the tail runs beside the int4
-// kernel.  Created on first use (default priority) and kept for the process;
-// fork_mutex() serializes the record/wait sequence between host threads.
-struct SideStream {
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr;
-  hipEvent_t join = nullptr;
-};
-
-static std::mutex& fork_mutex() {
-  static std::mutex mu;
-  return mu;
-}
-
-// Caller holds fork_mutex().
-static hipError_t side_stream(SideStream** out) {
-  static SideStream side[64];
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-  SideStream& st = side[dev];
-  if (!st.stream) {
-    if ((e = hipEventCreateWithFlags(&st.fork, hipEventDisableTiming)) != hipSuccess) return e;
-    if ((e = hipEventCreateWithFlags(&st.join, hipEventDisableTiming)) != hipSuccess) return e;
-    if ((e = hipStreamCreateWithFlags(&st.stream, hipStreamNonBlocking)) != hipSuccess) return e;
-  }
-  *out = &st;
-  return hipSuccess;
-}
-
 // Log-sum-exp combine of a request's work items: one wave per (request, query
 // head), four heads per workgroup.  Lane s holds item s's (m, l) of the current
 // chunk of 64 items; the weights 2^(m_s - max) go to every lane through
 // readlane, and each lane accumulates columns lane + 64*k of sum_s w_s * o_s.
-// Items with m = -inf (no position) carry weight 0 and their o is never read.
+// The o rows of the first kPre items are loaded before the (m, l) pass, so a
+// request with up to kPre items costs one round trip to memory instead of one
+// per few items.  Items with m = -inf (no position) carry weight 0 and their o
+// never reaches the sum (selected out, so stale bytes cannot turn it NaN).
 template <typename TO, int KD>
 __global__ void __launch_bounds__(256)
 decode_combine_kernel(int hq, int d, const int32_t* __restrict__ seq_meta, int meta_stride,
                       int first_col, const float* __restrict__ ws_o,
                       const float* __restrict__ ws_ml, TO* __restrict__ out) {
+  constexpr int kPre = 16;
   const int lane = threadIdx.x & 63;
   const int hh = blockIdx.y * 4 + (threadIdx.x >> 6);
   if (hh >= hq) return;  // whole wave: no workgroup barrier below
@@ -345,6 +316,27 @@ decode_combine_kernel(int hq, int d, const int32_t* __restrict__ seq_meta, int m
   const int32_t* sm = seq_meta + static_cast<int64_t>(meta_stride) * b;
   const int fw = sm[first_col];
   const int nw = sm[first_col + 1];
+  TO* orow = out + (static_cast<int64_t>(b) * hq + hh) * d;
+  if (nw <= 0) {  // no items: the empty sum, as the loops below would leave it
+#pragma unroll
+    for (int k = 0; k < KD; ++k) {
+      const int c = lane + 64 * k;
+      if (c < d) orow[c] = from_f32<TO>(0.0f);
+    }
+    return;
+  }
+  const int64_t stride = static_cast<int64_t>(hq) * d;
+  const float* rows = ws_o + (static_cast<int64_t>(fw) * hq + hh) * d;
+  float pre[kPre][KD];
+#pragma unroll
+  for (int j = 0; j < kPre; ++j)
+#pragma unroll
+    for (int k = 0; k < KD; ++k) {
+      const int c = lane + 64 * k;
+      // rows past the request or columns past d are read in bounds (item 0,
+      // column 0) and never used
+      pre[j][k] = rows[(j < nw ? j * stride : 0) + (c < d ? c : 0)];
+    }
   float mx = -INFINITY;
   for (int s0 = 0; s0 < nw; s0 += 64) {
     const int s = s0 + lane;
@@ -368,10 +360,19 @@ decode_combine_kernel(int hq, int d, const int32_t* __restrict__ seq_meta, int m
       }
     }
     const int cnt = nw - s0 < 64 ? nw - s0 : 64;
-    const float* row0 = ws_o + (static_cast<int64_t>(fw + s0) * hq + hh) * d;
-    const int64_t stride = static_cast<int64_t>(hq) * d;
+    int j0 = 0;
+    if (s0 == 0) {
+#pragma unroll
+      for (int j = 0; j < kPre; ++j) {
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), j));
+#pragma unroll
+        for (int k = 0; k < KD; ++k) acc[k] += wj != 0.0f ? wj * pre[j][k] : 0.0f;
+      }
+      j0 = kPre;
+    }
+    const float* row0 = rows + s0 * stride;
 #pragma unroll 4
-    for (int j = 0; j < cnt; ++j) {
+    for (int j = j0; j < cnt; ++j) {
       const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), j));
       const float* row = row0 + j * stride;
 #pragma unroll
@@ -385,7 +386,6 @@ decode_combine_kernel(int hq, int d, const int32_t* __restrict__ seq_meta, int m
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) wsum += __shfl_xor(wsum, o, 64);
   const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
-  TO* orow = out + (static_cast<int64_t>(b) * hq + hh) * d;
 #pragma unroll
   for (int k = 0; k < KD; ++k) {
     const int c = lane + 64 * k;
@@ -446,33 +446,24 @@ extern "C" int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batc
   float* ws_ml = ws_o + num_work * num_heads * head_size;
   const float qscale = scale * 1.4426950408889634f;  // fold log2(e): exp2 in the kernels
 
-  // tail items (kind 1) on the side stream, int4 items (kind 0) on the
-  // caller's stream; the combine waits for both
-  std::lock_guard<std::mutex> lock(kvq::fork_mutex());
-  kvq::SideStream* side = nullptr;
-  hipError_t he = kvq::side_stream(&side);
-  if (he != hipSuccess) return static_cast<int>(he);
-  if ((he = hipEventRecord(side->fork, s)) != hipSuccess) return static_cast<int>(he);
-  if ((he = hipStreamWaitEvent(side->stream, side->fork, 0)) != hipSuccess)
-    return static_cast<int>(he);
-  bool tail = false;
-  int rc = kvq::launch_kivi_decode_tail_mfma(query, q_dtype, num_heads, num_kv_heads,
-                                             head_size, qscale, k_quant, k_scale, k_mn, v_quant,
-                                             v_scale, v_mn, block_size, group_size, num_blocks,
-                                             block_table, max_blocks, seq_meta, work, num_work,
-                                             ring_k, ring_v, ring_dtype, ring_len, ws_o, ws_ml,
-                                             side->stream, &tail);
-  // the join is recorded whatever happened, so the caller's stream never waits
-  // on a stale fork
-  if ((he = hipEventRecord(side->join, side->stream)) != hipSuccess) return static_cast<int>(he);
+  // int4 items (kind 0), and the tail items (kind 1) in a second pass of the
+  // same grid where the tail path applies
+  bool mfma = false, tail = false;
+  int rc = kvq::launch_kivi_decode_mfma(query, q_dtype, num_heads, num_kv_heads, head_size,
+                                       qscale, k_quant, k_scale, k_mn, v_quant, v_scale, v_mn,
+                                       block_size, group_size, num_blocks, block_table,
+                                       max_blocks, seq_meta, work, num_work, ring_k, ring_v,
+                                       ring_dtype, ring_len, ws_o, ws_ml, s, &mfma, &tail);
   if (rc != KVQ_OK) return rc;
-  bool mfma = false;
-  rc = kvq::launch_kivi_decode_mfma(query, q_dtype, num_heads, num_kv_heads, head_size,
-                                   qscale, k_quant, k_scale, k_mn, v_quant, v_scale, v_mn,
-                                   block_size, group_size, num_blocks, block_table, max_blocks,
-                                   seq_meta, work, num_work, ws_o, ws_ml, s, &mfma);
-  if ((he = hipStreamWaitEvent(s, side->join, 0)) != hipSuccess) return static_cast<int>(he);
-  if (rc != KVQ_OK) return rc;
+  if (!tail) {
+    rc = kvq::launch_kivi_decode_tail_mfma(query, q_dtype, num_heads, num_kv_heads, head_size,
+                                           qscale, k_quant, k_scale, k_mn, v_quant, v_scale,
+                                           v_mn, block_size, group_size, num_blocks,
+                                           block_table, max_blocks, seq_meta, work, num_work,
+                                           ring_k, ring_v, ring_dtype, ring_len, ws_o, ws_ml, s,
+                                           &tail);
+    if (rc != KVQ_OK) return rc;
+  }
   if (!mfma || !tail) {
     const dim3 grid(static_cast<unsigned>(num_work), num_kv_heads);
     const int rep = num_heads / num_kv_heads;

@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "kvq_hip.h"
 
 namespace kvq {
@@ -255,6 +257,29 @@ struct Raw8<f16> {
     for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(h[i]);
   }
 };
+
+// LDS one workgroup may use on the current device, cached per device (the
+// attribute query is host work that a decode step should not repeat).
+inline int device_lds_max(int64_t* out) {
+  static std::atomic<int64_t> cache[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= 64) {
+    *out = 0;
+    return KVQ_OK;
+  }
+  int64_t v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int vmax = 0;
+    e = hipDeviceGetAttribute(&vmax, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (e != hipSuccess) return static_cast<int>(e);
+    v = vmax;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  *out = v;
+  return KVQ_OK;
+}
 
 }  // namespace kvq
 

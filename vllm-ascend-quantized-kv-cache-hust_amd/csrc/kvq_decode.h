@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kvq_hip.h"
+
 namespace kvq {
 
 // ---- XCD-aware grid mapping ------------------------------------------------
@@ -33,19 +35,29 @@ inline int64_t decode_workspace_bytes(int64_t num_work, int num_heads, int head_
          static_cast<int64_t>(sizeof(float));
 }
 
+// The MFMA tail path (kind-1 items) applies: D = 128, GQA group <= 16, query
+// and ring in the same 16-bit dtype.
+inline bool tail_path_applies(int q_dtype, int hq, int kvh, int d, int ring_dtype) {
+  return d == 128 && hq / kvh <= 16 && ring_dtype == q_dtype &&
+         (q_dtype == KVQ_DTYPE_BF16 || q_dtype == KVQ_DTYPE_F16);
+}
+
 // Launch the MFMA kernel for the kind-0 work items when the geometry is one it
-// covers; *launched tells the caller whether kind-0 items still need the
-// generic kernel.
+// covers, taking the kind-1 items too (in a second pass of the same grid) when
+// the tail path applies.  *launched / *tail_done tell the caller which kinds
+// still need another kernel.
 int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int d, float qscale,
                             const int32_t* kq, const float* ks, const float* km,
                             const int32_t* vq, const float* vs, const float* vm, int bs, int g,
                             int64_t nb, const int32_t* block_table, int64_t maxb,
                             const int32_t* seq_meta, const int32_t* work, int64_t num_work,
-                            float* ws_o, float* ws_ml, hipStream_t s, bool* launched);
+                            const void* ring_k, const void* ring_v, int ring_dtype, int ring_len,
+                            float* ws_o, float* ws_ml, hipStream_t s, bool* launched,
+                            bool* tail_done);
 
-// MFMA kernel for the kind-1 (mixed-source tail) items: D = 128, query and
-// ring in the same 16-bit dtype.  *launched tells the caller whether kind-1
-// items still need the generic kernel.
+// Standalone MFMA tail kernel for the kind-1 items, for geometries the int4
+// kernel does not cover.  *launched tells the caller whether kind-1 items still
+// need the generic kernel.
 int launch_kivi_decode_tail_mfma(const void* query, int q_dtype, int hq, int kvh, int d,
                                  float qscale, const int32_t* kq, const float* ks,
                                  const float* km, const int32_t* vq, const float* vs,

@@ -586,18 +586,9 @@ extern "C" int kvq_prefill_attn(const void* query, const void* key, const void* 
     return KVQ_ERR_GEOMETRY;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const float qscale = scale * 1.4426950408889634f;
-  // LDS one workgroup may use on this device (cached per device)
-  static int64_t lds_cache[64] = {};
-  int dev = 0;
-  hipError_t he = hipGetDevice(&dev);
-  if (he != hipSuccess) return static_cast<int>(he);
-  if (dev >= 0 && dev < 64 && lds_cache[dev] == 0) {
-    int vmax = 0;
-    he = hipDeviceGetAttribute(&vmax, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
-    if (he != hipSuccess) return static_cast<int>(he);
-    lds_cache[dev] = vmax;
-  }
-  const int64_t lds_max = dev >= 0 && dev < 64 ? lds_cache[dev] : 0;
+  int64_t lds_max = 0;  // LDS one workgroup may use on this device
+  const int lrc = device_lds_max(&lds_max);
+  if (lrc != KVQ_OK) return lrc;
   const int64_t fa_lds = head_size == 64 ? FaLds<64>::BYTES : FaLds<128>::BYTES;
   if ((dtype == KVQ_DTYPE_BF16 || dtype == KVQ_DTYPE_F16) &&
       (head_size == 64 || head_size == 128) && fa_lds <= lds_max) {
