@@ -10,9 +10,10 @@ evicts the oldest value (and flushes a full key window) into int4 history,
 and runs fused INT4 decode attention.  Plans are built on the host before the
 timed region; the timed region is the device work only.
 
-``value`` = algorithmic bytes of the step / step time (GB/s).  ``roofline``
-covers the fused decode attention (the dominant kernel), timed with HIP
-events on its stream.  ``extra`` carries the other BASELINE configs: INT4
+``value`` = algorithmic bytes of the step / step time (GB/s), the steps run
+back to back between two HIP events.  ``roofline`` covers the fused decode
+attention (the dominant kernel): the last step's decode call repeated back to
+back between two events on its stream.  ``extra`` carries the other BASELINE configs: INT4
 pack, gather-dequant and the chunk's causal attention (config 4), INT8 decode
 (config 2) and long-context INT4 decode (config 5).  ``cpu_baseline`` times the
 CPU oracle (the reference algorithm restated in torch) on a bounded sample.
@@ -238,9 +239,11 @@ def bench_kivi_decode(torch, dev, *, b, hq, kvh, d, g, r, bs, lens, steps, warmu
     kflat = ring.key.view(-1, kvh, d)
     vflat = ring.value.view(-1, kvh, d)
 
-    ev = []
+    def decode(p, q):
+        kivi_decode_attention(q, st.caches, st.table, [], ring.key, ring.value, scale, g,
+                              out=out, plan=(p["meta"], p["work"]))
 
-    def run_step(i, timed):
+    def run_step(i):
         p = plans[i]
         if p["n_pack_k"]:
             pack_key_rows(kflat, new_k[i], p["kidx"], p["kslots"], kq, ks, km, g)
@@ -248,31 +251,33 @@ def bench_kivi_decode(torch, dev, *, b, hq, kvh, d, g, r, bs, lens, steps, warmu
             pack_value_rows(vflat, new_v[i], p["vidx"], p["vslots"], vq, vs, vm, g)
         ring_write(ring.key, new_k[i], p["ksrc"], p["kdst"])
         ring_write(ring.value, new_v[i], p["vsrc"], p["vdst"])
-        if timed:
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record()
-        kivi_decode_attention(qs[i], st.caches, st.table, [], ring.key, ring.value, scale, g,
-                              out=out, plan=(p["meta"], p["work"]))
-        if timed:
-            e1.record()
-            ev.append((e0, e1))
+        decode(p, qs[i])
 
     for i in range(warmup):
-        run_step(i, False)
+        run_step(i)
     torch.cuda.synchronize()
     s0 = torch.cuda.Event(enable_timing=True)
     s1 = torch.cuda.Event(enable_timing=True)
     s0.record()
     for i in range(warmup, total):
-        run_step(i, True)
+        run_step(i)
     s1.record()
     torch.cuda.synchronize()
     step_ms = s0.elapsed_time(s1) / steps
-    dec_ms = sum(a.elapsed_time(z) for a, z in ev) / len(ev)
     timed = plans[warmup:]
     step_bytes = sum(p["step_bytes"] for p in timed) / steps
-    dec_bytes = sum(p["decode_bytes"] for p in timed) / steps
+    # the decode alone: the last step's call again (its plan matches the state
+    # the last step left), back to back between two events
+    last = plans[-1]
+    for _ in range(3):
+        decode(last, qs[total - 1])
+    s0.record()
+    for _ in range(steps):
+        decode(last, qs[total - 1])
+    s1.record()
+    torch.cuda.synchronize()
+    dec_ms = s0.elapsed_time(s1) / steps
+    dec_bytes = last["decode_bytes"]
     res = {
         "step_ms": step_ms,
         "decode_ms": dec_ms,

@@ -472,14 +472,19 @@ __device__ __forceinline__ void compute_tile(const uint32_t* W, const VALS& vals
   f4 sacc[T::NJ];
 #pragma unroll
   for (int j = 0; j < T::NJ; ++j) sacc[j] = f4{0.f, 0.f, 0.f, 0.f};
+  // key words of k-step s4: dims 32*s4 + 4*ii + kg of chunk `chunk`, pairs 32
+  // words apart; each k-step's words are read while the previous one computes
+  uint32_t wkb[2][8];
+  auto load_keys = [&](int s4, uint32_t (&w)[8]) {
+    const uint32_t* kw = W + T::KW + (32 * s4 + kg) * CPG + chunk;
+#pragma unroll
+    for (int ii = 0; ii < 8; ++ii) w[ii] = kw[4 * ii * CPG];
+  };
+  load_keys(0, wkb[0]);
 #pragma unroll
   for (int s4 = 0; s4 < 4; ++s4) {
-    uint32_t w[8];  // dims 32*s4 + 4*ii + kg of chunk `chunk`: pairs 32 words apart
-    {
-      const uint32_t* kw = W + T::KW + (32 * s4 + kg) * CPG + chunk;
-#pragma unroll
-      for (int ii = 0; ii < 8; ++ii) w[ii] = kw[4 * ii * CPG];
-    }
+    if (s4 < 3) load_keys(s4 + 1, wkb[(s4 + 1) & 1]);
+    const uint32_t(&w)[8] = wkb[s4 & 1];
 #pragma unroll
     for (int jm = 0; jm < T::NJ; ++jm) {
       const uint32_t sel = ln.selk[jm];
