@@ -1,14 +1,15 @@
 # SPDX-License-Identifier: Apache-2.0
 """The pack kernels' division-free KIVI quantization rule, checked on the CPU.
 
-The device quantizes with v = (x - mn) * rcp(scale), code
-min(rndne(v), 15), and redoes a whole word with the exact
-(x - mn) / scale + 0.5 when any of its 8 elements has v within 1e-5 of a
-tie k + 0.5 (kivi_pack_word in csrc/kvq_common.h).  This test replays that rule in
-numpy fp32 with the reciprocal off by up to one ulp either way (v_rcp_f32's
-bound) and requires codes identical to the exact rule of the reference
-(pkg/ops/triton/kivi_pack.py:98-104, 195-204) on random groups and on groups
-built so the quotients sit on the x.5 boundaries.
+The device quantizes with v = (x - mn) * rcp(scale), code rndne(v) with no
+clamp (v stays inside [0, 15 + 4e-6]), and redoes an element with the exact
+(x - mn) / scale + 0.5 when its v lies within 1e-5 of a tie k + 0.5
+(kivi_pack_word in csrc/kvq_common.h).  This test replays that rule in numpy
+fp32 with the reciprocal off by up to one ulp either way (v_rcp_f32's bound)
+and requires codes identical to the exact rule of the reference
+(pkg/ops/triton/kivi_pack.py:98-104, 195-204) on random groups, on groups on
+the bf16 grid (where exact ties are common) and on groups built so the
+quotients sit on the x.5 boundaries.
 """
 
 from __future__ import annotations
@@ -28,11 +29,10 @@ def _rule(x, mn, sc, rcp):
     v = (d * rcp).astype(F)
     r = np.rint(v)  # round half to even, as v_rndne_f32
     near = ~(np.abs((v - r).astype(F)) <= F(0.49999))
-    fast = np.minimum(r, F(15))
-    # the fallback redoes whole words of 8 consecutive elements
-    k = min(8, near.shape[1])
-    word_near = np.repeat(near.reshape(near.shape[0], -1, k).any(axis=-1), k, axis=-1)
-    return np.where(word_near, _exact(x, mn, sc), fast), near.mean()
+    # without a clamp the fast codes must already be codes
+    assert (r[~near] >= 0).all() and (r[~near] <= 15).all()
+    # the fallback redoes the near-tie elements alone
+    return np.where(near, _exact(x, mn, sc), r), near.mean()
 
 
 def _boundary_groups(rng, rows, g):
@@ -69,6 +69,17 @@ def test_rule_matches_exact_on_random_groups():
     for g in (8, 32, 128):
         _check(rng.normal(size=(512, g)).astype(F))
         _check((rng.normal(size=(256, g)) * np.exp(rng.normal(size=(256, 1)) * 3)).astype(F))
+
+
+def test_rule_matches_exact_on_the_bf16_grid():
+    import torch
+
+    rng = np.random.default_rng(2)
+    for g in (64, 128):
+        x = torch.from_numpy(rng.normal(size=(1024, g)).astype(F))
+        x = x * torch.exp(torch.from_numpy(rng.normal(size=(1, g)).astype(F)))
+        rate = _check(x.to(torch.bfloat16).float().numpy())
+        assert rate > 1e-4  # ties are frequent on a 16-bit grid
 
 
 def test_rule_matches_exact_on_boundary_quotients():

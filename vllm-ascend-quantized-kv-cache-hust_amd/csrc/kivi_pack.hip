@@ -2,7 +2,10 @@
 // KIVI INT4 pack kernels for MI355X (gfx950).
 //
 // Key pack  (reference: pkg/ops/triton/kivi_pack.py:134-226)
-//   One workgroup per (token group, kv head).  Thread (tc, dv) owns an 8x8
+//   Head size 128 with G in {64, 128} and 16-bit input: the register form
+//   below (kivi_pack_key_wave_kernel), one wave per group, head and half of
+//   the dims.  Other geometries: one workgroup per (token group, kv head).
+//   Thread (tc, dv) owns an 8x8
 //   tile: 8 consecutive tokens x 8 consecutive dims, read as 8 16-byte rows
 //   (16 lanes cover one 256-byte head row, fully coalesced).  Per-dim min/max
 //   over the group's tokens go through LDS; each thread then quantizes its
@@ -17,8 +20,8 @@
 //   whose rows do not tile a wave keep the one-thread-per-word kernel.
 //
 // Both quantize with kivi_pack_word: a reciprocal per group and a
-// round-to-nearest per element, falling back to the exact division for the
-// rare word with a quotient at a rounding tie, so codes stay bit-exact.
+// round-to-nearest per element, falling back to the exact division for an
+// element whose quotient sits at a rounding tie, so codes stay bit-exact.
 #include <mutex>
 
 #include "kvq_common.h"
@@ -120,6 +123,127 @@ kivi_pack_key_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __restri
     const int c = i / nchunk;
     const int w = i - c * nchunk;
     out[(row_base + c) * words_per_dim + off / 8 + w] = s_words[i];
+  }
+}
+
+// Key pack, register form (head size 128, G in {64, 128}, 16-bit input): one
+// wave per (token group, kv head, half of the head dims).  Lane (tg, dl) holds
+// G/8 consecutive tokens (token group tg of 8) x 8 consecutive dims (dl of 8)
+// as raw 16-byte rows -- each load instruction reads 8 whole 128-byte
+// half-rows -- so the per-dim min/max is a register pass plus a three-step
+// butterfly over tg, and every output word (8 consecutive tokens of one dim)
+// is built from one lane's own registers.  No LDS, no barrier; the whole
+// group's input stays in 64 VGPRs.
+template <typename T>
+__device__ __forceinline__ void unpack8(const uint4& v, float (&x)[8]);
+template <>
+__device__ __forceinline__ void unpack8<bf16>(const uint4& v, float (&x)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __uint_as_float(w[i] << 16);
+    x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void unpack8<f16>(const uint4& v, float (&x)[8]) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  const h8 h = __builtin_bit_cast(h8, v);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(h[i]);
+}
+
+template <typename T, typename I, int G>
+__global__ void __launch_bounds__(256)
+kivi_pack_key_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __restrict__ src_b,
+                          const int64_t* __restrict__ src_index, const I* __restrict__ slots,
+                          int64_t units, int kvh, int bs, int32_t* __restrict__ kq,
+                          float* __restrict__ ks, float* __restrict__ km) {
+  constexpr int D = 128;
+  constexpr int TPL = G / 8;  // tokens per lane
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (u >= units) return;  // whole wave
+  const int lane = threadIdx.x & 63;
+  const int hf = static_cast<int>(u & 1);
+  const int h = static_cast<int>((u >> 1) % kvh);
+  const int64_t t0 = (u >> 1) / kvh * G;
+  const int64_t first = ld_index(slots, t0);
+  if (first < 0) return;  // uniform across the wave
+  const int64_t blk = first / bs;
+  const int off = static_cast<int>(first - blk * bs);
+  const int dl = lane & 7;
+  const int tg = lane >> 3;
+  const int64_t row_elems = static_cast<int64_t>(kvh) * D;
+  const int col = h * D + hf * 64 + 8 * dl;
+
+  uint4 raw[TPL];
+#pragma unroll
+  for (int k = 0; k < TPL; ++k) {
+    const int64_t t = t0 + TPL * tg + k;
+    const int64_t row = src_index ? src_index[t] : t;
+    raw[k] = *reinterpret_cast<const uint4*>(src_row(src_a, n_a, src_b, row, row_elems) + col);
+  }
+  float mn[8], mx[8];
+  {
+    float x[8];
+    unpack8<T>(raw[0], x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mn[j] = mx[j] = x[j];
+#pragma unroll
+    for (int k = 1; k < TPL; ++k) {
+      unpack8<T>(raw[k], x);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        mn[j] = fmin_ordered(mn[j], x[j]);
+        mx[j] = fmax_ordered(mx[j], x[j]);
+      }
+    }
+  }
+  // the 8 token groups of a dim are lanes dl + 8*tg: combine over tg
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    mn[j] = fmin_ordered(mn[j], lane_xor<8>(mn[j]));
+    mx[j] = fmax_ordered(mx[j], lane_xor<8>(mx[j]));
+    mn[j] = fmin_ordered(mn[j], lane_xor<16>(mn[j]));
+    mx[j] = fmax_ordered(mx[j], lane_xor<16>(mx[j]));
+    mn[j] = fmin_ordered(mn[j], lane_xor<32>(mn[j]));
+    mx[j] = fmax_ordered(mx[j], lane_xor<32>(mx[j]));
+  }
+  float sc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sc[j] = kivi_group_scale(mn[j], mx[j]);
+
+  const int64_t row_base = (blk * kvh + h) * static_cast<int64_t>(D) + hf * 64 + 8 * dl;
+  const int wpd = bs / 8;
+  uint32_t* out = reinterpret_cast<uint32_t*>(kq);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    uint32_t wd[TPL / 8];
+#pragma unroll
+    for (int c = 0; c < TPL / 8; ++c) {
+      float col8[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float x[8];
+        unpack8<T>(raw[8 * c + i], x);
+        col8[i] = x[j];
+      }
+      wd[c] = kivi_pack_word(col8, mn[j], sc[j]);
+    }
+    uint32_t* dst = out + (row_base + j) * wpd + off / 8 + (TPL / 8) * tg;
+    if constexpr (TPL / 8 == 2)
+      *reinterpret_cast<uint2*>(dst) = make_uint2(wd[0], wd[1]);
+    else
+      dst[0] = wd[0];
+  }
+  if (tg == 0) {
+    const int gpb = bs / G;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t sidx = (row_base + j) * gpb + off / G;
+      ks[sidx] = sc[j];
+      km[sidx] = mn[j];
+    }
   }
 }
 
@@ -363,6 +487,28 @@ extern "C" int kvq_kivi_pack_key(const void* src_a, int64_t n_a, const void* src
   if (num_tokens % group_size) return KVQ_ERR_INVALID;
   if (!src_index && n_a < num_tokens) return KVQ_ERR_INVALID;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (head_size == 128 && (group_size == 64 || group_size == 128) &&
+      (src_dtype == KVQ_DTYPE_BF16 || src_dtype == KVQ_DTYPE_F16)) {
+    // register form: one wave per (token group, head, half of the dims)
+    const int64_t units = num_tokens / group_size * num_kv_heads * 2;
+    const int64_t blocks = (units + 3) / 4;
+    if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
+#define KVQ_LAUNCH_KEY_WAVE(T, GG)                                                            \
+  KVQ_DISPATCH_INDEX(slot_index_type, I,                                                      \
+    hipLaunchKernelGGL((kivi_pack_key_wave_kernel<T, I, GG>),                                 \
+                       dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s,                  \
+                       static_cast<const T*>(src_a), n_a, static_cast<const T*>(src_b),       \
+                       src_index, static_cast<const I*>(slot_mapping), units, num_kv_heads,   \
+                       block_size, k_quant, k_scale, k_mn))
+    if (src_dtype == KVQ_DTYPE_BF16) {
+      if (group_size == 128) { KVQ_LAUNCH_KEY_WAVE(bf16, 128); } else { KVQ_LAUNCH_KEY_WAVE(bf16, 64); }
+    } else {
+      if (group_size == 128) { KVQ_LAUNCH_KEY_WAVE(f16, 128); } else { KVQ_LAUNCH_KEY_WAVE(f16, 64); }
+    }
+#undef KVQ_LAUNCH_KEY_WAVE
+    KVQ_LAUNCH_CHECK();
+    return KVQ_OK;
+  }
   const int tiles = (group_size / 8) * (head_size / 8);
   if (tiles > 1024) return KVQ_ERR_GEOMETRY;
   const int threads = ((tiles + 63) / 64) * 64;

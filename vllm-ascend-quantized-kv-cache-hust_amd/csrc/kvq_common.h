@@ -123,26 +123,32 @@ __device__ __forceinline__ uint32_t kivi_quantize(float x, float mn, float scale
 // the product), and the reference's floor(RN(RN(d / scale) + 0.5)) sits
 // within another 2e-6 of floor(d / scale + 0.5).  So rndne(v) -- which
 // differs from rounding half up only at a tie -- is the reference's code
-// whenever v is more than 1e-5 away from k + 0.5 (codes from 16 up clamp to
-// 15 on both sides).  A word holding a v within 1e-5 of a tie (about 2e-5 of
-// the elements) is redone with the exact division.
+// whenever v is more than 1e-5 away from k + 0.5.  An element whose v lies
+// within 1e-5 of a tie is redone with the exact division, on its own: on bf16
+// inputs about 2e-3 of the elements do (exact ties 30 (x - mn) = (2k+1) (mx -
+// mn) are common on a 16-bit grid), and redoing whole words made a wave take
+// the division branch for most of its words.
+//
+// mn <= x and scale >= (x - mn) / 15 (rounded up by at most an ulp, or the
+// 1e-6 floor) keep v inside [0, 15 + 4e-6], so rndne(v) is already a code in
+// 0..15: v_cvt_pk_u8_f32 drops each one into a byte (even codes of the word in
+// one register, odd codes in another) and a single shift-or interleaves the
+// nibbles.
 __device__ __forceinline__ uint32_t kivi_pack_word(const float (&x)[8], float mn, float scale) {
   const float rcp = __builtin_amdgcn_rcpf(scale);
-  uint32_t word = 0;
-  float worst = 0.0f;  // max |v - rndne(v)|: 0.5 at a tie
+  uint32_t ev = 0, od = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float v = (x[i] - mn) * rcp;
-    const float r = __builtin_rintf(v);
-    worst = fmaxf(worst, fabsf(v - r));
-    word |= static_cast<uint32_t>(fminf(r, 15.0f)) << (4 * i);
+    float r = __builtin_rintf(v);
+    if (__builtin_expect(!(fabsf(v - r) <= 0.49999f), 0))
+      r = static_cast<float>(kivi_quantize(x[i], mn, scale));
+    if (i % 2 == 0)
+      ev = __builtin_amdgcn_cvt_pk_u8_f32(r, i / 2, ev);
+    else
+      od = __builtin_amdgcn_cvt_pk_u8_f32(r, i / 2, od);
   }
-  if (!(worst <= 0.49999f)) {
-    word = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) word |= kivi_quantize(x[i], mn, scale) << (4 * i);
-  }
-  return word;
+  return ev | (od << 4);
 }
 
 // The 8 nibbles of a packed word as floats (nibble i -> c[i]): one mask per
