@@ -141,8 +141,8 @@ int8_dequant_gather_kernel(const int8_t* __restrict__ kc, const int8_t* __restri
     xk[i] = round_to<T>(kq * ak[i]);  // (x.to(dtype) - 0) * (1/inv) in the dtype
     xv[i] = round_to<T>(vq * av[i]);
   }
-  store8(out_k + (row0 + p) * channels + c8, xk);
-  store8(out_v + (row0 + p) * channels + c8, xv);
+  store8_nt(out_k + (row0 + p) * channels + c8, xk);
+  store8_nt(out_v + (row0 + p) * channels + c8, xv);
 }
 
 // ---- decode (generic wave-per-item kernel) ---------------------------------

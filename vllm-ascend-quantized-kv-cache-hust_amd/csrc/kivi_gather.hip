@@ -111,7 +111,7 @@ kivi_gather_kernel(const int32_t* __restrict__ kq, const float* __restrict__ ks,
 #pragma unroll
           for (int i = 0; i < 8; ++i) x[i] = kivi_dequant((w[i] >> (4 * l)) & 0xfu, sc[i], mn[i]);
         }
-        store8(out_k + (row0 + p) * hd + h * d + dv * 8, x);
+        store8_nt(out_k + (row0 + p) * hd + h * d + dv * 8, x);
       }
     }
   }
@@ -142,7 +142,7 @@ kivi_gather_kernel(const int32_t* __restrict__ kq, const float* __restrict__ ks,
 #pragma unroll
         for (int l = 0; l < 8; ++l) x[l] = __fadd_rn(__fmul_rn(x[l], sc), mn);
       }
-      store8(out_v + (row0 + p) * hd + h * d + w * 8, x);
+      store8_nt(out_v + (row0 + p) * hd + h * d + w * 8, x);
     }
   }
 }

@@ -230,11 +230,14 @@ kivi_pack_key_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __r
       }
       wd[c] = kivi_pack_word(col8, mn[j], sc[j]);
     }
+    // streaming (nontemporal) stores: the packed pages are not re-read soon
     uint32_t* dst = out + (row_base + j) * wpd + off / 8 + (TPL / 8) * tg;
-    if constexpr (TPL / 8 == 2)
-      *reinterpret_cast<uint2*>(dst) = make_uint2(wd[0], wd[1]);
-    else
-      dst[0] = wd[0];
+    if constexpr (TPL / 8 == 2) {
+      typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+      __builtin_nontemporal_store(u2v{wd[0], wd[1]}, reinterpret_cast<u2v*>(dst));
+    } else {
+      __builtin_nontemporal_store(wd[0], dst);
+    }
   }
   if (tg == 0) {
     const int gpb = bs / G;
@@ -422,7 +425,7 @@ kivi_pack_value_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* _
       const uint32_t t = kvh_div.div(static_cast<uint32_t>(r));
       const int h = static_cast<int>(r) - static_cast<int>(t) * kvh;
       const int64_t orow = slot * kvh + h;  // page row (blk * bs + off) of head h
-      reinterpret_cast<uint32_t*>(vq)[orow * WPR + w] = word;
+      __builtin_nontemporal_store(word, reinterpret_cast<uint32_t*>(vq) + orow * WPR + w);
       if (w % gw == 0) {
         const int64_t sidx = orow * ng + w / gw;
         vs[sidx] = sc;

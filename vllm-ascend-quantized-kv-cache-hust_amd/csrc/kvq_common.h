@@ -100,6 +100,32 @@ __device__ __forceinline__ void store8(f16* p, const float (&x)[8]) {
   *reinterpret_cast<h8*>(p) = v;
 }
 
+// Streaming stores for dense outputs nobody re-reads soon (gathered K/V):
+// nontemporal global stores (the `nt` bit) do not allocate in L2 on the way
+// out.  The config-4 gather writes 335 MB of bf16 K/V; with plain stores it
+// ran at 3.7 TB/s, with these at 5.8 TB/s.
+typedef uint32_t kvq_u4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store16_nt(void* p, kvq_u4v v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<kvq_u4v*>(p));
+}
+__device__ __forceinline__ void store8_nt(float* p, const float (&x)[8]) {
+  store16_nt(p, kvq_u4v{__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
+                        __float_as_uint(x[3])});
+  store16_nt(p + 4, kvq_u4v{__float_as_uint(x[4]), __float_as_uint(x[5]), __float_as_uint(x[6]),
+                            __float_as_uint(x[7])});
+}
+__device__ __forceinline__ void store8_nt(bf16* p, const float (&x)[8]) {
+  store16_nt(p, kvq_u4v{bf16x2_bits(x[0], x[1]), bf16x2_bits(x[2], x[3]),
+                        bf16x2_bits(x[4], x[5]), bf16x2_bits(x[6], x[7])});
+}
+__device__ __forceinline__ void store8_nt(f16* p, const float (&x)[8]) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  h8 v;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = static_cast<_Float16>(x[i]);
+  store16_nt(p, __builtin_bit_cast(kvq_u4v, v));
+}
+
 // KIVI group scale: max((mx - mn) / 15, 1e-6); the floor applies to the scale.
 __device__ __forceinline__ float kivi_group_scale(float mn, float mx) {
   const float s = (mx - mn) / 15.0f;
