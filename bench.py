@@ -118,7 +118,7 @@ class KiviState:
                 pack_key_rows(key, None, None, slots[:hk], kq, ks, km, g)
             if hv:
                 pack_value_rows(value, None, None, slots[:hv], vq, vs, vm, g)
-            base = i * r
+            base = i * self.ring.ring_len
             for is_key, h, src in ((True, hk, key), (False, hv, value)):
                 cnt = n - h
                 dst = torch.arange(base, base + cnt, device=dev, dtype=torch.int64)
@@ -127,7 +127,7 @@ class KiviState:
                 lane_slots = [int(x) for x in self.slot_list(i, h, n)]
                 self.ring.start[is_key][i] = 0
                 self.ring.length[is_key][i] = cnt
-                ls = [-1] * r
+                ls = [-1] * self.ring.ring_len
                 ls[:cnt] = lane_slots
                 self.ring.lane_slot[is_key][i] = ls
                 self.ring.slot_lane[is_key][i] = {s_: j for j, s_ in enumerate(lane_slots)}
@@ -178,6 +178,7 @@ def bench_kivi_decode(torch, dev, *, b, hq, kvh, d, g, r, bs, lens, steps, warmu
         plan_decode_work,
     )
     from vllm_ascend_quantized_kv_cache.ops.kivi_pack import (
+        kivi_store,
         pack_key_rows,
         pack_value_rows,
         ring_write,
@@ -227,7 +228,10 @@ def bench_kivi_decode(torch, dev, *, b, hq, kvh, d, g, r, bs, lens, steps, warmu
             "seqs": seqs,
             "n_pack_k": len(plan.key.pack_slots), "n_pack_v": len(plan.value.pack_slots),
             "n_ring": len(plan.key.ring) + len(plan.value.ring),
+            "one": plan.one_launch_jobs(),
         }
+        if p["one"] is not None:
+            p["one"] = (dev_t(p["one"][0]), p["one"][1])
         p["decode_bytes"] = decode_bytes(seqs, kvh=kvh, d=d, g=g, hq=hq, bs=bs)
         p["step_bytes"] = (
             p["decode_bytes"]
@@ -245,6 +249,12 @@ def bench_kivi_decode(torch, dev, *, b, hq, kvh, d, g, r, bs, lens, steps, warmu
 
     def run_step(i):
         p = plans[i]
+        # one launch for the whole store (the path the backend takes for a
+        # hazard-free plan, which every single-token step is)
+        if p["one"] is not None and kivi_store(new_k[i], new_v[i], ring.key, ring.value,
+                                               p["one"][0], p["one"][1], st.caches, g):
+            decode(p, qs[i])
+            return
         if p["n_pack_k"]:
             pack_key_rows(kflat, new_k[i], p["kidx"], p["kslots"], kq, ks, km, g)
         if p["n_pack_v"]:

@@ -88,6 +88,28 @@ int kvq_kivi_ring_write(const void* src, int src_dtype, const int64_t* src_rows,
                         const int64_t* dst_rows, int64_t num_rows, int row_elems,
                         void* ring, int ring_dtype, void* stream);
 
+/* One-launch store of a batch: the key pack, value pack and both sides' ring
+ * writes of kvq_kivi_pack_key / kvq_kivi_pack_value / kvq_kivi_ring_write in
+ * a single grid.  Replaces the flush-then-append sequence of
+ * _store_kivi_residual_entries (pkg/methods/kivi_int4/attention_backend.py:
+ * 442-462, with _flush_kivi_residual_prefix) for a whole step.
+ * jobs (int64, device): [key pack src | key pack slot | value pack src |
+ * value pack slot | key ring src | key ring dst | value ring src | value ring
+ * dst] with n_key_pack, n_value_pack, n_key_ring, n_value_ring entries.  Pack
+ * sources index [ring rows (ring_rows of them) ; input rows]; ring src are
+ * input rows, ring dst ring rows.  Inputs and rings are [rows, KVH, D] of
+ * `dtype`.  Precondition: no ring dst is a pack source of the same side (the
+ * batch then has no order inside it).  Head size 128, group size 64 or 128,
+ * bf16/fp16 only: other geometries return KVQ_ERR_GEOMETRY and the caller
+ * uses the separate entry points.  n_key_pack % group_size == 0 with the
+ * group rules of kvq_kivi_pack_key. */
+int kvq_kivi_store(const void* key_input, const void* value_input, void* ring_k,
+                   void* ring_v, int64_t ring_rows, int dtype, int num_kv_heads,
+                   int head_size, int group_size, int block_size, const int64_t* jobs,
+                   int64_t n_key_pack, int64_t n_value_pack, int64_t n_key_ring,
+                   int64_t n_value_ring, int32_t* k_quant, float* k_scale, float* k_mn,
+                   int32_t* v_quant, float* v_scale, float* v_mn, void* stream);
+
 /* Paged gather-dequant to dense TND with an optional residual-tail overlay.
  * out_k/out_v are [cu_seqlens[batch], KVH, D] of `out_dtype`; request b owns
  * rows [cu_seqlens[b], cu_seqlens[b+1]).  Negative block ids read block 0 and

@@ -237,6 +237,74 @@ def test_bulk_prefill_flushes_a_full_window_that_incremental_writes_keep_exact()
     assert inc.kivi_residual_key_len[row] == tokens == inc.kivi_residual_value_len[row]
 
 
+def test_single_token_steps_plan_one_launch():
+    """With R + 1 lanes per row, a step that appends one token per request
+    never writes a ring lane the same step packs (keys flush whole windows,
+    values evict one lane), so every such plan is one launch; the window still
+    holds the newest R tokens in order."""
+    from vllm_ascend_quantized_kv_cache.methods.kivi_int4.residual import (
+        KiviResidualRing,
+        StorePlan,
+    )
+
+    window, rows = 8, 3
+    ring = KiviResidualRing(rows, window, 1, 8, device="cpu")
+    assert ring.ring_len == window + 1 and ring.key.shape[1] == window + 1
+    seen = {"kp": 0, "vp": 0}
+    for step in range(5 * window + 3):
+        plan = StorePlan()
+        for row in range(rows):
+            slot = [row * 1000 + step]
+            for is_key in (True, False):
+                ring.plan_store(plan, row, slot, [row], is_key=is_key, block_size=8,
+                                group_size=8)
+        one = plan.one_launch_jobs()
+        assert one is not None, f"step {step} writes a lane it packs"
+        jobs, (nkp, nvp, nkr, nvr) = one
+        assert len(jobs) == 2 * (nkp + nvp + nkr + nvr)
+        assert (nkr, nvr) == (rows, rows)
+        seen["kp"] += nkp
+        seen["vp"] += nvp
+        for row in range(rows):
+            newest = [row * 1000 + x for x in range(step + 1)]
+            assert ring.window_slots(row, is_key=False) == newest[-window:]
+            n_keys = len(ring.window_slots(row, is_key=True))
+            assert ring.window_slots(row, is_key=True) == newest[len(newest) - n_keys:]
+            assert 1 <= n_keys <= window
+    assert seen["kp"] > 0 and seen["vp"] > 0
+
+
+def test_multi_token_batch_that_reuses_a_packed_lane_is_not_one_launch():
+    """Two tokens into a full value window: the second lands on the lane the
+    first evicted and packed, so the plan must keep packs before ring writes."""
+    from vllm_ascend_quantized_kv_cache.methods.kivi_int4.residual import (
+        KiviResidualRing,
+        StorePlan,
+    )
+
+    window = 4
+    ring = KiviResidualRing(1, window, 1, 8, device="cpu")
+    plan = StorePlan()
+    ring.plan_store(plan, 0, list(range(window)), list(range(window)), is_key=False,
+                    block_size=8, group_size=8)
+    assert plan.one_launch_jobs() is not None  # no pack yet
+    plan = StorePlan()
+    ring.plan_store(plan, 0, [window, window + 1], [0, 1], is_key=False, block_size=8,
+                    group_size=8)
+    assert plan.value.pack_slots == [0, 1]
+    assert plan.one_launch_jobs() is None
+
+
+def test_one_launch_store_geometry_gate():
+    from vllm_ascend_quantized_kv_cache.ops.kivi_pack import store_one_launch_supported
+
+    assert store_one_launch_supported(128, 128, torch.bfloat16)
+    assert store_one_launch_supported(128, 64, torch.float16)
+    assert not store_one_launch_supported(64, 64, torch.bfloat16)
+    assert not store_one_launch_supported(128, 32, torch.bfloat16)
+    assert not store_one_launch_supported(128, 128, torch.float32)
+
+
 def test_misaligned_key_flush_fails_closed_before_kernel():
     impl = _make_impl()
     key = torch.randn(GROUP, KVH, HEAD)

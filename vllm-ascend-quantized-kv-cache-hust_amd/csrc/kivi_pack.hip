@@ -153,17 +153,15 @@ __device__ __forceinline__ void unpack8<f16>(const uint4& v, float (&x)[8]) {
   for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(h[i]);
 }
 
+// Unit u = ((group * kvh) + head) * 2 + half; the whole wave calls it.
 template <typename T, typename I, int G>
-__global__ void __launch_bounds__(256)
-kivi_pack_key_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __restrict__ src_b,
-                          const int64_t* __restrict__ src_index, const I* __restrict__ slots,
-                          int64_t units, int kvh, int bs, int32_t* __restrict__ kq,
-                          float* __restrict__ ks, float* __restrict__ km) {
+__device__ __forceinline__ void key_pack_wave(const T* src_a, int64_t n_a, const T* src_b,
+                                              const int64_t* __restrict__ src_index,
+                                              const I* __restrict__ slots, int64_t u, int lane,
+                                              int kvh, int bs, int32_t* __restrict__ kq,
+                                              float* __restrict__ ks, float* __restrict__ km) {
   constexpr int D = 128;
   constexpr int TPL = G / 8;  // tokens per lane
-  const int64_t u = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (u >= units) return;  // whole wave
-  const int lane = threadIdx.x & 63;
   const int hf = static_cast<int>(u & 1);
   const int h = static_cast<int>((u >> 1) % kvh);
   const int64_t t0 = (u >> 1) / kvh * G;
@@ -248,6 +246,18 @@ kivi_pack_key_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __r
       km[sidx] = mn[j];
     }
   }
+}
+
+template <typename T, typename I, int G>
+__global__ void __launch_bounds__(256)
+kivi_pack_key_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __restrict__ src_b,
+                          const int64_t* __restrict__ src_index, const I* __restrict__ slots,
+                          int64_t units, int kvh, int bs, int32_t* __restrict__ kq,
+                          float* __restrict__ ks, float* __restrict__ km) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (u >= units) return;  // whole wave
+  key_pack_wave<T, I, G>(src_a, n_a, src_b, src_index, slots, u, threadIdx.x & 63, kvh, bs, kq,
+                         ks, km);
 }
 
 template <typename T, typename I>
@@ -339,6 +349,49 @@ ring_write_kernel(const TS* __restrict__ src, const int64_t* __restrict__ src_ro
   store8(ring + dst_rows[i] * row_elems + c, x);
 }
 
+// One value word: the lane's 8 dims x (word w of a row of head h, stored at
+// page slot `slot`).  The head-dim group's min/max is a butterfly over its gw
+// adjacent lanes; every lane of the wave runs it (lanes of rows past the end
+// included), then only valid lanes with a slot store.
+template <int WPR>
+__device__ __forceinline__ void value_pack_word(const float (&x)[8], int w, bool valid,
+                                                int64_t slot, int h, int kvh, int gw, int ng,
+                                                int32_t* __restrict__ vq, float* __restrict__ vs,
+                                                float* __restrict__ vm) {
+  float mn = x[0], mx = x[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) {
+    mn = fminf(mn, x[i]);
+    mx = fmaxf(mx, x[i]);
+  }
+  // every step runs; steps at or past gw keep the lane's value (a uniform
+  // select, no branch)
+#define KVQ_GROUP_STEP(O)                                               \
+  {                                                                     \
+    const float pn = fminf(mn, lane_xor<O>(mn));                        \
+    const float px = fmaxf(mx, lane_xor<O>(mx));                        \
+    mn = gw > O ? pn : mn;                                              \
+    mx = gw > O ? px : mx;                                              \
+  }
+  if (WPR > 1) KVQ_GROUP_STEP(1)
+  if (WPR > 2) KVQ_GROUP_STEP(2)
+  if (WPR > 4) KVQ_GROUP_STEP(4)
+  if (WPR > 8) KVQ_GROUP_STEP(8)
+  if (WPR > 16) KVQ_GROUP_STEP(16)
+  if (WPR > 32) KVQ_GROUP_STEP(32)
+#undef KVQ_GROUP_STEP
+  if (!valid || slot < 0) return;
+  const float sc = kivi_group_scale(mn, mx);
+  const uint32_t word = kivi_pack_word(x, mn, sc);
+  const int64_t orow = slot * kvh + h;  // page row (blk * bs + off) of head h
+  __builtin_nontemporal_store(word, reinterpret_cast<uint32_t*>(vq) + orow * WPR + w);
+  if (w % gw == 0) {
+    const int64_t sidx = orow * ng + w / gw;
+    vs[sidx] = sc;
+    vm[sidx] = mn;
+  }
+}
+
 // ---- wave-pipelined value pack ---------------------------------------------
 // Waves walk their units with a register double buffer: the next units'
 // source rows are in flight while the current ones are reduced, quantized and
@@ -396,41 +449,9 @@ kivi_pack_value_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* _
       const int64_t r = (u0 + k) * RPU + lane / WPR;
       float x[8];
       b.x[k].get(x);
-      float mn = x[0], mx = x[0];
-#pragma unroll
-      for (int i = 1; i < 8; ++i) {
-        mn = fminf(mn, x[i]);
-        mx = fmaxf(mx, x[i]);
-      }
-      // butterfly over the group's gw lanes: every step runs, steps at or past
-      // gw keep the lane's value (a uniform select, no branch)
-#define KVQ_GROUP_STEP(O)                                               \
-      {                                                                 \
-        const float pn = fminf(mn, lane_xor<O>(mn));                    \
-        const float px = fmaxf(mx, lane_xor<O>(mx));                    \
-        mn = gw > O ? pn : mn;                                          \
-        mx = gw > O ? px : mx;                                          \
-      }
-      if (WPR > 1) KVQ_GROUP_STEP(1)
-      if (WPR > 2) KVQ_GROUP_STEP(2)
-      if (WPR > 4) KVQ_GROUP_STEP(4)
-      if (WPR > 8) KVQ_GROUP_STEP(8)
-      if (WPR > 16) KVQ_GROUP_STEP(16)
-      if (WPR > 32) KVQ_GROUP_STEP(32)
-#undef KVQ_GROUP_STEP
-      const int64_t slot = b.slot[k];
-      if (r >= rows || slot < 0) continue;
-      const float sc = kivi_group_scale(mn, mx);
-      const uint32_t word = kivi_pack_word(x, mn, sc);
-      const uint32_t t = kvh_div.div(static_cast<uint32_t>(r));
-      const int h = static_cast<int>(r) - static_cast<int>(t) * kvh;
-      const int64_t orow = slot * kvh + h;  // page row (blk * bs + off) of head h
-      __builtin_nontemporal_store(word, reinterpret_cast<uint32_t*>(vq) + orow * WPR + w);
-      if (w % gw == 0) {
-        const int64_t sidx = orow * ng + w / gw;
-        vs[sidx] = sc;
-        vm[sidx] = mn;
-      }
+      const uint32_t t = kvh_div.div(static_cast<uint32_t>(r < rows ? r : rows - 1));
+      const int h = static_cast<int>(r < rows ? r : rows - 1) - static_cast<int>(t) * kvh;
+      value_pack_word<WPR>(x, w, r < rows, b.slot[k], h, kvh, gw, ng, vq, vs, vm);
     }
   };
 
@@ -445,6 +466,68 @@ kivi_pack_value_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* _
     if (u + 2 * step < units) load(ba, u + 2 * step);
     compute(bb, u + step);
   }
+}
+
+// ---- one-launch store -------------------------------------------------------
+// A store batch (key pack groups, value pack rows, ring-row writes of both
+// sides) whose ring writes overwrite no row that the same batch packs has no
+// order inside it, so it runs as one grid of 4-wave workgroups split into
+// [key pack | value pack | ring rows].  Pack sources index [ring rows ; input
+// rows]; ring writes copy input rows to ring rows (same dtype, 16 bytes per
+// thread).  jobs (int64): key pack src | key pack slot | value pack src |
+// value pack slot | key ring src | key ring dst | value ring src | value ring
+// dst.  The ring is read (pack sources) and written (ring rows) by the same
+// grid, so its pointers are not restrict-qualified.
+template <typename T, int G>
+__global__ void __launch_bounds__(256)
+kivi_store_kernel(T* ring_k, T* ring_v, int64_t n_ring, const T* __restrict__ in_k,
+                  const T* __restrict__ in_v, const int64_t* __restrict__ jobs, int64_t nkp,
+                  int64_t nvp, int64_t nkr, int64_t nvr, int64_t kblocks, int64_t vblocks,
+                  FastDiv kvh_div, int bs, int32_t* __restrict__ kq, float* __restrict__ ks,
+                  float* __restrict__ km, int32_t* __restrict__ vq, float* __restrict__ vs,
+                  float* __restrict__ vm) {
+  constexpr int D = 128;
+  constexpr int WPR = D / 8;
+  const int kvh = static_cast<int>(kvh_div.d);
+  const int64_t row_elems = static_cast<int64_t>(kvh) * D;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int64_t b = blockIdx.x;
+  if (b < kblocks) {
+    const int64_t u = b * 4 + wave;
+    if (u < nkp / G * kvh * 2)
+      key_pack_wave<T, int64_t, G>(ring_k, n_ring, in_k, jobs, jobs + nkp, u, lane, kvh, bs, kq,
+                                   ks, km);
+    return;
+  }
+  b -= kblocks;
+  if (b < vblocks) {
+    const int64_t* vsrc = jobs + 2 * nkp;
+    const int64_t* vslot = vsrc + nvp;
+    const int64_t rows = nvp * kvh;  // the host keeps this below 2^31
+    const int64_t r = (b * 4 + wave) * (64 / WPR) + lane / WPR;
+    const int64_t rc = r < rows ? r : rows - 1;  // past the end: read the last row, store nothing
+    const uint32_t t = kvh_div.div(static_cast<uint32_t>(rc));
+    const int h = static_cast<int>(rc) - static_cast<int>(t) * kvh;
+    const int w = lane % WPR;
+    float x[8];
+    load8(src_row<T>(ring_v, n_ring, in_v, vsrc[t], row_elems) + h * D + w * 8, x);
+    value_pack_word<WPR>(x, w, r < rows, vslot[t], h, kvh, G / 8, D / G, vq, vs, vm);
+    return;
+  }
+  b -= vblocks;
+  const int per_row = kvh * (D / 8);
+  const int64_t c = b * 256 + threadIdx.x;
+  const int64_t i = c / per_row;
+  if (i >= nkr + nvr) return;
+  const int64_t e = (c - i * per_row) * 8;
+  const bool key = i < nkr;
+  const int64_t j = key ? i : i - nkr;
+  const int64_t n = key ? nkr : nvr;
+  const int64_t* rs = jobs + 2 * (nkp + nvp) + (key ? 0 : 2 * nkr);
+  const T* src = (key ? in_k : in_v) + rs[j] * row_elems + e;
+  T* dst = (key ? ring_k : ring_v) + rs[n + j] * row_elems + e;
+  *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
 }
 
 // Workgroups of `kernel` that fit the device at once (CUs x occupancy),
@@ -605,6 +688,58 @@ extern "C" int kvq_kivi_ring_write(const void* src, int src_dtype, const int64_t
       hipLaunchKernelGGL((ring_write_kernel<TS, TD>), dim3(static_cast<unsigned>(blocks)),
                          dim3(256), 0, s, static_cast<const TS*>(src), src_rows, dst_rows,
                          num_rows, row_elems, static_cast<TD*>(ring))));
+  KVQ_LAUNCH_CHECK();
+  return KVQ_OK;
+}
+
+extern "C" int kvq_kivi_store(const void* key_input, const void* value_input, void* ring_k,
+                              void* ring_v, int64_t ring_rows, int dtype, int num_kv_heads,
+                              int head_size, int group_size, int block_size, const int64_t* jobs,
+                              int64_t n_key_pack, int64_t n_value_pack, int64_t n_key_ring,
+                              int64_t n_value_ring, int32_t* k_quant, float* k_scale,
+                              float* k_mn, int32_t* v_quant, float* v_scale, float* v_mn,
+                              void* stream) {
+  if (n_key_pack < 0 || n_value_pack < 0 || n_key_ring < 0 || n_value_ring < 0 ||
+      ring_rows < 0)
+    return KVQ_ERR_INVALID;
+  if (n_key_pack + n_value_pack + n_key_ring + n_value_ring == 0) return KVQ_OK;
+  if (!jobs || !ring_k || !ring_v) return KVQ_ERR_INVALID;
+  if ((n_key_pack || n_key_ring) && !key_input) return KVQ_ERR_INVALID;
+  if ((n_value_pack || n_value_ring) && !value_input) return KVQ_ERR_INVALID;
+  if (n_key_pack && (!k_quant || !k_scale || !k_mn)) return KVQ_ERR_INVALID;
+  if (n_value_pack && (!v_quant || !v_scale || !v_mn)) return KVQ_ERR_INVALID;
+  if (!kivi_geometry_ok(num_kv_heads, head_size, group_size, block_size))
+    return KVQ_ERR_GEOMETRY;
+  // the register key pack's geometry; callers fall back to the separate
+  // pack and ring-write entry points elsewhere
+  if (head_size != 128 || (group_size != 64 && group_size != 128) ||
+      (dtype != KVQ_DTYPE_BF16 && dtype != KVQ_DTYPE_F16))
+    return KVQ_ERR_GEOMETRY;
+  if (n_key_pack % group_size) return KVQ_ERR_INVALID;
+  if (n_value_pack * num_kv_heads >= 0x7fffffff) return KVQ_ERR_INVALID;
+  const int64_t kunits = n_key_pack / group_size * num_kv_heads * 2;
+  const int64_t kblocks = (kunits + 3) / 4;
+  const int64_t vunits = (n_value_pack * num_kv_heads + 3) / 4;  // 4 rows per wave
+  const int64_t vblocks = (vunits + 3) / 4;
+  const int64_t rchunks = (n_key_ring + n_value_ring) * num_kv_heads * (head_size / 8);
+  const int64_t rblocks = (rchunks + 255) / 256;
+  const int64_t blocks = kblocks + vblocks + rblocks;
+  if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const FastDiv kdiv = FastDiv::make(static_cast<uint32_t>(num_kv_heads));
+#define KVQ_LAUNCH_STORE(T, GG)                                                               \
+  hipLaunchKernelGGL((kivi_store_kernel<T, GG>), dim3(static_cast<unsigned>(blocks)),         \
+                     dim3(256), 0, s, static_cast<T*>(ring_k), static_cast<T*>(ring_v),        \
+                     ring_rows, static_cast<const T*>(key_input),                              \
+                     static_cast<const T*>(value_input), jobs, n_key_pack, n_value_pack,       \
+                     n_key_ring, n_value_ring, kblocks, vblocks, kdiv, block_size, k_quant,    \
+                     k_scale, k_mn, v_quant, v_scale, v_mn)
+  if (dtype == KVQ_DTYPE_BF16) {
+    if (group_size == 128) { KVQ_LAUNCH_STORE(bf16, 128); } else { KVQ_LAUNCH_STORE(bf16, 64); }
+  } else {
+    if (group_size == 128) { KVQ_LAUNCH_STORE(f16, 128); } else { KVQ_LAUNCH_STORE(f16, 64); }
+  }
+#undef KVQ_LAUNCH_STORE
   KVQ_LAUNCH_CHECK();
   return KVQ_OK;
 }

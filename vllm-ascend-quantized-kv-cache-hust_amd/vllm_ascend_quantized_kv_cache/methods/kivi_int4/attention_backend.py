@@ -291,6 +291,13 @@ class AscendKiviInt4AttentionBackendMixin:
     def _execute_kivi_plan(self, plan: StorePlan, key: Any, value: Any) -> None:
         if plan.empty():
             return
+        # the one-launch store stands in for the three launch hooks below, so
+        # it is used only while none of them (or the hooks they defer to) is
+        # replaced
+        hooks = ("_launch_kivi_key_pack", "_launch_kivi_value_pack",
+                 "_launch_kivi_key_pack_rows", "_launch_kivi_value_pack_rows",
+                 "_launch_kivi_ring_write", "_launch_kivi_store")
+        store = None if any(_hook_replaced(self, h) for h in hooks) else self._launch_kivi_store
         self._kivi_ring.execute(
             plan,
             key,
@@ -298,6 +305,7 @@ class AscendKiviInt4AttentionBackendMixin:
             pack_key=self._launch_kivi_key_pack_rows,
             pack_value=self._launch_kivi_value_pack_rows,
             ring_write=self._launch_kivi_ring_write,
+            store=store,
         )
 
     def _adopt_ring_dtype(self, *tensors: Any) -> None:
@@ -563,6 +571,17 @@ class AscendKiviInt4AttentionBackendMixin:
         from ...ops.kivi_pack import ring_write
 
         ring_write(self._kivi_ring.tensor(is_key), src, src_rows, dst_rows)
+
+    def _launch_kivi_store(self, key: Any, value: Any, jobs: Any, counts: Any) -> bool:
+        """A whole hazard-free store batch in one launch (``kvq_kivi_store``);
+        False when the geometry needs the separate pack and ring launches."""
+        from ...ops.kivi_pack import kivi_store
+
+        ring = self._kivi_ring
+        caches = (self.k_quant_cache, self.k_scale_cache, self.k_mn_cache,
+                  self.v_quant_cache, self.v_scale_cache, self.v_mn_cache)
+        return kivi_store(key, value, ring.key, ring.value, jobs, counts, caches,
+                          self.kivi_group_size)
 
     def _launch_kivi_gather(self, block_table: Any, cu_seqlens: Any, total: int,
                             target_dtype: Any, ring_meta: Any) -> tuple[Any, Any]:

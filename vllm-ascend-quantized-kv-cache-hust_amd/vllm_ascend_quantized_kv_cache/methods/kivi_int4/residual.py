@@ -13,11 +13,16 @@ reading the device:
 * otherwise, while the window is full, keys flush the whole window and values
   evict the single oldest lane (``:448-455``); then the token is appended.
 
+A row has ``R + 1`` lanes for a window of ``R`` tokens: the free lane is where
+the next token goes, so a step that evicts and appends never writes the lane
+it packs, and the whole step can run as one launch.
+
 Replaying a batch of tokens yields a ``StorePlan``: packed-history writes
 (sources are old ring lanes or rows of this step's input) and final ring-lane
-writes.  ``execute`` issues them as at most three launches per side (key
-pack, value pack, ring write), in an order that reads every old lane before
-it is overwritten.
+writes.  ``execute`` issues them as one launch when no ring write of the batch
+overwrites a lane the batch packs (every single-token step), otherwise as up
+to three launches per side (key pack, value pack, ring write), in an order
+that reads every old lane before it is overwritten.
 """
 
 from __future__ import annotations
@@ -55,21 +60,43 @@ class StorePlan:
     def empty(self) -> bool:
         return self.key.empty() and self.value.empty()
 
+    def one_launch_jobs(self) -> tuple[list[int], tuple[int, int, int, int]] | None:
+        """``(jobs, counts)`` for a single store launch, or ``None``.
+
+        ``jobs`` is key pack src | key pack slot | value pack src | value pack
+        slot | key ring src | key ring dst | value ring src | value ring dst;
+        ``counts`` the four lengths.  ``None`` when a ring write overwrites a
+        ring row the same batch packs: the packs must then run first.
+        """
+        k, v = self.key, self.value
+        for side in (k, v):
+            if side.ring and side.pack_src and not side.ring.keys().isdisjoint(side.pack_src):
+                return None
+        jobs = (k.pack_src + k.pack_slots + v.pack_src + v.pack_slots
+                + list(k.ring.values()) + list(k.ring.keys())
+                + list(v.ring.values()) + list(v.ring.keys()))
+        return jobs, (len(k.pack_src), len(v.pack_src), len(k.ring), len(v.ring))
+
 
 class KiviResidualRing:
-    """Ring tensors ``[rows, R, KVH, D]`` (keys, values) plus their host mirror."""
+    """Ring tensors ``[rows, R + 1, KVH, D]`` (keys, values) plus their host mirror.
+
+    ``window`` is the residual length ``R``; ``ring_len = R + 1`` lanes per row.
+    """
 
     def __init__(
         self,
         rows: int,
-        ring_len: int,
+        window: int,
         num_kv_heads: int,
         head_size: int,
         *,
         device,
         dtype=torch.float32,
     ) -> None:
+        ring_len = window + 1
         self.rows = rows
+        self.window = window
         self.ring_len = ring_len
         self.num_kv_heads = num_kv_heads
         self.head_size = head_size
@@ -188,6 +215,7 @@ class KiviResidualRing:
         """
         side = plan.side(is_key)
         r = self.ring_len
+        cap = self.window
         na = self.rows * r
         base = row * r
         ls = self.lane_slot[is_key][row]
@@ -202,8 +230,8 @@ class KiviResidualRing:
                 side.lane_src[base + lane] = na + irow
                 side.ring[base + lane] = irow
                 continue
-            while self.length[is_key][row] >= r:
-                count = r if is_key else 1
+            while self.length[is_key][row] >= cap:
+                count = cap if is_key else 1
                 ev = self.lanes(row, is_key=is_key)[:count]
                 ev_slots = [ls[lane] for lane in ev]
                 if is_key:
@@ -220,9 +248,11 @@ class KiviResidualRing:
                     ls[lane] = -1
                     side.ring.pop(base + lane, None)
                     side.lane_src.pop(base + lane, None)
-                n = self.length[is_key][row] - count
-                self.length[is_key][row] = n
-                self.start[is_key][row] = (self.start[is_key][row] + count) % r if n else 0
+                # the start moves past the evicted lanes even when the window
+                # empties, so the append below lands on the lane that was free
+                # before this flush, never on one it packs
+                self.length[is_key][row] -= count
+                self.start[is_key][row] = (self.start[is_key][row] + count) % r
             tail = (self.start[is_key][row] + self.length[is_key][row]) % r
             ls[tail] = slot
             sl[slot] = tail
@@ -254,7 +284,7 @@ class KiviResidualRing:
             side.ring.pop(base + lane, None)
             side.lane_src.pop(base + lane, None)
         self.length[is_key][row] = n - count
-        self.start[is_key][row] = (self.start[is_key][row] + count) % self.ring_len if n - count else 0
+        self.start[is_key][row] = (self.start[is_key][row] + count) % self.ring_len
 
     # -- execution ---------------------------------------------------------
 
@@ -267,15 +297,32 @@ class KiviResidualRing:
         pack_key,
         pack_value,
         ring_write,
+        store=None,
     ) -> None:
-        """Issue a plan: history packs first (they read old lanes), then ring writes.
+        """Issue a plan: one launch when the plan allows it, else history packs
+        first (they read old lanes), then ring writes.
 
         ``pack_key/pack_value(src_a, src_b, src_index, slots)`` and
         ``ring_write(src, src_rows, dst_rows, is_key)`` are the launch hooks;
-        ``src_a`` is the ring viewed as ``[rows*R, KVH, D]``, ``src_b`` the
-        step's input converted to the ring dtype.
+        ``src_a`` is the ring viewed as ``[rows*(R+1), KVH, D]``, ``src_b`` the
+        step's input converted to the ring dtype.  ``store(key_input,
+        value_input, jobs, counts)`` (optional) issues a whole hazard-free plan
+        (``StorePlan.one_launch_jobs``) and returns False when it cannot.
         """
         dev = self.key.device
+        if store is not None:
+            one = plan.one_launch_jobs()
+            if one is not None:
+                jobs, counts = one
+                kin, vin = (
+                    None if x is None else x.to(self.dtype).contiguous()
+                    for x in (key_input, value_input)
+                )
+                jt = torch.tensor(jobs, dtype=torch.int64).to(dev, non_blocking=True)
+                if store(kin, vin, jt, counts):
+                    if counts[2] or counts[3]:
+                        self.written = True
+                    return
         inputs = {True: key_input, False: value_input}
         for is_key in (True, False):
             side = plan.side(is_key)

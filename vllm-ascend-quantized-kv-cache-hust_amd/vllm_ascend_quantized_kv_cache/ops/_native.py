@@ -36,6 +36,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_P, _I64, _P, _P, _I, _P, _I, _I64, _I, _I, _I, _I, _P, _P, _P, _P],
     ),
     "kvq_kivi_ring_write": (_I, [_P, _I, _P, _P, _I64, _I, _P, _I, _P]),
+    "kvq_kivi_store": (
+        _I,
+        [_P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _I64, _I64, _I64, _I64,
+         _P, _P, _P, _P, _P, _P, _P],
+    ),
     "kvq_kivi_gather_dequant": (
         _I,
         [_P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _P, _I, _I64, _P, _I64,

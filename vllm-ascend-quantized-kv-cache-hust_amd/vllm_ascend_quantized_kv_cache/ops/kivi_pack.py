@@ -180,10 +180,52 @@ def ring_write(
     _native.check(rc, "kvq_kivi_ring_write")
 
 
+def store_one_launch_supported(head_size: int, group_size: int, dtype: torch.dtype) -> bool:
+    """Geometries ``kvq_kivi_store`` runs (the others use the separate launches)."""
+    return head_size == 128 and group_size in (64, 128) and dtype in (torch.bfloat16, torch.float16)
+
+
+def kivi_store(
+    key_input: torch.Tensor | None,
+    value_input: torch.Tensor | None,
+    ring_k: torch.Tensor,
+    ring_v: torch.Tensor,
+    jobs: torch.Tensor,
+    counts: tuple[int, int, int, int],
+    caches: tuple[torch.Tensor, ...],
+    group_size: int,
+) -> bool:
+    """Key pack, value pack and both ring writes of a store batch in one launch.
+
+    ``jobs`` (int64, on the device) and ``counts`` come from
+    ``StorePlan.one_launch_jobs``; inputs are ``[n, KVH, D]`` contiguous in the
+    ring dtype.  Returns False (nothing launched) for a geometry the one-launch
+    kernel does not cover.
+    """
+    kq, ks, km, vq, vs, vm = caches
+    nb, kvh, d, pbs = kq.shape
+    if not store_one_launch_supported(d, group_size, ring_k.dtype):
+        return False
+    if sum(counts) == 0:
+        return True
+    _native.require_gpu_tensors("kivi store", ring_k, ring_v, jobs, kq, key_input, value_input)
+    rc = _native.lib().kvq_kivi_store(
+        _native.ptr(key_input), _native.ptr(value_input), _native.ptr(ring_k),
+        _native.ptr(ring_v), ring_k.shape[0] * ring_k.shape[1], _native.dtype_code(ring_k.dtype),
+        kvh, d, group_size, pbs * 8, _native.ptr(jobs), *counts,
+        _native.ptr(kq), _native.ptr(ks), _native.ptr(km), _native.ptr(vq), _native.ptr(vs),
+        _native.ptr(vm), _native.stream_of(ring_k),
+    )
+    _native.check(rc, "kvq_kivi_store")
+    return True
+
+
 __all__ = [
     "kivi_pack_key_cache",
     "kivi_pack_value_cache",
+    "kivi_store",
     "pack_key_rows",
     "pack_value_rows",
     "ring_write",
+    "store_one_launch_supported",
 ]
