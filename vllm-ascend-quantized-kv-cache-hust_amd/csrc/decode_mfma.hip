@@ -151,8 +151,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 // apart) as pairs with ds_read2_b32.  tk(st, kg, i) is the token of PV slot
 // 8*kg + i in k-step st: the token whose p the lane already holds from the
 // score layout.
-template <int CPG>
+// VG1: one value group spans the whole head (G >= 128 at CPG 8), so every PV
+// column group shares the token's value scale and min: they are gathered and
+// applied once per PV k-step instead of once per column group.
+template <int CPG, bool VG1 = false>
 struct Tile {
+  static_assert(!VG1 || CPG == 8, "VG1 needs 64-token tiles");
   static constexpr int D = 128;
   static constexpr int GT = 8 * CPG;    // tokens per tile
   static constexpr int NJ = CPG / 2;    // score MFMAs per k-step (16 tokens each)
@@ -160,21 +164,25 @@ struct Tile {
   static constexpr int NVG = 16 / CPG;  // PV column groups (one value group each)
   static constexpr int NJJ = CPG / 2;   // PV MFMAs per column group (NVG * NJJ == 8)
   static constexpr int PVS = CPG / 4;   // PV k-steps (32 tokens) per tile
+  static constexpr int NVS = VG1 ? 1 : NVG;  // value scale/min groups per PV k-step
   static constexpr int KW = 0;
   static constexpr int KS = KW + D * CPG;
   static constexpr int KM = KS + D;
   static constexpr int KEY_WORDS = KM + D;  // the key part: a wave's own region
   static constexpr int VW = KEY_WORDS;
   static constexpr int VS = VW + GT * 16;
-  static constexpr int VM = VS + PVS * NVG * 32;
-  static constexpr int WORDS = VM + PVS * NVG * 32;
+  static constexpr int VM = VS + PVS * NVS * 32;
+  static constexpr int WORDS = VM + PVS * NVS * 32;
   static constexpr int BYTES = 4 * WORDS;
   // DMA instructions per tile; the waits rely on this number
   static constexpr int KW_INST = D * CPG * 4 / 1024;  // 16-byte lanes
   static constexpr int VW_INST = GT * 64 / 1024;      // 16-byte lanes
   static constexpr int KS_INST = D / 64;              // 4-byte lanes
-  static constexpr int VS_INST = PVS * NVG * 32 / 64; // 4-byte lanes
+  static constexpr int VS_INST = PVS * NVS * 32 / 64; // 4-byte lanes
   static constexpr int NINST = KW_INST + VW_INST + 2 * KS_INST + 2 * VS_INST;
+  // a tile that continues the previous tile's key group skips the key
+  // scale/min DMA (prepare_group reads them only at a group's first tile)
+  static constexpr int NINST_CONT = NINST - 2 * KS_INST;
   static_assert(NINST < 64, "vmcnt range");
 };
 
@@ -205,10 +213,10 @@ __device__ __forceinline__ int key_scale_off(int e, int gpb) {
   const int ii = e % 8, kg = (e / 8) % 4, s4 = e / 32;
   return (32 * s4 + 4 * ii + kg) * gpb;
 }
-template <int CPG>
+template <int CPG, bool VG1>
 __device__ __forceinline__ int value_scale_off(int e, int kvh, int ng, int g) {
-  constexpr int NVG = 16 / CPG;
-  const int i8 = e % 8, kg = (e / 8) % 4, v = (e / 32) % NVG, st = e / (32 * NVG);
+  constexpr int NVS = Tile<CPG, VG1>::NVS;
+  const int i8 = e % 8, kg = (e / 8) % 4, v = (e / 32) % NVS, st = e / (32 * NVS);
   return tile_token<CPG>(st, kg, i8) * kvh * ng + (8 * CPG * v) / g;
 }
 
@@ -216,14 +224,14 @@ struct LaneDma {
   uint32_t k, v, ks, vs;  // byte offsets of this lane's DMA data (lane part)
 };
 
-template <int CPG>
+template <int CPG, bool VG1>
 __device__ __forceinline__ LaneDma lane_dma(int lane, int wpd, int kvh, int gpb, int ng, int g) {
   constexpr int LPR = CPG / 4;  // 16-byte lanes per key dim row (CPG words)
   LaneDma ld;
   ld.k = static_cast<uint32_t>(4 * ((lane / LPR) * wpd + 4 * (lane % LPR)));
   ld.v = static_cast<uint32_t>(4 * ((lane / 4) * kvh * 16 + 4 * (lane % 4)));
   ld.ks = static_cast<uint32_t>(4 * key_scale_off<CPG>(lane, gpb));
-  ld.vs = static_cast<uint32_t>(4 * value_scale_off<CPG>(lane, kvh, ng, g));
+  ld.vs = static_cast<uint32_t>(4 * value_scale_off<CPG, VG1>(lane, kvh, ng, g));
   return ld;
 }
 
@@ -234,7 +242,7 @@ __device__ __forceinline__ LaneDma lane_dma(int lane, int wpd, int kvh, int gpb,
 template <int CPG>
 __device__ __forceinline__ void issue_keys(char* buf, const LaneDma& ld, const uint32_t* kq_t,
                                            int wpd, const float* ks_t, const float* km_t,
-                                           int gpb) {
+                                           int gpb, bool with_ks) {
   using T = Tile<CPG>;
   constexpr int LPR = CPG / 4;
   constexpr int DPI = 64 / LPR;  // key dim rows per instruction
@@ -244,6 +252,7 @@ __device__ __forceinline__ void issue_keys(char* buf, const LaneDma& ld, const u
 #pragma unroll
   for (int i = 0; i < T::KW_INST; ++i)
     dma16(kb + 4 * (i * DPI * wpd) + ld.k, buf + 4 * T::KW + 1024 * i);
+  if (!with_ks) return;  // uniform
 #pragma unroll
   for (int i = 0; i < T::KS_INST; ++i) {
     const int o = 4 * key_scale_off<CPG>(64 * i, gpb);
@@ -255,13 +264,14 @@ __device__ __forceinline__ void issue_keys(char* buf, const LaneDma& ld, const u
 // DMA of one whole tile (keys and the gathered value operands) for kv head h
 // into the wave's tile buffer; vq_t, vs_t, vm_t point at the tile's first value
 // word / scale of head h.
-template <int CPG>
+template <int CPG, bool VG1>
 __device__ __forceinline__ void issue_tile(char* buf, const LaneDma& ld, const uint32_t* kq_t,
                                            int wpd, const uint32_t* vq_t, int kvh,
                                            const float* ks_t, const float* km_t, int gpb,
-                                           const float* vs_t, const float* vm_t, int ng, int g) {
-  using T = Tile<CPG>;
-  issue_keys<CPG>(buf, ld, kq_t, wpd, ks_t, km_t, gpb);
+                                           const float* vs_t, const float* vm_t, int ng, int g,
+                                           bool with_ks) {
+  using T = Tile<CPG, VG1>;
+  issue_keys<CPG>(buf, ld, kq_t, wpd, ks_t, km_t, gpb, with_ks);
   const char* vb = reinterpret_cast<const char*>(vq_t);
   const char* vsb = reinterpret_cast<const char*>(vs_t);
   const char* vmb = reinterpret_cast<const char*>(vm_t);
@@ -270,7 +280,7 @@ __device__ __forceinline__ void issue_tile(char* buf, const LaneDma& ld, const u
     dma16(vb + 4 * (16 * i * kvh * 16) + ld.v, buf + 4 * T::VW + 1024 * i);
 #pragma unroll
   for (int i = 0; i < T::VS_INST; ++i) {
-    const int o = 4 * value_scale_off<CPG>(64 * i, kvh, ng, g);
+    const int o = 4 * value_scale_off<CPG, VG1>(64 * i, kvh, ng, g);
     dma4(vsb + o + ld.vs, buf + 4 * (T::VS + 64 * i));
     dma4(vmb + o + ld.vs, buf + 4 * (T::VM + 64 * i));
   }
@@ -293,15 +303,15 @@ __device__ __forceinline__ void read8f(const uint32_t* p, float (&f)[8]) {
 // gathered copy (VW [token][16 words]; VS, VM in PV-slot order, 8 consecutive
 // floats per lane and step), resolved to the lane (kg, chunk) once so that
 // each read is a base plus an immediate offset.
-template <int CPG>
+template <int CPG, bool VG1>
 struct WaveValues {
   const uint32_t* vw;  // VW + 16 * tile_token_lane(kg) + chunk
   const uint32_t* sm;  // the tile + 8 * kg
   __device__ __forceinline__ WaveValues(const uint32_t* W, int kg, int chunk)
-      : vw(W + Tile<CPG>::VW + 16 * tile_token_lane<CPG>(kg) + chunk), sm(W + 8 * kg) {}
+      : vw(W + Tile<CPG, VG1>::VW + 16 * tile_token_lane<CPG>(kg) + chunk), sm(W + 8 * kg) {}
   __device__ __forceinline__ void scales(int st, int v, float (&sc)[8], float (&mn)[8]) const {
-    using T = Tile<CPG>;
-    const int base = (st * T::NVG + v) * 32;
+    using T = Tile<CPG, VG1>;
+    const int base = (st * T::NVS + (VG1 ? 0 : v)) * 32;
     read8f(sm + T::VS + base, sc);
     read8f(sm + T::VM + base, mn);
   }
@@ -457,7 +467,7 @@ __device__ __forceinline__ float add_ror8(float x) {
 
 // One tile of scores, softmax update and PV.  FULL: every token < pe.  W is
 // the wave's key region; `vals` reads the tile's value operands.
-template <typename TQ, int CPG, bool FULL, bool FOLD, typename VALS>
+template <typename TQ, int CPG, bool VG1, bool FULL, bool FOLD, typename VALS>
 __device__ __forceinline__ void compute_tile(const uint32_t* W, const VALS& vals, int p0, int pe, int n, int kg,
                                              const QGroup& qg, float qscale,
                                              const LaneNib<CPG>& ln, float& m_run, float& l_run, f4 (&o_acc)[8],
@@ -465,7 +475,7 @@ __device__ __forceinline__ void compute_tile(const uint32_t* W, const VALS& vals
   // attention math is tolerance-checked: let mul+add fuse here (the library
   // builds with -ffp-contract=off for the bit-exact pack/dequant paths)
 #pragma clang fp contract(fast)
-  using T = Tile<CPG>;
+  using T = Tile<CPG, VG1>;
   const int chunk = n % CPG;
   const h8 ones_b = as_h8(kMagic, kMagic, kMagic, kMagic);
   // ---- scores ----------------------------------------------------------------
@@ -537,16 +547,20 @@ __device__ __forceinline__ void compute_tile(const uint32_t* W, const VALS& vals
   }
   l_run = l_run * alpha + sum_kg(psum);
   m_run = m_new;
+  // once the running max settles most tiles leave it alone (alpha == 1 on
+  // every lane): the rescale is skipped as a whole (multiplying by 1 is exact)
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float ar = __shfl(alpha, 4 * kg + r, 64);
+    for (int r = 0; r < 4; ++r) {
+      const float ar = __shfl(alpha, 4 * kg + r, 64);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) o_acc[q][r] *= ar;
+      for (int q = 0; q < 8; ++q) o_acc[q][r] *= ar;
 #pragma unroll
-    for (int v = 0; v < T::NVG; ++v) c_acc[v][r] *= ar;
+      for (int v = 0; v < T::NVS; ++v) c_acc[v][r] *= ar;
+    }
+#pragma unroll
+    for (int v = 0; v < T::NVS; ++v) bias_v[v] *= alpha;
   }
-#pragma unroll
-  for (int v = 0; v < T::NVG; ++v) bias_v[v] *= alpha;
 
   // ---- PV ----------------------------------------------------------------------
 #pragma unroll
@@ -554,27 +568,30 @@ __device__ __forceinline__ void compute_tile(const uint32_t* W, const VALS& vals
     float pv[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) pv[i] = sacc[2 * st + i / 4][i % 4];
+    h8 a;  // P' of the k-step for column group v (VG1: for all of them)
 #pragma unroll
     for (int v = 0; v < T::NVG; ++v) {
-      float sc[8], mn[8];
-      vals.scales(st, v, sc, mn);
-      float pp[8];
+      if (!VG1 || v == 0) {
+        float sc[8], mn[8];
+        vals.scales(st, v, sc, mn);
+        float pp[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float s_ = sc[i], m_ = mn[i];
-        if (!FULL) {
-          // past the range p = 0, but the scale/min bytes are unwritten:
-          // select zeros so a stale NaN cannot reach the sums
-          const bool live = p0 + tile_token<CPG>(st, kg, i) < pe;
-          s_ = live ? s_ : 0.0f;
-          m_ = live ? m_ : 0.0f;
+        for (int i = 0; i < 8; ++i) {
+          float s_ = sc[i], m_ = mn[i];
+          if (!FULL) {
+            // past the range p = 0, but the scale/min bytes are unwritten:
+            // select zeros so a stale NaN cannot reach the sums
+            const bool live = p0 + tile_token<CPG>(st, kg, i) < pe;
+            s_ = live ? s_ : 0.0f;
+            m_ = live ? m_ : 0.0f;
+          }
+          pp[i] = pv[i] * s_;
+          bias_v[v] += pv[i] * m_;
         }
-        pp[i] = pv[i] * s_;
-        bias_v[v] += pv[i] * m_;
+        a = as_h8(pack_h2(pp[0], pp[1]), pack_h2(pp[2], pp[3]), pack_h2(pp[4], pp[5]),
+                  pack_h2(pp[6], pp[7]));
+        c_acc[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ones_b, c_acc[v], 0, 0, 0);
       }
-      const h8 a = as_h8(pack_h2(pp[0], pp[1]), pack_h2(pp[2], pp[3]), pack_h2(pp[4], pp[5]),
-                         pack_h2(pp[6], pp[7]));
-      c_acc[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ones_b, c_acc[v], 0, 0, 0);
       uint32_t w[8];  // word chunk + CPG*v of tokens tk(st, kg, i)
       vals.words(st, v, w);
 #pragma unroll
@@ -646,9 +663,10 @@ struct PageIds {
 // Running state of one wave: softmax max / sum (log2 domain), the PV
 // accumulators (codes read as 1024 + c or 1024 + 16c), the constant-B MFMA
 // sums that remove the 1024 offset, and the value-minima term per column group.
-template <int CPG>
+template <int CPG, bool VG1>
 struct WaveAcc {
   static constexpr int NVG = 16 / CPG;
+  static constexpr int NVS = Tile<CPG, VG1>::NVS;  // c_acc / bias_v entries in use
   float m_run, l_run;
   f4 o_acc[8];
   f4 c_acc[NVG];
@@ -673,20 +691,21 @@ struct WaveAcc {
     constexpr int NJJ = CPG / 2;
     constexpr int SUB = 16 / CPG;
 #pragma unroll
-    for (int v = 0; v < NVG; ++v) bias_v[v] = sum_kg(bias_v[v]);
+    for (int v = 0; v < NVS; ++v) bias_v[v] = sum_kg(bias_v[v]);
     const int64_t head0 = static_cast<int64_t>(wi) * hq + h * rep;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int hh = 4 * kg + r;
 #pragma unroll
       for (int v = 0; v < NVG; ++v) {
-        const float bv = __shfl(bias_v[v], hh, 64);
+        const int vs_ = VG1 ? 0 : v;
+        const float bv = __shfl(bias_v[vs_], hh, 64);
 #pragma unroll
         for (int jj = 0; jj < NJJ; ++jj) {
           const int dim = 8 * (n % CPG + CPG * v) + jj * SUB + n / CPG;
           if (hh < rep)
             ws_o[(head0 + hh) * D + dim] =
-                (o_acc[v * NJJ + jj][r] - c_acc[v][r]) * ln.col_scale + bv;
+                (o_acc[v * NJJ + jj][r] - c_acc[vs_][r]) * ln.col_scale + bv;
         }
       }
     }
@@ -701,7 +720,7 @@ struct WaveAcc {
 // (kind-0) items, the second the tail (kind-1) items, so every tail wave is
 // dispatched after every int4 wave and runs in the slots the shorter int4
 // items free, with no second stream or event between the two.
-template <typename TQ, int CPG, bool FOLD, bool TAIL>
+template <typename TQ, int CPG, bool VG1, bool FOLD, bool TAIL>
 __global__ void __launch_bounds__(64, 2)
 kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qscale,
                         const uint32_t* __restrict__ kq, const float* __restrict__ ks,
@@ -712,7 +731,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
                         const int32_t* __restrict__ work, int64_t num_work,
                         const TQ* __restrict__ ring_k, const TQ* __restrict__ ring_v,
                         int ring_len, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
-  using T = Tile<CPG>;
+  using T = Tile<CPG, VG1>;
   constexpr int D = T::D;
   constexpr int GT = T::GT;
 
@@ -744,19 +763,19 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
 
   const QRegs<TQ> qv = load_q<TQ, FOLD>(query, b, hq, h, rep, n, kg);
   const LaneNib<CPG> ln(n, kg);
-  const LaneDma ld = lane_dma<CPG>(lane, wpd, kvh, gpb, ng, g);
+  const LaneDma ld = lane_dma<CPG, VG1>(lane, wpd, kvh, gpb, ng, g);
 
-  WaveAcc<CPG> acc;
+  WaveAcc<CPG, VG1> acc;
   acc.init();
   PageIds pages(block_table + static_cast<int64_t>(b) * maxb, maxb, nb, bs, pb, pe, lane);
-  auto issue = [&](char* buf, int p) {
+  auto issue = [&](char* buf, int p, bool with_ks) {
     const int64_t blk = pages.page(p);
     const int off0 = p % bs;
     const int64_t krow = (blk * kvh + h) * D;
     const int64_t vtok = (blk * bs + off0) * kvh + h;
-    issue_tile<CPG>(buf, ld, kq + krow * wpd + off0 / 8, wpd, vq + vtok * 16, kvh,
-                    ks + krow * gpb + off0 / g, km + krow * gpb + off0 / g, gpb, vs + vtok * ng,
-                    vm + vtok * ng, ng, g);
+    issue_tile<CPG, VG1>(buf, ld, kq + krow * wpd + off0 / 8, wpd, vq + vtok * 16, kvh,
+                         ks + krow * gpb + off0 / g, km + krow * gpb + off0 / g, gpb,
+                         vs + vtok * ng, vm + vtok * ng, ng, g, with_ks);
   };
   // One tile step: DMA of tile p0 + GT into `nxt`, then compute tile p0 from
   // `cur`.  Both buffers are __restrict__ within the step, which tells the
@@ -768,8 +787,15 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   auto step = [&](const char* __restrict__ cur, char* __restrict__ nxt, int p0) {
     const int p1 = p0 + GT;
     if (p1 < pe) {
-      issue(nxt, p1);
-      wait_vmcnt<T::NINST>();
+      // items start on 128-token boundaries and g <= 128 divides them, so a
+      // tile needs the key scales exactly when it starts a key group
+      if (p1 % g == 0) {
+        issue(nxt, p1, true);
+        wait_vmcnt<T::NINST>();
+      } else {
+        issue(nxt, p1, false);
+        wait_vmcnt<T::NINST_CONT>();
+      }
     } else {
       wait_vmcnt<0>();
     }
@@ -777,15 +803,15 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
     // tiles are GT-aligned and GT divides g: a tile starts a key group or
     // continues the previous tile's
     if (p0 == pb || p0 % g == 0) prepare_group<TQ, CPG, FOLD>(W, n, kg, qv, qscale, qg);
-    const WaveValues<CPG> vals(W, kg, n % CPG);
+    const WaveValues<CPG, VG1> vals(W, kg, n % CPG);
     if (p0 + GT <= pe)
-      compute_tile<TQ, CPG, true, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run, acc.l_run,
-                                  acc.o_acc, acc.c_acc, acc.bias_v);
+      compute_tile<TQ, CPG, VG1, true, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run,
+                                             acc.l_run, acc.o_acc, acc.c_acc, acc.bias_v);
     else
-      compute_tile<TQ, CPG, false, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run, acc.l_run,
-                                   acc.o_acc, acc.c_acc, acc.bias_v);
+      compute_tile<TQ, CPG, VG1, false, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run,
+                                              acc.l_run, acc.o_acc, acc.c_acc, acc.bias_v);
   };
-  if (pb < pe) issue(lds_raw, pb);  // prologue: tile 0 into buffer 0
+  if (pb < pe) issue(lds_raw, pb, true);  // prologue: tile 0 into buffer 0
   int cur = 0;
   for (int p0 = pb; p0 < pe; p0 += GT) {
     step(lds_raw + cur * T::BYTES, lds_raw + (cur ^ 1) * T::BYTES, p0);
@@ -856,20 +882,26 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
   const dim3 block(64);
   // GQA groups of at most 8 heads fold the hi/lo score parts into one MFMA
   const bool fold = hq / kvh <= 8;
-  const size_t lds_int4 = 2 * static_cast<size_t>(cpg == 8 ? Tile<8>::BYTES : Tile<4>::BYTES);
+  // one value group per head row: value scales gathered once per PV k-step
+  const bool vg1 = cpg == 8 && g >= 128;
+  const size_t lds_int4 =
+      2 * static_cast<size_t>(cpg == 8 ? (vg1 ? Tile<8, true>::BYTES : Tile<8>::BYTES)
+                                       : Tile<4>::BYTES);
   const size_t lds_tail = static_cast<size_t>(tail::kLdsBytes);
   const size_t lds = tail && lds_tail > lds_int4 ? lds_tail : lds_int4;
-#define KVQ_LAUNCH_MFMA(TQ, C, F, TL)                                                         \
-  hipLaunchKernelGGL((kivi_decode_mfma_kernel<TQ, C, F, TL>), grid, block, lds, s,           \
+#define KVQ_LAUNCH_MFMA(TQ, C, V, F, TL)                                                      \
+  hipLaunchKernelGGL((kivi_decode_mfma_kernel<TQ, C, V, F, TL>), grid, block, lds, s,        \
                      static_cast<const TQ*>(query), hq, kvh, qscale, kqu, ks, km, vqu, vs, vm,\
                      bs, g, nb, block_table, maxb, seq_meta, work, num_work,                 \
                      static_cast<const TQ*>(ring_k), static_cast<const TQ*>(ring_v),         \
                      ring_len, ws_o, ws_ml)
+#define KVQ_LAUNCH_MFMA_F(TQ, C, V, TL)                                                       \
+  if (fold) KVQ_LAUNCH_MFMA(TQ, C, V, true, TL); else KVQ_LAUNCH_MFMA(TQ, C, V, false, TL);
 #define KVQ_LAUNCH_MFMA_CF(TQ, TL)                                                            \
   if (cpg == 8) {                                                                             \
-    if (fold) KVQ_LAUNCH_MFMA(TQ, 8, true, TL); else KVQ_LAUNCH_MFMA(TQ, 8, false, TL);      \
+    if (vg1) { KVQ_LAUNCH_MFMA_F(TQ, 8, true, TL) } else { KVQ_LAUNCH_MFMA_F(TQ, 8, false, TL) } \
   } else {                                                                                    \
-    if (fold) KVQ_LAUNCH_MFMA(TQ, 4, true, TL); else KVQ_LAUNCH_MFMA(TQ, 4, false, TL);      \
+    KVQ_LAUNCH_MFMA_F(TQ, 4, false, TL)                                                       \
   }
   if (tail && q_dtype == KVQ_DTYPE_BF16) {
     KVQ_LAUNCH_MFMA_CF(bf16, true);
@@ -881,6 +913,7 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
     KVQ_DISPATCH_FLOAT(q_dtype, TQ, KVQ_LAUNCH_MFMA_CF(TQ, false));
   }
 #undef KVQ_LAUNCH_MFMA_CF
+#undef KVQ_LAUNCH_MFMA_F
 #undef KVQ_LAUNCH_MFMA
   KVQ_LAUNCH_CHECK();
   *launched = true;
