@@ -256,14 +256,15 @@ def test_decode_attention_matches_oracle(gpu_device, d, kvh, g, bs, rep):
 
 
 @pytest.mark.parametrize("kvh,g,bs,rep", [
-    (8, 32, 64, 8),     # workgroup kernel, 32-token tiles, 4 value groups per token
-    (16, 64, 128, 2),   # two workgroups per item (head groups 0-7, 8-15)
-    (8, 128, 256, 7),
-    (8, 128, 128, 12),  # GQA group above 8: per-wave kernel (two score MFMAs)
-    (4, 64, 128, 8),    # kv heads not a multiple of 8: per-wave kernel
+    (8, 32, 64, 8),     # 32-token tiles, 4 value groups per token
+    (16, 64, 128, 2),   # two value groups per head, key scales gathered per tile
+    (8, 128, 256, 7),   # one value group per head; two key groups per page
+    (8, 128, 128, 12),  # GQA group above 8 (two score MFMAs); one key group per page
+    (4, 64, 128, 8),    # kv heads not a multiple of 8
 ])
 def test_decode_head_group_geometries(gpu_device, kvh, g, bs, rep):
-    """Decode over the workgroup (shared value rows) and per-wave kernel forms."""
+    """Decode across the kernel's tile forms: tile size, value groups per
+    head, key-scale DMA form, folded and unfolded score MFMAs."""
     from vllm_ascend_quantized_kv_cache.ops.kivi_decode import DecodeSeq, kivi_decode_attention
 
     d = 128

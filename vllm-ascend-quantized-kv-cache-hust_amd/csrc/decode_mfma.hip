@@ -154,7 +154,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 // VG1: one value group spans the whole head (G >= 128 at CPG 8), so every PV
 // column group shares the token's value scale and min: they are gathered and
 // applied once per PV k-step instead of once per column group.
-template <int CPG, bool VG1 = false>
+// KSV: the key scales of a group are one contiguous run per head (one group
+// per page, bs == g): one 16-byte-lane DMA brings both the scales (lanes
+// 0-31) and the minima (lanes 32-63) in dim order, instead of four 4-byte
+// gathers in the permuted order prepare_group reads.
+template <int CPG, bool VG1 = false, bool KSV = false>
 struct Tile {
   static_assert(!VG1 || CPG == 8, "VG1 needs 64-token tiles");
   static constexpr int D = 128;
@@ -177,12 +181,13 @@ struct Tile {
   // DMA instructions per tile; the waits rely on this number
   static constexpr int KW_INST = D * CPG * 4 / 1024;  // 16-byte lanes
   static constexpr int VW_INST = GT * 64 / 1024;      // 16-byte lanes
-  static constexpr int KS_INST = D / 64;              // 4-byte lanes
+  static constexpr int KS_INST = D / 64;              // 4-byte lanes (per array)
+  static constexpr int KS_DMA = KSV ? 1 : 2 * KS_INST; // key scale + min DMA instructions
   static constexpr int VS_INST = PVS * NVS * 32 / 64; // 4-byte lanes
-  static constexpr int NINST = KW_INST + VW_INST + 2 * KS_INST + 2 * VS_INST;
+  static constexpr int NINST = KW_INST + VW_INST + KS_DMA + 2 * VS_INST;
   // a tile that continues the previous tile's key group skips the key
   // scale/min DMA (prepare_group reads them only at a group's first tile)
-  static constexpr int NINST_CONT = NINST - 2 * KS_INST;
+  static constexpr int NINST_CONT = NINST - KS_DMA;
   static_assert(NINST < 64, "vmcnt range");
 };
 
@@ -224,13 +229,13 @@ struct LaneDma {
   uint32_t k, v, ks, vs;  // byte offsets of this lane's DMA data (lane part)
 };
 
-template <int CPG, bool VG1>
+template <int CPG, bool VG1, bool KSV>
 __device__ __forceinline__ LaneDma lane_dma(int lane, int wpd, int kvh, int gpb, int ng, int g) {
   constexpr int LPR = CPG / 4;  // 16-byte lanes per key dim row (CPG words)
   LaneDma ld;
   ld.k = static_cast<uint32_t>(4 * ((lane / LPR) * wpd + 4 * (lane % LPR)));
   ld.v = static_cast<uint32_t>(4 * ((lane / 4) * kvh * 16 + 4 * (lane % 4)));
-  ld.ks = static_cast<uint32_t>(4 * key_scale_off<CPG>(lane, gpb));
+  ld.ks = static_cast<uint32_t>(KSV ? 16 * (lane & 31) : 4 * key_scale_off<CPG>(lane, gpb));
   ld.vs = static_cast<uint32_t>(4 * value_scale_off<CPG, VG1>(lane, kvh, ng, g));
   return ld;
 }
@@ -239,11 +244,11 @@ __device__ __forceinline__ LaneDma lane_dma(int lane, int wpd, int kvh, int gpb,
 // wave's key region `buf`.  kq_t, ks_t, km_t point at the tile's first word /
 // scale (page blk, token offset off0, key group grp); every lane address stays
 // inside the tile's rows of that page.
-template <int CPG>
+template <int CPG, bool KSV>
 __device__ __forceinline__ void issue_keys(char* buf, const LaneDma& ld, const uint32_t* kq_t,
                                            int wpd, const float* ks_t, const float* km_t,
                                            int gpb, bool with_ks) {
-  using T = Tile<CPG>;
+  using T = Tile<CPG, false, KSV>;
   constexpr int LPR = CPG / 4;
   constexpr int DPI = 64 / LPR;  // key dim rows per instruction
   const char* kb = reinterpret_cast<const char*>(kq_t);
@@ -253,6 +258,11 @@ __device__ __forceinline__ void issue_keys(char* buf, const LaneDma& ld, const u
   for (int i = 0; i < T::KW_INST; ++i)
     dma16(kb + 4 * (i * DPI * wpd) + ld.k, buf + 4 * T::KW + 1024 * i);
   if (!with_ks) return;  // uniform
+  if constexpr (KSV) {
+    // KM follows KS in the tile, so lane l lands at KS + 16 l either way
+    dma16((threadIdx.x & 32 ? mb : sb) + ld.ks, buf + 4 * T::KS);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < T::KS_INST; ++i) {
     const int o = 4 * key_scale_off<CPG>(64 * i, gpb);
@@ -264,14 +274,14 @@ __device__ __forceinline__ void issue_keys(char* buf, const LaneDma& ld, const u
 // DMA of one whole tile (keys and the gathered value operands) for kv head h
 // into the wave's tile buffer; vq_t, vs_t, vm_t point at the tile's first value
 // word / scale of head h.
-template <int CPG, bool VG1>
+template <int CPG, bool VG1, bool KSV>
 __device__ __forceinline__ void issue_tile(char* buf, const LaneDma& ld, const uint32_t* kq_t,
                                            int wpd, const uint32_t* vq_t, int kvh,
                                            const float* ks_t, const float* km_t, int gpb,
                                            const float* vs_t, const float* vm_t, int ng, int g,
                                            bool with_ks) {
-  using T = Tile<CPG, VG1>;
-  issue_keys<CPG>(buf, ld, kq_t, wpd, ks_t, km_t, gpb, with_ks);
+  using T = Tile<CPG, VG1, KSV>;
+  issue_keys<CPG, KSV>(buf, ld, kq_t, wpd, ks_t, km_t, gpb, with_ks);
   const char* vb = reinterpret_cast<const char*>(vq_t);
   const char* vsb = reinterpret_cast<const char*>(vs_t);
   const char* vmb = reinterpret_cast<const char*>(vm_t);
@@ -427,7 +437,7 @@ struct QGroup {
   float kb;
 };
 
-template <typename TQ, int CPG, bool FOLD>
+template <typename TQ, int CPG, bool FOLD, bool KSV>
 __device__ __forceinline__ void prepare_group(const uint32_t* W, int n, int kg,
                                               const QRegs<TQ>& qv, float qscale, QGroup& qg) {
 #pragma clang fp contract(fast)
@@ -436,8 +446,18 @@ __device__ __forceinline__ void prepare_group(const uint32_t* W, int n, int kg,
 #pragma unroll
   for (int s4 = 0; s4 < 4; ++s4) {
     float sc[8], mn[8];
-    read8f(W + T::KS + (s4 * 4 + kg) * 8, sc);
-    read8f(W + T::KM + (s4 * 4 + kg) * 8, mn);
+    if constexpr (KSV) {  // dim order: dims 32*s4 + 4*ii + kg, 16 bytes apart
+      const float* ksf = reinterpret_cast<const float*>(W + T::KS) + 32 * s4 + kg;
+      const float* kmf = reinterpret_cast<const float*>(W + T::KM) + 32 * s4 + kg;
+#pragma unroll
+      for (int ii = 0; ii < 8; ++ii) {
+        sc[ii] = ksf[4 * ii];
+        mn[ii] = kmf[4 * ii];
+      }
+    } else {
+      read8f(W + T::KS + (s4 * 4 + kg) * 8, sc);
+      read8f(W + T::KM + (s4 * 4 + kg) * 8, mn);
+    }
     uint32_t qh[4], ql[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
@@ -720,7 +740,7 @@ struct WaveAcc {
 // (kind-0) items, the second the tail (kind-1) items, so every tail wave is
 // dispatched after every int4 wave and runs in the slots the shorter int4
 // items free, with no second stream or event between the two.
-template <typename TQ, int CPG, bool VG1, bool FOLD, bool TAIL>
+template <typename TQ, int CPG, bool VG1, bool KSV, bool FOLD, bool TAIL>
 __global__ void __launch_bounds__(64, 2)
 kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qscale,
                         const uint32_t* __restrict__ kq, const float* __restrict__ ks,
@@ -731,7 +751,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
                         const int32_t* __restrict__ work, int64_t num_work,
                         const TQ* __restrict__ ring_k, const TQ* __restrict__ ring_v,
                         int ring_len, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
-  using T = Tile<CPG, VG1>;
+  using T = Tile<CPG, VG1, KSV>;
   constexpr int D = T::D;
   constexpr int GT = T::GT;
 
@@ -763,7 +783,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
 
   const QRegs<TQ> qv = load_q<TQ, FOLD>(query, b, hq, h, rep, n, kg);
   const LaneNib<CPG> ln(n, kg);
-  const LaneDma ld = lane_dma<CPG, VG1>(lane, wpd, kvh, gpb, ng, g);
+  const LaneDma ld = lane_dma<CPG, VG1, KSV>(lane, wpd, kvh, gpb, ng, g);
 
   WaveAcc<CPG, VG1> acc;
   acc.init();
@@ -773,7 +793,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
     const int off0 = p % bs;
     const int64_t krow = (blk * kvh + h) * D;
     const int64_t vtok = (blk * bs + off0) * kvh + h;
-    issue_tile<CPG, VG1>(buf, ld, kq + krow * wpd + off0 / 8, wpd, vq + vtok * 16, kvh,
+    issue_tile<CPG, VG1, KSV>(buf, ld, kq + krow * wpd + off0 / 8, wpd, vq + vtok * 16, kvh,
                          ks + krow * gpb + off0 / g, km + krow * gpb + off0 / g, gpb,
                          vs + vtok * ng, vm + vtok * ng, ng, g, with_ks);
   };
@@ -802,7 +822,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
     const uint32_t* W = reinterpret_cast<const uint32_t*>(cur);
     // tiles are GT-aligned and GT divides g: a tile starts a key group or
     // continues the previous tile's
-    if (p0 == pb || p0 % g == 0) prepare_group<TQ, CPG, FOLD>(W, n, kg, qv, qscale, qg);
+    if (p0 == pb || p0 % g == 0) prepare_group<TQ, CPG, FOLD, KSV>(W, n, kg, qv, qscale, qg);
     const WaveValues<CPG, VG1> vals(W, kg, n % CPG);
     if (p0 + GT <= pe)
       compute_tile<TQ, CPG, VG1, true, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run,
@@ -884,24 +904,28 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
   const bool fold = hq / kvh <= 8;
   // one value group per head row: value scales gathered once per PV k-step
   const bool vg1 = cpg == 8 && g >= 128;
+  // a key group per page: its scales are contiguous per head
+  const bool ksv = vg1 && bs == g;
   const size_t lds_int4 =
       2 * static_cast<size_t>(cpg == 8 ? (vg1 ? Tile<8, true>::BYTES : Tile<8>::BYTES)
                                        : Tile<4>::BYTES);
   const size_t lds_tail = static_cast<size_t>(tail::kLdsBytes);
   const size_t lds = tail && lds_tail > lds_int4 ? lds_tail : lds_int4;
-#define KVQ_LAUNCH_MFMA(TQ, C, V, F, TL)                                                      \
-  hipLaunchKernelGGL((kivi_decode_mfma_kernel<TQ, C, V, F, TL>), grid, block, lds, s,        \
+#define KVQ_LAUNCH_MFMA(TQ, C, V, KV, F, TL)                                                  \
+  hipLaunchKernelGGL((kivi_decode_mfma_kernel<TQ, C, V, KV, F, TL>), grid, block, lds, s,    \
                      static_cast<const TQ*>(query), hq, kvh, qscale, kqu, ks, km, vqu, vs, vm,\
                      bs, g, nb, block_table, maxb, seq_meta, work, num_work,                 \
                      static_cast<const TQ*>(ring_k), static_cast<const TQ*>(ring_v),         \
                      ring_len, ws_o, ws_ml)
-#define KVQ_LAUNCH_MFMA_F(TQ, C, V, TL)                                                       \
-  if (fold) KVQ_LAUNCH_MFMA(TQ, C, V, true, TL); else KVQ_LAUNCH_MFMA(TQ, C, V, false, TL);
+#define KVQ_LAUNCH_MFMA_F(TQ, C, V, KV, TL)                                                   \
+  if (fold) KVQ_LAUNCH_MFMA(TQ, C, V, KV, true, TL); else KVQ_LAUNCH_MFMA(TQ, C, V, KV, false, TL);
 #define KVQ_LAUNCH_MFMA_CF(TQ, TL)                                                            \
   if (cpg == 8) {                                                                             \
-    if (vg1) { KVQ_LAUNCH_MFMA_F(TQ, 8, true, TL) } else { KVQ_LAUNCH_MFMA_F(TQ, 8, false, TL) } \
+    if (ksv) { KVQ_LAUNCH_MFMA_F(TQ, 8, true, true, TL) }                                     \
+    else if (vg1) { KVQ_LAUNCH_MFMA_F(TQ, 8, true, false, TL) }                               \
+    else { KVQ_LAUNCH_MFMA_F(TQ, 8, false, false, TL) }                                       \
   } else {                                                                                    \
-    KVQ_LAUNCH_MFMA_F(TQ, 4, false, TL)                                                       \
+    KVQ_LAUNCH_MFMA_F(TQ, 4, false, false, TL)                                                \
   }
   if (tail && q_dtype == KVQ_DTYPE_BF16) {
     KVQ_LAUNCH_MFMA_CF(bf16, true);
