@@ -142,11 +142,17 @@ int kvq_kivi_gather_dequant(const int32_t* k_quant, const float* k_scale, const 
  *               positions < k_hist (v_hist) read int4 keys (values); the
  *               others read ring lane (first_lane + p - hist) % ring_len
  *   work        int32 [num_work, 4] = {request, pos_begin, pos_end, kind}
- *               kind 0: both sides int4 over the whole range (int4 MFMA
- *                       kernel, 128-aligned ranges);
- *               kind 1: any mix of sources (MFMA tail kernel on the side
- *                       stream; the generic kernel for geometries neither
- *                       MFMA kernel covers)
+ *               kind 0: both sides int4 over the whole range, pos_begin a
+ *                       multiple of 64 (the int4 MFMA kernel's tiles);
+ *               kind 1: any mix of sources (the MFMA kernel's tail path, the
+ *                       standalone MFMA tail kernel, or the generic kernel
+ *                       for geometries neither covers)
+ *               a request's items are contiguous, from first_work on
+ *   pieces      int32 [num_pieces + 1] or NULL: piece k is work items
+ *               [pieces[k], pieces[k+1]).  Where the MFMA kernel runs both
+ *               kinds, one wave per (piece, kv head) runs its piece's items
+ *               in order in a single pass, so pieces of equal cost end
+ *               together; elsewhere the pieces are ignored.
  *   workspace   >= kvq_kivi_decode_workspace_bytes(num_work, num_heads, D)
  *   block_table int32 [batch, max_blocks]
  * Replaces the decode branch: _forward_kivi_paged_decode_attention
@@ -160,6 +166,7 @@ int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batch, int num_
                          int64_t num_blocks, int block_size, int group_size,
                          const int32_t* block_table, int64_t max_blocks,
                          const int32_t* seq_meta, const int32_t* work, int64_t num_work,
+                         const int32_t* pieces, int64_t num_pieces,
                          const void* ring_k, const void* ring_v, int ring_dtype, int ring_len,
                          void* workspace, void* out, void* stream);
 

@@ -289,6 +289,45 @@ def test_decode_head_group_geometries(gpu_device, kvh, g, bs, rep):
         torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("kvh,g,bs,rep", [(8, 128, 128, 5), (8, 64, 128, 8), (4, 32, 64, 4)])
+@pytest.mark.parametrize("cu_count", [1, 3, 256])
+def test_decode_pieces_match_oracle(gpu_device, kvh, g, bs, rep, cu_count):
+    """Equal-cost pieces: one wave per (piece, kv head) walks several items of
+    several requests, int4 and tail alike (few CUs: many items per piece; int4
+    items that start mid key group), in the kernel's single pass."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
+        DecodeSeq,
+        kivi_decode_attention,
+        plan_decode_pieces,
+    )
+
+    d = 128
+    r_len = 2 * g if g <= 64 else g
+    lens = [r_len * 9 + 3, 1, r_len + 5, 0, r_len * 5 + 64, 77]
+    cpu, table, ring_k, ring_v, seqs, wk, wv, _, _ = _ring_case(
+        gpu_device, d, kvh, g, bs, r_len, lens, seed=33, ring_dtype=torch.bfloat16
+    )
+    hq = kvh * rep
+    q = torch.randn(len(lens), hq, d, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    scale = d ** -0.5
+    dk, dv = ref.dequant_gather(*cpu, table, torch.tensor(lens), torch.float32, g)
+    dk = ref.overlay_residual(dk, lens, wk)
+    dv = ref.overlay_residual(dv, lens, wv)
+    want = ref.attention(q, dk, dv, [1] * len(lens), lens, scale, causal=True)
+    dseqs = [DecodeSeq(n, hk, hv, row, ks_, vs_) for (n, hk, hv, row, ks_, vs_) in seqs]
+    meta, work, pieces = plan_decode_pieces(dseqs, kvh, cu_count)
+    print(f"pieces case kvh={kvh} g={g} cu={cu_count}: {len(work)} items, "
+          f"{len(pieces) - 1} pieces", flush=True)
+    dev = gpu_device
+    got = kivi_decode_attention(
+        q.to(dev), to_dev(cpu, dev), table.to(dev), dseqs, ring_k.to(dev), ring_v.to(dev),
+        scale, g, plan=(torch.from_numpy(meta).to(dev), torch.from_numpy(work).to(dev),
+                        torch.from_numpy(pieces).to(dev)),
+    )
+    # rows of empty requests are the empty sum (zeros) in both
+    torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
+
+
 def test_mfma_lane_layout(gpu_device):
     """The 16x16x32 f16 MFMA lane mapping the decode kernels assume."""
     from vllm_ascend_quantized_kv_cache.ops import _native

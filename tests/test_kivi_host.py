@@ -305,6 +305,71 @@ def test_one_launch_store_geometry_gate():
     assert not store_one_launch_supported(128, 128, torch.float32)
 
 
+@pytest.mark.parametrize("cu_count,kvh", [(256, 8), (3, 4), (1, 1), (256, 2)])
+def test_plan_decode_pieces_invariants(cu_count, kvh):
+    """Equal-cost pieces: at most one wave slot per piece, items of a request
+    contiguous and covering it exactly (int4 items on 64-position starts,
+    both sides int4 over them), pieces covering the list in order, and piece
+    costs within one step of each other."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
+        PIECE_MAX_COST,
+        TAIL_POSITION_COST,
+        DecodeSeq,
+        plan_decode_pieces,
+    )
+
+    rng = random.Random(cu_count * 10 + kvh)
+    seqs = []
+    for i in range(40):
+        n = rng.choice([0, 1, 63, 64, 65, 300, 4097, rng.randrange(1, 20000)])
+        r = 128
+        hk = ((n - 1) // r) * r if n else 0
+        hv = max(0, n - r)
+        seqs.append(DecodeSeq(n, hk, hv, i, 0, 0))
+    meta, work, pieces = plan_decode_pieces(seqs, kvh, cu_count)
+    slots = max(1, cu_count * 8 // kvh)
+    total = 0.0
+    for s in seqs:
+        a = max(0, min(s.k_hist, s.v_hist, s.seq_len))
+        total += -(-a // 64) * 64 + (s.seq_len - a) * TAIL_POSITION_COST
+    slots *= max(1, -(-int(total) // int(slots * PIECE_MAX_COST)))  # whole rounds
+    assert 1 <= len(pieces) - 1 <= slots
+    assert pieces[0] == 0 and pieces[-1] == len(work)
+    assert all(a < b for a, b in zip(pieces[:-1], pieces[1:]))
+    for b, s in enumerate(seqs):
+        first, count = int(meta[b, 6]), int(meta[b, 7])
+        assert count >= 1
+        its = work[first : first + count]
+        assert (its[:, 0] == b).all()
+        pos = 0
+        for _, p, e, kind in its.tolist():
+            assert p == pos and e >= p
+            pos = e
+            if kind == 0:
+                assert p % 64 == 0 and e <= min(s.k_hist, s.v_hist) and e > p
+        assert pos == s.seq_len
+    if len(pieces) - 1 == slots and slots > 1:
+        cost = [
+            sum(-(-(e - p) // 64) * 64 if k == 0 else (e - p) * TAIL_POSITION_COST
+                for _, p, e, k in work[pieces[i] : pieces[i + 1]].tolist())
+            for i in range(len(pieces) - 1)
+        ]
+        step = sum(cost) / slots
+        assert max(cost) <= step + 2 * 32 * TAIL_POSITION_COST + 64
+
+
+def test_plan_decode_picks_pieces_for_one_round_and_splits_beyond():
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import DecodeSeq, plan_decode
+
+    small = [DecodeSeq(9000, 8960, 8872, i, 0, 0) for i in range(32)]
+    _, work, pieces = plan_decode(small, 8, 256)
+    assert pieces is not None and pieces[-1] == len(work)
+    big = [DecodeSeq(32768, 32640, 32640, i, 0, 0) for i in range(256)]
+    _, work, pieces = plan_decode(big, 8, 256)
+    assert pieces is None
+    assert (work[work[:, 3] == 0][:, 1] % 128 == 0).all()
+
+
 def test_misaligned_key_flush_fails_closed_before_kernel():
     impl = _make_impl()
     key = torch.randn(GROUP, KVH, HEAD)

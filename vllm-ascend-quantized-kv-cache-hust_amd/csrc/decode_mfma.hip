@@ -736,10 +736,14 @@ struct WaveAcc {
   }
 };
 
-// TAIL: the grid covers the work items twice; the first pass takes the int4
-// (kind-0) items, the second the tail (kind-1) items, so every tail wave is
-// dispatched after every int4 wave and runs in the slots the shorter int4
-// items free, with no second stream or event between the two.
+// Without pieces (TAIL): the grid covers the work items twice; the first pass
+// takes the int4 (kind-0) items, the second the tail (kind-1) items, so every
+// tail wave is dispatched after every int4 wave and runs in the slots the
+// shorter int4 items free, with no second stream or event between the two.
+// With pieces (TAIL only): one wave per (piece, kv head) walks the piece's
+// items [pieces[k], pieces[k+1]) in order, int4 and tail alike; the host cuts
+// the pieces to about equal cost, so every wave of the single pass ends at
+// about the same time.
 template <typename TQ, int CPG, bool VG1, bool KSV, bool FOLD, bool TAIL>
 __global__ void __launch_bounds__(64, 2)
 kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qscale,
@@ -749,6 +753,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
                         int g, int64_t nb, const int32_t* __restrict__ block_table,
                         int64_t maxb, const int32_t* __restrict__ seq_meta,
                         const int32_t* __restrict__ work, int64_t num_work,
+                        const int32_t* __restrict__ pieces_arg, int64_t num_pieces,
                         const TQ* __restrict__ ring_k, const TQ* __restrict__ ring_v,
                         int ring_len, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   using T = Tile<CPG, VG1, KSV>;
@@ -756,19 +761,31 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   constexpr int GT = T::GT;
 
   extern __shared__ __align__(16) char lds_raw[];
-  int wi, h;
-  const int64_t pass_len = xcd_grid_size(num_work, kvh);
-  const int pass = TAIL && blockIdx.x >= pass_len ? 1 : 0;
-  if (!xcd_item_head(blockIdx.x - pass * pass_len, kvh, num_work, wi, h)) return;
+  const int32_t* pieces = TAIL ? pieces_arg : nullptr;
   const int lane = threadIdx.x;
+  int it0, it1, h, pass = 0;
+  if (pieces) {
+    int k;
+    if (!xcd_item_head(blockIdx.x, kvh, num_pieces, k, h)) return;
+    it0 = pieces[k];
+    it1 = pieces[k + 1];
+  } else {
+    const int64_t pass_len = xcd_grid_size(num_work, kvh);
+    pass = TAIL && blockIdx.x >= pass_len ? 1 : 0;
+    if (!xcd_item_head(blockIdx.x - pass * pass_len, kvh, num_work, it0, h)) return;
+    it1 = it0 + 1;
+  }
+  for (int wi = it0; wi < it1; ++wi) {
   const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
-  if (wk[3] != pass) return;  // the other pass (or the tail kernel) owns it (uniform)
+  const int kind = wk[3];
+  // without pieces the other pass (or the tail kernel) owns it (uniform)
+  if (!pieces && kind != pass) continue;
   if constexpr (TAIL) {
-    if (pass == 1) {
+    if (kind == 1) {
       tail::tail_item<TQ>(lds_raw, query, hq, kvh, qscale, kq, ks, km, vq, vs, vm, bs, g, nb,
                           block_table, maxb, seq_meta, wk, wi, h, ring_k, ring_v, ring_len,
                           ws_o, ws_ml);
-      return;
+      continue;
     }
   }
   const int b = wk[0];
@@ -841,6 +858,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
     cur ^= 1;
   }
   acc.store(ln, wi, hq, h, rep, n, kg, ws_o, ws_ml);
+  }  // items
 }
 
 // Copies 1 KiB with 16-byte DMA lanes and 256 B with 4-byte DMA lanes through
@@ -884,6 +902,7 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
                             const int32_t* vq, const float* vs, const float* vm, int bs, int g,
                             int64_t nb, const int32_t* block_table, int64_t maxb,
                             const int32_t* seq_meta, const int32_t* work, int64_t num_work,
+                            const int32_t* pieces, int64_t num_pieces,
                             const void* ring_k, const void* ring_v, int ring_dtype, int ring_len,
                             float* ws_o, float* ws_ml, hipStream_t s, bool* launched,
                             bool* tail_done) {
@@ -897,8 +916,13 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
   const uint32_t* vqu = reinterpret_cast<const uint32_t*>(vq);
   const int64_t pass_len = xcd_grid_size(num_work, kvh);
   const bool tail = tail_path_applies(q_dtype, hq, kvh, d, ring_dtype);
-  if ((tail ? 2 : 1) * pass_len > 0x7fffffff) return KVQ_ERR_INVALID;
-  const dim3 grid(static_cast<unsigned>((tail ? 2 : 1) * pass_len));
+  // pieces need the tail path (a piece mixes int4 and tail items)
+  const bool use_pieces = tail && pieces && num_pieces > 0;
+  const int64_t blocks =
+      use_pieces ? xcd_grid_size(num_pieces, kvh) : (tail ? 2 : 1) * pass_len;
+  if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
+  const int32_t* pieces_k = use_pieces ? pieces : nullptr;
+  const dim3 grid(static_cast<unsigned>(blocks));
   const dim3 block(64);
   // GQA groups of at most 8 heads fold the hi/lo score parts into one MFMA
   const bool fold = hq / kvh <= 8;
@@ -914,8 +938,8 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
 #define KVQ_LAUNCH_MFMA(TQ, C, V, KV, F, TL)                                                  \
   hipLaunchKernelGGL((kivi_decode_mfma_kernel<TQ, C, V, KV, F, TL>), grid, block, lds, s,    \
                      static_cast<const TQ*>(query), hq, kvh, qscale, kqu, ks, km, vqu, vs, vm,\
-                     bs, g, nb, block_table, maxb, seq_meta, work, num_work,                 \
-                     static_cast<const TQ*>(ring_k), static_cast<const TQ*>(ring_v),         \
+                     bs, g, nb, block_table, maxb, seq_meta, work, num_work, pieces_k,       \
+                     num_pieces, static_cast<const TQ*>(ring_k), static_cast<const TQ*>(ring_v),\
                      ring_len, ws_o, ws_ml)
 #define KVQ_LAUNCH_MFMA_F(TQ, C, V, KV, TL)                                                   \
   if (fold) KVQ_LAUNCH_MFMA(TQ, C, V, KV, true, TL); else KVQ_LAUNCH_MFMA(TQ, C, V, KV, false, TL);

@@ -428,7 +428,8 @@ extern "C" int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batc
                                     const float* v_scale, const float* v_mn, int64_t num_blocks,
                                     int block_size, int group_size, const int32_t* block_table,
                                     int64_t max_blocks, const int32_t* seq_meta,
-                                    const int32_t* work, int64_t num_work, const void* ring_k,
+                                    const int32_t* work, int64_t num_work,
+                                    const int32_t* pieces, int64_t num_pieces, const void* ring_k,
                                     const void* ring_v, int ring_dtype, int ring_len,
                                     void* workspace, void* out, void* stream) {
   if (batch == 0) return KVQ_OK;
@@ -441,6 +442,7 @@ extern "C" int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batc
     return KVQ_ERR_GEOMETRY;
   if (num_heads / num_kv_heads > kMaxRep) return KVQ_ERR_GEOMETRY;
   if (num_work > 0x7fffffff || batch > 0x7fffffff || num_heads > 65535) return KVQ_ERR_INVALID;
+  if (num_pieces < 0 || num_pieces > num_work) return KVQ_ERR_INVALID;
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* ws_o = static_cast<float*>(workspace);
   float* ws_ml = ws_o + num_work * num_heads * head_size;
@@ -452,8 +454,9 @@ extern "C" int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batc
   int rc = kvq::launch_kivi_decode_mfma(query, q_dtype, num_heads, num_kv_heads, head_size,
                                        qscale, k_quant, k_scale, k_mn, v_quant, v_scale, v_mn,
                                        block_size, group_size, num_blocks, block_table,
-                                       max_blocks, seq_meta, work, num_work, ring_k, ring_v,
-                                       ring_dtype, ring_len, ws_o, ws_ml, s, &mfma, &tail);
+                                       max_blocks, seq_meta, work, num_work, pieces,
+                                       num_pieces, ring_k, ring_v, ring_dtype, ring_len, ws_o,
+                                       ws_ml, s, &mfma, &tail);
   if (rc != KVQ_OK) return rc;
   if (!tail) {
     rc = kvq::launch_kivi_decode_tail_mfma(query, q_dtype, num_heads, num_kv_heads, head_size,

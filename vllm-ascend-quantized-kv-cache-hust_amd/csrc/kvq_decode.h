@@ -43,15 +43,16 @@ inline bool tail_path_applies(int q_dtype, int hq, int kvh, int d, int ring_dtyp
 }
 
 // Launch the MFMA kernel for the kind-0 work items when the geometry is one it
-// covers, taking the kind-1 items too (in a second pass of the same grid) when
-// the tail path applies.  *launched / *tail_done tell the caller which kinds
-// still need another kernel.
+// covers, taking the kind-1 items too when the tail path applies: in a second
+// pass of the same grid, or, given pieces, in one pass of one wave per (piece,
+// kv head).  *launched / *tail_done tell the caller which kinds still need
+// another kernel.
 int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int d, float qscale,
                             const int32_t* kq, const float* ks, const float* km,
                             const int32_t* vq, const float* vs, const float* vm, int bs, int g,
                             int64_t nb, const int32_t* block_table, int64_t maxb,
                             const int32_t* seq_meta, const int32_t* work, int64_t num_work,
-                            const void* ring_k, const void* ring_v, int ring_dtype, int ring_len,
+                            const int32_t* pieces, int64_t num_pieces, const void* ring_k, const void* ring_v, int ring_dtype, int ring_len,
                             float* ws_o, float* ws_ml, hipStream_t s, bool* launched,
                             bool* tail_done);
 

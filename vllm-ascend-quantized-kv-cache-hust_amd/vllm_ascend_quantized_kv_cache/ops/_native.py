@@ -50,7 +50,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "kvq_kivi_decode_attn": (
         _I,
         [_P, _I, _I64, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _P, _I64,
-         _P, _P, _I64, _P, _P, _I, _I, _P, _P, _P],
+         _P, _P, _I64, _P, _I64, _P, _P, _I, _I, _P, _P, _P],
     ),
     "kvq_prefill_attn": (
         _I, [_P, _P, _P, _I, _P, _P, _I64, _I64, _I, _I, _I, _F, _I, _P, _P]
