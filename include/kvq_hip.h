@@ -147,6 +147,11 @@ int kvq_kivi_gather_dequant(const int32_t* k_quant, const float* k_scale, const 
  *               kind 1: any mix of sources (the MFMA kernel's tail path, the
  *                       standalone MFMA tail kernel, or the generic kernel
  *                       for geometries neither covers)
+ *               kind 2 / 3: as kind 0 (pos_begin a multiple of 64), over
+ *                       the even / odd 64-position chunks of the range only.
+ *                       A kind-2 item at an even index followed by its
+ *                       kind-3 twin run on one XCD at the same time and
+ *                       share the range's key lines through its L2.
  *               a request's items are contiguous, from first_work on
  *   pieces      int32 [num_pieces + 1] or NULL: piece k is work items
  *               [pieces[k], pieces[k+1]).  Where the MFMA kernel runs both

@@ -328,6 +328,43 @@ def test_decode_pieces_match_oracle(gpu_device, kvh, g, bs, rep, cu_count):
     torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("d,kvh,g,bs", [(128, 8, 128, 128), (128, 8, 64, 128), (128, 4, 32, 64),
+                                         (64, 4, 16, 32)])
+@pytest.mark.parametrize("split", [128, 256])
+def test_decode_paired_items_match_oracle(gpu_device, d, kvh, g, bs, split):
+    """Paired int4 items (even / odd 64-position chunks of one range, on one
+    XCD) through the MFMA kernel, 32-token tiles included, and through the
+    generic kernel (D = 64)."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
+        DecodeSeq,
+        kivi_decode_attention,
+        plan_decode_work,
+    )
+
+    r_len = 2 * g if g <= 64 else g
+    lens = [r_len * 9 + 3, 1, r_len + 5, 0, r_len * 5 + 64, 77, 700]
+    cpu, table, ring_k, ring_v, seqs, wk, wv, _, _ = _ring_case(
+        gpu_device, d, kvh, g, bs, r_len, lens, seed=41, ring_dtype=torch.bfloat16
+    )
+    rep = 5
+    hq = kvh * rep
+    q = torch.randn(len(lens), hq, d, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16)
+    scale = d ** -0.5
+    dk, dv = ref.dequant_gather(*cpu, table, torch.tensor(lens), torch.float32, g)
+    dk = ref.overlay_residual(dk, lens, wk)
+    dv = ref.overlay_residual(dv, lens, wv)
+    want = ref.attention(q, dk, dv, [1] * len(lens), lens, scale, causal=True)
+    dseqs = [DecodeSeq(n, hk, hv, row, ks_, vs_) for (n, hk, hv, row, ks_, vs_) in seqs]
+    meta, work = plan_decode_work(dseqs, split, paired=True)
+    print(f"paired case d={d} g={g} split={split}: {len(work)} items", flush=True)
+    dev = gpu_device
+    got = kivi_decode_attention(
+        q.to(dev), to_dev(cpu, dev), table.to(dev), dseqs, ring_k.to(dev), ring_v.to(dev),
+        scale, g, plan=(torch.from_numpy(meta).to(dev), torch.from_numpy(work).to(dev)),
+    )
+    torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
+
+
 def test_mfma_lane_layout(gpu_device):
     """The 16x16x32 f16 MFMA lane mapping the decode kernels assume."""
     from vllm_ascend_quantized_kv_cache.ops import _native

@@ -370,6 +370,41 @@ def test_plan_decode_picks_pieces_for_one_round_and_splits_beyond():
     assert (work[work[:, 3] == 0][:, 1] % 128 == 0).all()
 
 
+@pytest.mark.parametrize("split", [128, 256, 4096])
+def test_plan_decode_work_pairs(split):
+    """Paired int4 items: kind 2 at an even index, its kind-3 twin right after
+    over the same range; a request's items stay contiguous and cover it."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import DecodeSeq, plan_decode_work
+
+    rng = random.Random(split)
+    seqs = []
+    for i in range(30):
+        n = rng.choice([0, 1, 130, 300, 4097, rng.randrange(1, 30000)])
+        hk = ((n - 1) // 128) * 128 if n else 0
+        seqs.append(DecodeSeq(n, hk, max(0, n - 128), i, 0, 0))
+    meta, work = plan_decode_work(seqs, split, paired=True)
+    kinds = work[:, 3].tolist()
+    for i, k in enumerate(kinds):
+        if k == 2:
+            assert i % 2 == 0 and kinds[i + 1] == 3
+            assert (work[i, :3] == work[i + 1, :3]).all()
+            assert work[i, 1] % 128 == 0 and work[i, 2] - work[i, 1] <= 2 * split
+        if k == 3:
+            assert i % 2 == 1 and kinds[i - 1] == 2
+        assert k != 0
+    for b, s in enumerate(seqs):
+        first, count = int(meta[b, 6]), int(meta[b, 7])
+        its = work[first : first + count]
+        assert (its[:, 0] == b).all()
+        covered = 0
+        for _, p, e, k in its.tolist():
+            if k == 3:
+                continue
+            assert p == covered or (p == 0 and e == 0)
+            covered = max(covered, e)
+        assert covered == s.seq_len
+
+
 def test_misaligned_key_flush_fails_closed_before_kernel():
     impl = _make_impl()
     key = torch.randn(GROUP, KVH, HEAD)

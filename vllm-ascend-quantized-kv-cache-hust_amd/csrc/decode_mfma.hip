@@ -778,8 +778,9 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   for (int wi = it0; wi < it1; ++wi) {
   const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
   const int kind = wk[3];
-  // without pieces the other pass (or the tail kernel) owns it (uniform)
-  if (!pieces && kind != pass) continue;
+  // without pieces the other pass (or the tail kernel) owns it (uniform);
+  // kinds 0, 2 and 3 are int4 ranges, kind 1 the tail
+  if (!pieces && (kind == 1 ? 1 : 0) != pass) continue;
   if constexpr (TAIL) {
     if (kind == 1) {
       tail::tail_item<TQ>(lds_raw, query, hq, kvh, qscale, kq, ks, km, vq, vs, vm, bs, g, nb,
@@ -791,6 +792,9 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   const int b = wk[0];
   const int pb = wk[1];
   const int pe = wk[2];
+  // kind 2 / 3: only the even / odd 64-position chunks of [pb, pe) (the
+  // other half is the paired item's, on the same XCD)
+  const int half = kind >= 2 ? kind - 2 : -1;
   const int rep = hq / kvh;
   const int n = lane & 15;
   const int kg = lane >> 4;
@@ -814,19 +818,33 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
                          ks + krow * gpb + off0 / g, km + krow * gpb + off0 / g, gpb,
                          vs + vtok * ng, vm + vtok * ng, ng, g, with_ks);
   };
-  // One tile step: DMA of tile p0 + GT into `nxt`, then compute tile p0 from
-  // `cur`.  Both buffers are __restrict__ within the step, which tells the
+  // the wave's tiles: every GT-aligned tile of [pb, pe), or with a half only
+  // those in its 64-position chunks
+  auto next_tile = [&](int p) {
+    p += GT;
+    if (half >= 0 && ((p - pb) >> 6 & 1) != half) p += 64;
+    return p;
+  };
+  auto prev_tile = [&](int p) {
+    p -= GT;
+    if (half >= 0 && ((p - pb) >> 6 & 1) != half) p -= 64;
+    return p;
+  };
+  const int p_first = half == 1 ? pb + 64 : pb;
+  const int gsh = __builtin_ctz(static_cast<unsigned>(g));  // g is a power of two
+  // One tile step: DMA of the wave's next tile into `nxt`, then compute tile
+  // p0 from `cur`.  Both buffers are __restrict__ within the step, which tells the
   // compiler's wait-count pass that the reads of `cur` cannot alias the DMA
   // in flight into `nxt`: without it the pass puts vmcnt(0) -- a wait for the
   // next tile -- in front of the first LDS read and the double buffer never
   // overlaps.  The wait for tile p0 itself is explicit.
   QGroup qg;
   auto step = [&](const char* __restrict__ cur, char* __restrict__ nxt, int p0) {
-    const int p1 = p0 + GT;
+    const int p1 = next_tile(p0);
     if (p1 < pe) {
-      // items start on 128-token boundaries and g <= 128 divides them, so a
-      // tile needs the key scales exactly when it starts a key group
-      if (p1 % g == 0) {
+      // a tile needs the key scales exactly when its key group differs from
+      // the wave's previous tile's
+      if ((p1 >> gsh) != (p0 >> gsh)) {
         issue(nxt, p1, true);
         wait_vmcnt<T::NINST>();
       } else {
@@ -837,9 +855,10 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
       wait_vmcnt<0>();
     }
     const uint32_t* W = reinterpret_cast<const uint32_t*>(cur);
-    // tiles are GT-aligned and GT divides g: a tile starts a key group or
-    // continues the previous tile's
-    if (p0 == pb || p0 % g == 0) prepare_group<TQ, CPG, FOLD, KSV>(W, n, kg, qv, qscale, qg);
+    // tiles are GT-aligned and GT divides g: the wave's first tile, or one in
+    // another key group than its previous tile, prepares the group's Q'
+    if (p0 == p_first || (p0 >> gsh) != (prev_tile(p0) >> gsh))
+      prepare_group<TQ, CPG, FOLD, KSV>(W, n, kg, qv, qscale, qg);
     const WaveValues<CPG, VG1> vals(W, kg, n % CPG);
     if (p0 + GT <= pe)
       compute_tile<TQ, CPG, VG1, true, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run,
@@ -848,9 +867,9 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
       compute_tile<TQ, CPG, VG1, false, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run,
                                               acc.l_run, acc.o_acc, acc.c_acc, acc.bias_v);
   };
-  if (pb < pe) issue(lds_raw, pb, true);  // prologue: tile 0 into buffer 0
+  if (p_first < pe) issue(lds_raw, p_first, true);  // prologue: tile 0 into buffer 0
   int cur = 0;
-  for (int p0 = pb; p0 < pe; p0 += GT) {
+  for (int p0 = p_first; p0 < pe; p0 = next_tile(p0)) {
     step(lds_raw + cur * T::BYTES, lds_raw + (cur ^ 1) * T::BYTES, p0);
     // every LDS read of this buffer has been consumed before the next
     // iteration's DMA may overwrite it

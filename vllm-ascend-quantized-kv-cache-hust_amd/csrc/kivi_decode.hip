@@ -183,10 +183,13 @@ kivi_decode_generic_kernel(const TQ* __restrict__ query, int hq, int kvh, int d,
   const int h = blockIdx.y;
   const int lane = threadIdx.x;
   const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
-  if ((skip_kind0 && wk[3] == 0) || (skip_kind1 && wk[3] == 1)) return;  // MFMA kernels own these
+  // the MFMA kernels own these (kinds 0, 2, 3: int4 ranges; kind 1: tail)
+  if ((skip_kind0 && wk[3] != 1) || (skip_kind1 && wk[3] == 1)) return;
   const int b = wk[0];
   const int pb = wk[1];
   const int pe = wk[2];
+  // kind 2 / 3: only the even / odd 64-position chunks of [pb, pe)
+  const int half = wk[3] >= 2 ? wk[3] - 2 : -1;
   const int32_t* sm = seq_meta + 8 * static_cast<int64_t>(b);
   const int khist = sm[1], vhist = sm[2], row = sm[3], kfirst = sm[4], vfirst = sm[5];
   const int rep = hq / kvh;
@@ -215,7 +218,7 @@ kivi_decode_generic_kernel(const TQ* __restrict__ query, int hq, int kvh, int d,
     for (int k = 0; k < kMaxDpl; ++k) acc[r][k] = 0.0f;
   }
 
-  for (int p0 = pb; p0 < pe; p0 += 64) {
+  for (int p0 = pb + (half == 1 ? 64 : 0); p0 < pe; p0 += (half >= 0 ? 128 : 64)) {
     const int n = (pe - p0) < 64 ? (pe - p0) : 64;
     {
       const int m = khist - p0 < 0 ? 0 : (khist - p0 < n ? khist - p0 : n);  // int4 keys

@@ -12,18 +12,22 @@ namespace kvq {
 // ---- XCD-aware grid mapping ------------------------------------------------
 // Workgroups are handed to the 8 XCDs round-robin (id % 8).  The kv heads of
 // one work item share HBM lines: a token's value words and value scales/mins
-// of all heads are contiguous.  Mapping id -> (item, head) so that every head
-// of an item lands on the same XCD lets that XCD's L2 serve each line once.
+// of all heads are contiguous.  Items are also taken in pairs (2P, 2P+1): a
+// paired int4 range's two halves (its even and its odd 64-position tiles)
+// read the two halves of the same key lines.  Mapping id -> (item, head) so
+// that every head of both items of a pair lands on XCD P % 8, dispatched back
+// to back, lets that XCD's L2 serve each of those lines once.
 constexpr int kXcds = 8;
 
 __host__ __device__ __forceinline__ int64_t xcd_grid_size(int64_t num_work, int kvh) {
-  return (num_work + kXcds - 1) / kXcds * kXcds * kvh;
+  return (num_work + 2 * kXcds - 1) / (2 * kXcds) * (2 * kXcds) * kvh;
 }
 
 __device__ __forceinline__ bool xcd_item_head(int64_t id, int kvh, int64_t num_work, int& item,
                                               int& head) {
   const int64_t j = id / kXcds;
-  const int64_t it = id % kXcds + kXcds * (j / kvh);
+  const int64_t pair = id % kXcds + kXcds * (j / (2 * kvh));
+  const int64_t it = 2 * pair + (j / kvh) % 2;
   head = static_cast<int>(j % kvh);
   item = static_cast<int>(it);
   return it < num_work;

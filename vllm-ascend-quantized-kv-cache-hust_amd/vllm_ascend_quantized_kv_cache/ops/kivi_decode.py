@@ -56,13 +56,18 @@ def choose_split_tokens(total_positions: int, num_kv_heads: int, cu_count: int =
 
 
 def plan_decode_work(
-    seqs: list[DecodeSeq], split_tokens: int
+    seqs: list[DecodeSeq], split_tokens: int, paired: bool = False
 ) -> tuple[np.ndarray, np.ndarray]:
     """``(seq_meta int32 [B, 8], work int32 [W, 4])`` for the decode kernel.
 
     Kind-0 items cover positions where both sides are int4 (split every
-    ``split_tokens``); one kind-1 item covers the rest (at most two residual
-    windows long).  Every request owns at least one item, contiguous in the list.
+    ``split_tokens``); kind-1 items cover the rest (at most two residual
+    windows long).  Every request owns at least one item, contiguous in the
+    list.  ``paired``: each int4 range of ``2 * split_tokens`` positions is
+    two items, kind 2 (its even 64-position chunks) at an even index and kind
+    3 (its odd chunks) right after, which the kernel runs side by side on one
+    XCD so the two share every key line (a request that would start a pair at
+    an odd index opens with an empty kind-1 item).
     """
     # kind-0 items start on 128-token boundaries: the MFMA kernel walks
     # page- and key-group-aligned tiles of up to 128 tokens
@@ -73,9 +78,16 @@ def plan_decode_work(
         first = len(work)
         end_a = max(0, min(s.k_hist, s.v_hist, s.seq_len))
         p = 0
+        if paired and end_a > 0 and len(work) % 2:
+            work.append((b, 0, 0, 1))
         while p < end_a:
-            e = min(end_a, p + split_tokens)
-            work.append((b, p, e, 0))
+            if paired:
+                e = min(end_a, p + 2 * split_tokens)
+                work.append((b, p, e, 2))
+                work.append((b, p, e, 3))
+            else:
+                e = min(end_a, p + split_tokens)
+                work.append((b, p, e, 0))
             p = e
         # the mixed-source tail (at most two residual windows) in 64-position
         # items, so tails of different requests and heads run side by side
@@ -174,11 +186,12 @@ def plan_decode(
     Work that fills the chip's wave slots once (pieces of at most
     ``PIECE_MAX_COST``) is cut into equal-cost pieces (``plan_decode_pieces``):
     with a single round, the wave that ends last sets the time, so every wave
-    gets the same cost.  More work runs as items split every
-    ``choose_split_tokens`` positions with the tail items last
-    (``plan_decode_work``): over many rounds the hardware hands items to free
-    slots, and the small tail items at the end fill the last round's gaps
-    (measured on 256 x 32K tokens: 2.63 ms against 2.71 ms for pieces).
+    gets the same cost.  More work runs as items of ``choose_split_tokens``
+    int4 positions per wave, in pairs that share their key lines, with the
+    tail items last (``plan_decode_work(paired=True)``): over many rounds the
+    hardware hands items to free slots, and the small tail items at the end
+    fill the last round's gaps (measured on 256 x 32K tokens, unpaired: 2.63
+    ms against 2.71 ms for pieces).
     """
     slots = max(1, cu_count * WAVES_PER_CU // max(1, num_kv_heads))
     total = 0.0
@@ -187,8 +200,10 @@ def plan_decode(
         total += -(-end_a // 64) * 64 + (s.seq_len - end_a) * TAIL_POSITION_COST
     if total <= slots * PIECE_MAX_COST:
         return plan_decode_pieces(seqs, num_kv_heads, cu_count)
+    # paired items: each wave still takes split_tokens int4 positions
     meta, work = plan_decode_work(
-        seqs, choose_split_tokens(sum(s.seq_len for s in seqs), num_kv_heads, cu_count)
+        seqs, choose_split_tokens(sum(s.seq_len for s in seqs), num_kv_heads, cu_count),
+        paired=True,
     )
     return meta, work, None
 
