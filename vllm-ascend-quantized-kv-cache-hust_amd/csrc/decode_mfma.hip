@@ -657,10 +657,10 @@ __device__ __forceinline__ QRegs<TQ> load_q(const TQ* __restrict__ query, int b,
 struct PageIds {
   const int32_t* bt;
   int64_t maxb, nb;
-  int bs, pg0, pg_last, lane, vec;
-  __device__ __forceinline__ PageIds(const int32_t* bt_, int64_t maxb_, int64_t nb_, int bs_,
+  int bsh, pg0, pg_last, lane, vec;  // bs = 1 << bsh
+  __device__ __forceinline__ PageIds(const int32_t* bt_, int64_t maxb_, int64_t nb_, int bsh_,
                                      int pb, int pe, int lane_)
-      : bt(bt_), maxb(maxb_), nb(nb_), bs(bs_), pg0(pb / bs_), pg_last((pe - 1) / bs_),
+      : bt(bt_), maxb(maxb_), nb(nb_), bsh(bsh_), pg0(pb >> bsh_), pg_last((pe - 1) >> bsh_),
         lane(lane_), vec(0) {
     if (pb < pe) vec = load();
   }
@@ -672,11 +672,11 @@ struct PageIds {
   // page of position p; positions only move forward, one tile (<= one page)
   // at a time
   __device__ __forceinline__ int64_t page(int p) {
-    if (p / bs - pg0 >= 64) {  // uniform; only items longer than 64 pages get here
+    if ((p >> bsh) - pg0 >= 64) {  // uniform; only items longer than 64 pages get here
       pg0 += 64;
       vec = load();
     }
-    return __builtin_amdgcn_readlane(vec, p / bs - pg0);
+    return __builtin_amdgcn_readlane(vec, (p >> bsh) - pg0);
   }
 };
 
@@ -808,14 +808,18 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
 
   WaveAcc<CPG, VG1> acc;
   acc.init();
-  PageIds pages(block_table + static_cast<int64_t>(b) * maxb, maxb, nb, bs, pb, pe, lane);
+  // bs and g are powers of two (the launcher checks): page, offset and key
+  // group come from shifts and masks, not integer divisions
+  const int bsh = __builtin_ctz(static_cast<unsigned>(bs));
+  const int gsh = __builtin_ctz(static_cast<unsigned>(g));
+  PageIds pages(block_table + static_cast<int64_t>(b) * maxb, maxb, nb, bsh, pb, pe, lane);
   auto issue = [&](char* buf, int p, bool with_ks) {
     const int64_t blk = pages.page(p);
-    const int off0 = p % bs;
+    const int off0 = p & (bs - 1);
     const int64_t krow = (blk * kvh + h) * D;
-    const int64_t vtok = (blk * bs + off0) * kvh + h;
-    issue_tile<CPG, VG1, KSV>(buf, ld, kq + krow * wpd + off0 / 8, wpd, vq + vtok * 16, kvh,
-                         ks + krow * gpb + off0 / g, km + krow * gpb + off0 / g, gpb,
+    const int64_t vtok = ((blk << bsh) + off0) * kvh + h;
+    issue_tile<CPG, VG1, KSV>(buf, ld, kq + krow * wpd + (off0 >> 3), wpd, vq + vtok * 16, kvh,
+                         ks + krow * gpb + (off0 >> gsh), km + krow * gpb + (off0 >> gsh), gpb,
                          vs + vtok * ng, vm + vtok * ng, ng, g, with_ks);
   };
   // the wave's tiles: every GT-aligned tile of [pb, pe), or with a half only
@@ -831,7 +835,6 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
     return p;
   };
   const int p_first = half == 1 ? pb + 64 : pb;
-  const int gsh = __builtin_ctz(static_cast<unsigned>(g));  // g is a power of two
   // One tile step: DMA of the wave's next tile into `nxt`, then compute tile
   // p0 from `cur`.  Both buffers are __restrict__ within the step, which tells the
   // compiler's wait-count pass that the reads of `cur` cannot alias the DMA
@@ -928,13 +931,14 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
   *launched = false;
   *tail_done = false;
   if (d != 128 || hq / kvh > 16 || g % 8 || d % g || g < 32 || g > 128) return KVQ_OK;
+  if (bs <= 0 || (bs & (bs - 1))) return KVQ_OK;  // power-of-two pages (shift arithmetic)
   // tiles of 64 tokens (32 for G = 32): inside one key group and one page
   const int cpg = g >= 64 ? 8 : 4;
   if (bs % (8 * cpg)) return KVQ_OK;
   const uint32_t* kqu = reinterpret_cast<const uint32_t*>(kq);
   const uint32_t* vqu = reinterpret_cast<const uint32_t*>(vq);
   const int64_t pass_len = xcd_grid_size(num_work, kvh);
-  const bool tail = tail_path_applies(q_dtype, hq, kvh, d, ring_dtype);
+  const bool tail = tail_path_applies(q_dtype, hq, kvh, d, ring_dtype, bs);
   // pieces need the tail path (a piece mixes int4 and tail items)
   const bool use_pieces = tail && pieces && num_pieces > 0;
   const int64_t blocks =

@@ -3,8 +3,8 @@
 // item), for one kv head, on one wave: the tail path of the int4 decode kernel.
 //
 // A request's tail is the positions past min(k_hist, v_hist): keys there are
-// int4 (below k_hist) or residual-ring rows, values are ring rows.  The wave
-// walks its item (at most 64 positions) in sub-tiles of kTT = 32 positions:
+// int4 (below k_hist) or residual-ring rows, values int4 (below v_hist) or
+// ring rows.  The wave walks its item in sub-tiles of kTT = 32 positions:
 //   * stages the sub-tile's K as [token][dim] in the activation dtype T: int4
 //     history is dequantized (q*scale then +mn in fp32, the reference's gather
 //     arithmetic, pkg/methods/kivi_int4/attention_backend.py:849-935) and kept
@@ -49,6 +49,30 @@ __device__ __forceinline__ uint16_t bits_of(float x) {
   return __builtin_bit_cast(uint16_t, v);
 }
 
+// Two values as T, round to nearest even, in one register (a in the low half):
+// one hardware pair conversion instead of two software roundings.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t pack2<bf16>(float a, float b) { return bf16x2_bits(a, b); }
+template <>
+__device__ __forceinline__ uint32_t pack2<f16>(float a, float b) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v{a, b}), h2v));
+}
+// The low / high T half of a pair, widened to fp32 (exact).
+template <typename T>
+__device__ __forceinline__ float half_f32(uint32_t w, int hi);
+template <>
+__device__ __forceinline__ float half_f32<bf16>(uint32_t w, int hi) {
+  return __uint_as_float(hi ? (w & 0xffff0000u) : (w << 16));
+}
+template <>
+__device__ __forceinline__ float half_f32<f16>(uint32_t w, int hi) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(hi ? w >> 16 : w)));
+}
+
 __device__ __forceinline__ float sum_kg(float v) {  // over the 4 lane groups of 16
   v += __shfl_xor(v, 16, 64);
   v += __shfl_xor(v, 32, 64);
@@ -60,10 +84,18 @@ __device__ __forceinline__ float max_kg(float v) {
   return v;
 }
 
-__device__ __forceinline__ int64_t clamp_page(const int32_t* __restrict__ bt, int p, int bs,
+__device__ __forceinline__ int64_t clamp_page(const int32_t* __restrict__ bt, int p, int bsh,
                                               int64_t nb) {
-  const int64_t blk = bt[p / bs];
+  const int64_t blk = bt[p >> bsh];
   return blk < 0 ? 0 : (blk >= nb ? nb - 1 : blk);  // never leave the cache
+}
+
+// Ring lane of window entry x = first + (p - hist): first < ring_len and the
+// window is shorter than the ring, so one conditional subtract replaces the
+// modulo; the clamp keeps a malformed entry inside the ring.
+__device__ __forceinline__ int ring_lane(int x, int ring_len) {
+  x = x >= ring_len ? x - ring_len : x;
+  return x < ring_len ? (x < 0 ? 0 : x) : ring_len - 1;
 }
 
 constexpr int kD = 128;
@@ -103,8 +135,12 @@ __device__ __forceinline__ void tail_item(char* __restrict__ lds_raw, const T* _
   const int rep = hq / kvh;
   const int n = lane & 15;
   const int kg = lane >> 4;
-  const int gpb = bs / g;
-  const int wpd = bs / 8;
+  // bs and g are powers of two: positions split into page and offset, and
+  // offsets into key groups, with shifts and masks, not integer divisions
+  const int bsh = __builtin_ctz(static_cast<unsigned>(bs));
+  const int gsh = __builtin_ctz(static_cast<unsigned>(g));
+  const int gpb = bs >> gsh;
+  const int wpd = bs >> 3;
   const int32_t* bt = block_table + static_cast<int64_t>(b) * maxb;
   const int64_t ring_row0 = static_cast<int64_t>(row) * ring_len;
 
@@ -134,33 +170,38 @@ __device__ __forceinline__ void tail_item(char* __restrict__ lds_raw, const T* _
     {
       const int mk = khist - p0 < 0 ? 0 : (khist - p0 < nt ? khist - p0 : nt);  // int4 keys
       if (mk > 0) {
-        // lane = dim: the <= kKW words of the dim covering positions [p0, p0+mk)
+        // lane: dims 2*lane and 2*lane + 1, the <= kKW words of each covering
+        // positions [p0, p0+mk); the two dims of a token go out as one pair
         const int first = p0 & ~7;
-        for (int c = lane; c < D; c += 64) {
-          uint32_t w[kKW];
-          float sc[kKW], mn[kKW];
+        const int c0 = 2 * lane;
+        uint32_t w[2][kKW];
+        float sc[2][kKW], mn[2][kKW];
 #pragma unroll
-          for (int k = 0; k < kKW; ++k) {
-            // clamped into [p0, p0 + mk): every load is valid and unconditional
-            const int p = first + 8 * k;
-            const int pp = p < p0 ? p0 : (p < p0 + mk ? p : p0 + mk - 1);
-            const int64_t r = (clamp_page(bt, pp, bs, nb) * kvh + h) * D + c;
-            const int off = pp % bs;
-            w[k] = kq[r * wpd + off / 8];
-            sc[k] = ks[r * gpb + off / g];
-            mn[k] = km[r * gpb + off / g];
+        for (int k = 0; k < kKW; ++k) {
+          // clamped into [p0, p0 + mk): every load is valid and unconditional
+          const int p = first + 8 * k;
+          const int pp = p < p0 ? p0 : (p < p0 + mk ? p : p0 + mk - 1);
+          const int64_t r = (clamp_page(bt, pp, bsh, nb) * kvh + h) * D + c0;
+          const int off = pp & (bs - 1);
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            w[e][k] = kq[(r + e) * wpd + (off >> 3)];
+            sc[e][k] = ks[(r + e) * gpb + (off >> gsh)];
+            mn[e][k] = km[(r + e) * gpb + (off >> gsh)];
           }
+        }
 #pragma unroll
-          for (int k = 0; k < kKW; ++k) {
+        for (int k = 0; k < kKW; ++k) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const int t = first + 8 * k + j - p0;
-              if (t >= 0 && t < mk) {
-                const float x = kivi_dequant((w[k] >> (4 * j)) & 0xfu, sc[k], mn[k]);
-                const T hi = from_f32<T>(x);
-                sk[t * kKP + c] = __builtin_bit_cast(uint16_t, hi);
-                skl[t * kKP + c] = bits_of<T>(x - to_f32(hi));
-              }
+          for (int j = 0; j < 8; ++j) {
+            const int t = first + 8 * k + j - p0;
+            if (t >= 0 && t < mk) {
+              const float x0 = kivi_dequant((w[0][k] >> (4 * j)) & 0xfu, sc[0][k], mn[0][k]);
+              const float x1 = kivi_dequant((w[1][k] >> (4 * j)) & 0xfu, sc[1][k], mn[1][k]);
+              const uint32_t hi = pack2<T>(x0, x1);
+              *reinterpret_cast<uint32_t*>(sk + t * kKP + c0) = hi;
+              *reinterpret_cast<uint32_t*>(skl + t * kKP + c0) =
+                  pack2<T>(x0 - half_f32<T>(hi, 0), x1 - half_f32<T>(hi, 1));
             }
           }
         }
@@ -174,7 +215,7 @@ __device__ __forceinline__ void tail_item(char* __restrict__ lds_raw, const T* _
           const int t0k = t0 + 64 * k + lane;
           const int t = t0k < tasks ? t0k : tasks - 1;  // clamped: unconditional load
           const int pi = mk + t / (D / 8);
-          const int rl = (kfirst + (p0 + pi - khist)) % ring_len;
+          const int rl = ring_lane(kfirst + (p0 + pi - khist), ring_len);
           x[k] = *reinterpret_cast<const uint4*>(ring_k + ((ring_row0 + rl) * kvh + h) * D +
                                                  8 * (t % (D / 8)));
         }
@@ -237,59 +278,61 @@ __device__ __forceinline__ void tail_item(char* __restrict__ lds_raw, const T* _
     }
 
     // ---- V rows, stored transposed ----------------------------------------------
+    // lane task = (token pair, 8-dim word): both tokens' 8 values as T pairs
+    // (int4 words dequantized, ring rows as they are), then for every dim one
+    // 32-bit store of the two tokens, which are adjacent in the [dim][token] rows
     {
       const int mv = vhist - p0 < 0 ? 0 : (vhist - p0 < nt ? vhist - p0 : nt);  // int4 values
       const int nd = D / 8;
-      for (int t0 = 0; t0 < mv * nd; t0 += 64 * 4) {
-        uint32_t w[4];
-        float sc[4], mn[4];
+      const int tasks = ((nt + 1) / 2) * nd;
+      for (int t0 = 0; t0 < tasks; t0 += 64 * 2) {
+        uint4 x[2][2];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < 2; ++k) {
           const int t0k = t0 + 64 * k + lane;
-          const int t = t0k < mv * nd ? t0k : mv * nd - 1;  // clamped: unconditional load
-          const int p = p0 + t / nd;
+          const int t = t0k < tasks ? t0k : tasks - 1;  // clamped: unconditional loads
           const int dv = t % nd;
-          const int64_t vrow = (clamp_page(bt, p, bs, nb) * bs + p % bs) * kvh + h;
-          w[k] = vq[vrow * nd + dv];
-          sc[k] = vs[vrow * (D / g) + (8 * dv) / g];
-          mn[k] = vm[vrow * (D / g) + (8 * dv) / g];
-        }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int t = t0 + 64 * k + lane;
-          if (t < mv * nd) {
-            const int pi = t / nd;
-            const int dv = t % nd;
+          for (int e = 0; e < 2; ++e) {
+            int pi = 2 * (t / nd) + e;
+            pi = pi < nt ? pi : nt - 1;  // an odd sub-tile's last pair: zeroed below
+            if (pi < mv) {
+              const int p = p0 + pi;
+              const int64_t vrow =
+                  ((clamp_page(bt, p, bsh, nb) << bsh) + (p & (bs - 1))) * kvh + h;
+              const uint32_t w = vq[vrow * nd + dv];
+              const float sc = vs[vrow * (D >> gsh) + ((8 * dv) >> gsh)];
+              const float mn = vm[vrow * (D >> gsh) + ((8 * dv) >> gsh)];
+              uint32_t q[4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-              svt[(8 * dv + i) * kVP + pi] =
-                  bits_of<T>(kivi_dequant((w[k] >> (4 * i)) & 0xfu, sc[k], mn[k]));
+              for (int i = 0; i < 4; ++i)
+                q[i] = pack2<T>(kivi_dequant((w >> (8 * i)) & 0xfu, sc, mn),
+                                kivi_dequant((w >> (8 * i + 4)) & 0xfu, sc, mn));
+              x[k][e] = make_uint4(q[0], q[1], q[2], q[3]);
+            } else {
+              const int rl = ring_lane(vfirst + (p0 + pi - vhist), ring_len);
+              x[k][e] = *reinterpret_cast<const uint4*>(
+                  ring_v + ((ring_row0 + rl) * kvh + h) * D + 8 * dv);
+            }
           }
         }
-      }
-      const int tasks = (nt - mv) * nd;
-      for (int t0 = 0; t0 < tasks; t0 += 64 * 4) {
-        uint4 x[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int t0k = t0 + 64 * k + lane;
-          const int t = t0k < tasks ? t0k : tasks - 1;  // clamped: unconditional load
-          const int pi = mv + t / nd;
-          const int rl = (vfirst + (p0 + pi - vhist)) % ring_len;
-          x[k] = *reinterpret_cast<const uint4*>(ring_v + ((ring_row0 + rl) * kvh + h) * D +
-                                                 8 * (t % nd));
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < 2; ++k) {
           const int t = t0 + 64 * k + lane;
           if (t < tasks) {
-            const int pi = mv + t / nd;
+            const int pi0 = 2 * (t / nd);
             const int dv = t % nd;
-            const uint32_t e[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+            const bool past = pi0 + 1 >= nt;
+            const uint32_t a[4] = {x[k][0].x, x[k][0].y, x[k][0].z, x[k][0].w};
+            const uint32_t b[4] = {x[k][1].x, x[k][1].y, x[k][1].z, x[k][1].w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              svt[(8 * dv + 2 * i) * kVP + pi] = static_cast<uint16_t>(e[i] & 0xffffu);
-              svt[(8 * dv + 2 * i + 1) * kVP + pi] = static_cast<uint16_t>(e[i] >> 16);
+              const uint32_t bb = past ? 0u : b[i];
+              // dim 8 dv + 2 i: the low halves; dim 8 dv + 2 i + 1: the high halves
+              *reinterpret_cast<uint32_t*>(svt + (8 * dv + 2 * i) * kVP + pi0) =
+                  __builtin_amdgcn_perm(bb, a[i], 0x05040100u);
+              *reinterpret_cast<uint32_t*>(svt + (8 * dv + 2 * i + 1) * kVP + pi0) =
+                  __builtin_amdgcn_perm(bb, a[i], 0x07060302u);
             }
           }
         }

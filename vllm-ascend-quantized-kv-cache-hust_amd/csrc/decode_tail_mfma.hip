@@ -44,7 +44,7 @@ int launch_kivi_decode_tail_mfma(const void* query, int q_dtype, int hq, int kvh
                                  int ring_len, float* ws_o, float* ws_ml, hipStream_t s,
                                  bool* launched) {
   *launched = false;
-  if (!tail_path_applies(q_dtype, hq, kvh, d, ring_dtype)) return KVQ_OK;
+  if (!tail_path_applies(q_dtype, hq, kvh, d, ring_dtype, bs)) return KVQ_OK;
   const dim3 grid(static_cast<unsigned>(xcd_grid_size(num_work, kvh)));
   const size_t lds = tail::kLdsBytes;
   const uint32_t* kqu = reinterpret_cast<const uint32_t*>(kq);

@@ -40,9 +40,10 @@ inline int64_t decode_workspace_bytes(int64_t num_work, int num_heads, int head_
 }
 
 // The MFMA tail path (kind-1 items) applies: D = 128, GQA group <= 16, query
-// and ring in the same 16-bit dtype.
-inline bool tail_path_applies(int q_dtype, int hq, int kvh, int d, int ring_dtype) {
-  return d == 128 && hq / kvh <= 16 && ring_dtype == q_dtype &&
+// and ring in the same 16-bit dtype, and a power-of-two block size (its
+// position arithmetic is shifts and masks).
+inline bool tail_path_applies(int q_dtype, int hq, int kvh, int d, int ring_dtype, int bs) {
+  return d == 128 && hq / kvh <= 16 && ring_dtype == q_dtype && bs > 0 && (bs & (bs - 1)) == 0 &&
          (q_dtype == KVQ_DTYPE_BF16 || q_dtype == KVQ_DTYPE_F16);
 }
 

@@ -25,7 +25,7 @@ TAIL_ITEM_TOKENS = 64
 #: decode waves resident per CU (the MFMA kernel's LDS and register budget)
 WAVES_PER_CU = 8
 #: cost of one residual-window (tail) position against one int4 position
-TAIL_POSITION_COST = 10.0
+TAIL_POSITION_COST = 8.0
 #: largest piece, in int4 positions: more work than one piece per wave slot
 #: of this size runs as several rounds of pieces, dispatched as slots free
 PIECE_MAX_COST = 4096.0
