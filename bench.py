@@ -570,6 +570,55 @@ def bench_int8_decode(torch, dev, *, reps=20, seed=0, layers=2):
             "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
 
 
+def bench_int8_ops(torch, dev, *, reps=10, seed=0):
+    """Config 2's prefill-side INT8 ops over its whole batch (64 x 4096 tokens,
+    8 KV heads, D 128, bf16): first-K/V scales, quantize + scatter into the
+    shuffled pages, and paged dequant back to dense TND."""
+    from vllm_ascend_quantized_kv_cache.ops.int8_ops import (
+        int8_calc_scales,
+        int8_dequant_gather,
+        int8_quant_scatter,
+    )
+
+    b, kvh, d, bs, n = 64, 8, 128, 128, 4096
+    nb = b * n // bs
+    gen = torch.Generator().manual_seed(seed)
+    table = torch.randperm(nb, generator=gen).view(b, n // bs).to(torch.int32).to(dev)
+    key_scales = torch.exp(torch.randn((kvh, d), generator=gen)).to(dev)
+    gdev = torch.Generator(device=dev).manual_seed(seed + 9)
+    t = b * n
+    key = (torch.randn((t, kvh, d), generator=gdev, device=dev) * key_scales).to(torch.bfloat16)
+    value = torch.randn((t, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
+    pos = torch.arange(n, device=dev)
+    slots = torch.cat([table[i].to(torch.int64)[pos // bs] * bs + pos % bs for i in range(b)])
+    kc = torch.zeros((nb, bs, kvh, d), dtype=torch.int8, device=dev)
+    vc = torch.zeros_like(kc)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn):
+        sustain(torch, fn)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    res = {}
+    elems = t * kvh * d  # per side
+    ms = timed(lambda: int8_calc_scales(key, value))
+    res["scales"] = (ms, 2 * elems * 2)  # reads both bf16 sides
+    k_inv, v_inv, k_aq, v_aq = int8_calc_scales(key, value)
+    ms = timed(lambda: int8_quant_scatter(key, value, k_inv, v_inv, slots, kc, vc))
+    res["quant_scatter"] = (ms, 2 * elems * (2 + 1))  # bf16 in, int8 out
+    ms = timed(lambda: int8_dequant_gather(kc, vc, table, [n] * b, torch.bfloat16, k_aq, v_aq))
+    res["dequant_gather"] = (ms, 2 * elems * (1 + 2))  # int8 in, bf16 out
+    del key, value, kc, vc
+    torch.cuda.empty_cache()
+    return {k: {"ms": round(ms, 4), "gbs": round(byt / ms / 1e6, 1),
+                "frac": round(byt / ms / 1e6 / HBM_PEAK_GBS, 4)} for k, (ms, byt) in res.items()}
+
+
 # ---------------------------------------------------------------------------
 
 
@@ -638,6 +687,10 @@ def main() -> int:
             f"attention {pg['attn_tflops']:.0f} TFLOP/s")
         i8 = bench_int8_decode(torch, dev)
         extra["config2_int8_decode"] = {k: round(v, 4) for k, v in i8.items()}
+        i8ops = bench_int8_ops(torch, dev)
+        for k, v in i8ops.items():
+            extra[f"config2_int8_{k}"] = v
+        log("config2: " + ", ".join(f"{k} {v['gbs']:.0f} GB/s" for k, v in i8ops.items()))
         log(f"config2: int8 decode {i8['us_per_layer']:.1f} us ({i8['gbs']:.0f} GB/s)")
         if not args.no_config5:
             # one layer: 10.8 GB of pages, far past any cache

@@ -18,7 +18,9 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("t,kvh,d", [(16, 2, 8), (300, 8, 128), (1, 4, 64)])
+@pytest.mark.parametrize("t,kvh,d", [(16, 2, 8), (300, 8, 128), (1, 4, 64),
+                                     (5000, 16, 256),  # two 2048-channel chunks, 5 token slices
+                                     (700, 3, 40)])    # 15 threads per row, 17 phases
 def test_int8_scales_and_quant_bit_exact(gpu_device, dtype, t, kvh, d):
     from vllm_ascend_quantized_kv_cache.ops.int8_ops import int8_calc_scales, int8_quant_scatter
 

@@ -11,6 +11,8 @@
 //   * decode     -- i8ab:173-205 (fused attention with per-channel antiquant).
 // Every arithmetic step of scales/quantize/dequant rounds to the activation
 // dtype exactly where torch does, so codes and scales are bit-exact.
+#include <algorithm>
+
 #include "kvq_common.h"
 #include "kvq_decode.h"
 
@@ -20,28 +22,60 @@ using namespace kvq;
 
 // ---- scales ----------------------------------------------------------------
 
-// amax over tokens: each thread reduces a strip of tokens for 8 channels and
-// folds it in with an integer atomicMax (|x| bits order like the floats).
+// amax over tokens, per channel and side.  A workgroup takes a slice of the
+// tokens for up to 2048 channels (blockIdx.y picks the 2048): thread (r, ph)
+// keeps the max of channels [8r, 8r + 8) over tokens t0 + ph, t0 + ph +
+// phases, ... with four rows in flight per step; the phases meet in LDS and
+// one integer atomicMax per channel and workgroup folds the slice in (|x| bits
+// order like the floats, and the max does not depend on the order).
 template <typename T>
 __global__ void __launch_bounds__(256)
 int8_amax_kernel(const T* __restrict__ key, const T* __restrict__ value, int64_t tokens,
                  int64_t channels, int64_t tokens_per_block, uint32_t* __restrict__ amax) {
-  const int64_t c8 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  __shared__ float part[256 * 8];
   const int side = blockIdx.z;
-  if (c8 >= channels) return;
-  const T* x = side == 0 ? key : value;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * tokens_per_block;
+  const int64_t cbase = static_cast<int64_t>(blockIdx.y) * 2048;
+  const int cn = static_cast<int>(channels - cbase < 2048 ? channels - cbase : 2048);
+  const int rt = cn / 8;         // threads per token row, <= 256
+  const int phases = 256 / rt;   // >= 1
+  const int tid = threadIdx.x;
+  const int r = tid % rt;
+  const int ph = tid / rt;
+  const T* x = (side == 0 ? key : value) + cbase + 8 * r;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * tokens_per_block;
   const int64_t t1 = t0 + tokens_per_block < tokens ? t0 + tokens_per_block : tokens;
   float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int64_t t = t0; t < t1; ++t) {
-    float v[8];
-    load8(x + t * channels + c8, v);
+  if (ph < phases) {
+    int64_t t = t0 + ph;
+    for (; t + 3 * phases < t1; t += 4 * phases) {
+      float v0[8], v1[8], v2[8], v3[8];
+      load8(x + t * channels, v0);
+      load8(x + (t + phases) * channels, v1);
+      load8(x + (t + 2 * phases) * channels, v2);
+      load8(x + (t + 3 * phases) * channels, v3);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) a[i] = fmaxf(a[i], fabsf(v[i]));
+      for (int i = 0; i < 8; ++i)
+        a[i] = fmaxf(a[i], fmaxf(fmaxf(fabsf(v0[i]), fabsf(v1[i])),
+                                 fmaxf(fabsf(v2[i]), fabsf(v3[i]))));
+    }
+    for (; t < t1; t += phases) {
+      float v[8];
+      load8(x + t * channels, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = fmaxf(a[i], fabsf(v[i]));
+    }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    atomicMax(amax + side * channels + c8 + i, __float_as_uint(a[i]));
+  for (int i = 0; i < 8; ++i) part[tid * 8 + i] = a[i];
+  __syncthreads();
+  if (tid < rt) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float m = part[tid * 8 + i];
+      for (int q = 1; q < phases; ++q) m = fmaxf(m, part[(q * rt + tid) * 8 + i]);
+      atomicMax(amax + side * channels + cbase + 8 * tid + i, __float_as_uint(m));
+    }
+  }
 }
 
 __global__ void zero_u32_kernel(uint32_t* p, int64_t n) {
@@ -276,11 +310,13 @@ extern "C" int kvq_int8_calc_scales(const void* key, const void* value, int dtyp
                      s, amax_ws, n);
   KVQ_LAUNCH_CHECK();
   if (num_tokens > 0) {
-    const int64_t cblocks = (channels / 8 + 255) / 256;
-    const int64_t tpb = 64;
+    // about 256 token slices per side (at least 1024 tokens each): enough
+    // workgroups to fill the chip, few atomics per channel
+    const int64_t cblocks = (channels + 2047) / 2048;
+    const int64_t tpb = std::max<int64_t>(1024, (num_tokens + 255) / 256);
     const int64_t tblocks = (num_tokens + tpb - 1) / tpb;
-    if (tblocks > 65535) return KVQ_ERR_INVALID;
-    const dim3 grid(static_cast<unsigned>(cblocks), static_cast<unsigned>(tblocks), 2);
+    if (tblocks > 0x7fffffff || cblocks > 65535) return KVQ_ERR_INVALID;
+    const dim3 grid(static_cast<unsigned>(tblocks), static_cast<unsigned>(cblocks), 2);
     KVQ_DISPATCH_FLOAT(dtype, T,
       hipLaunchKernelGGL((int8_amax_kernel<T>), grid, dim3(256), 0, s,
                          static_cast<const T*>(key), static_cast<const T*>(value), num_tokens,
