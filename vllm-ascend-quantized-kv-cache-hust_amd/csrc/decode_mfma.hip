@@ -1,10 +1,13 @@
 // SPDX-License-Identifier: Apache-2.0
-// MFMA decode attention over KIVI int4 pages (kind-0 work items) for gfx950.
+// MFMA decode attention over KIVI int4 pages (kind-0, -2 and -3 work items)
+// for gfx950, with the tail (kind-1) items through decode_tail.h.
 //
-// One wave per (work item, kv head).  A work item is a 128-aligned range of
-// positions whose keys and values are both in int4 pages; the wave walks it in
-// "group tiles" of GT = 8*CPG tokens (CPG = 8 for G >= 64, 4 for G = 32), each
-// inside one page and one key-scale group.
+// One wave per (work item, kv head), or per (piece, kv head) walking a piece's
+// items.  An int4 item is a range of positions, starting on a multiple of 64,
+// whose keys and values are both in int4 pages (kinds 2 / 3: only its even /
+// odd 64-position chunks); the wave walks it in "group tiles" of GT = 8*CPG
+// tokens (CPG = 8 for G >= 64, 4 for G = 32), each inside one page and one
+// key-scale group.
 //
 // Tiles are double-buffered in the wave's LDS: while tile i is computed, the
 // DMA loads of tile i+1 (global_load_lds, 16-byte and 4-byte lanes, written

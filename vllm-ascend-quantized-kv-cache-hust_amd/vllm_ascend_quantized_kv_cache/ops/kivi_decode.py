@@ -69,8 +69,9 @@ def plan_decode_work(
     XCD so the two share every key line (a request that would start a pair at
     an odd index opens with an empty kind-1 item).
     """
-    # kind-0 items start on 128-token boundaries: the MFMA kernel walks
-    # page- and key-group-aligned tiles of up to 128 tokens
+    # int4 items start on 128-token boundaries, so paired items split on
+    # 64-position chunks and the MFMA kernel's tiles stay inside pages and
+    # key groups
     split_tokens = max(128, -(-int(split_tokens) // 128) * 128)
     meta = np.zeros((len(seqs), 8), dtype=np.int32)
     work: list[tuple[int, int, int, int]] = []
