@@ -365,14 +365,15 @@ def bench_kivi_decode(torch, dev, *, b, hq, kvh, d, g, r, bs, lens, steps, warmu
     return res
 
 
-def cpu_baseline_decode(torch, st, q, seqs, *, hq, kvh, d, g, bs, scale, sample=2):
-    """Oracle (reference algorithm in torch-CPU) on ``sample`` of the sequences."""
+def cpu_baseline_decode(torch, st, q, seqs, *, hq, kvh, d, g, bs, scale, sample=32):
+    """Oracle (reference algorithm in torch-CPU) on ``sample`` of the sequences
+    (the whole config-3 batch by default: about 3 s per run, 4 runs)."""
     from oracle import kvq_oracle as ref
 
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
     caches = tuple(t.cpu() for t in st.caches)
-    idx = list(range(sample))
+    idx = list(range(min(sample, len(seqs))))
     table = st.table_cpu[idx]
     lens = [seqs[i].seq_len for i in idx]
     wk, wv = [], []
@@ -403,7 +404,7 @@ def cpu_baseline_decode(torch, st, q, seqs, *, hq, kvh, d, g, bs, scale, sample=
         "cores": threads,
         "kind": "port",
         "sample": (
-            f"{sample} of {len(seqs)} config-3 sequences ({sum(lens)} tokens): oracle "
+            f"{len(idx)} of {len(seqs)} config-3 sequences ({sum(lens)} tokens): oracle "
             f"dequant-gather + residual overlay + fp32 SDPA, median of 3, {t * 1e3:.1f} ms"
         ),
         "ms": round(t * 1e3, 2),
