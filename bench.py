@@ -47,7 +47,7 @@ METRIC = "INT4 pack/gather-dequant GB/s (% HBM peak); fused INT4 decode attn µs
 def recorded_traffic(name: str) -> int | None:
     """HBM bytes per call recorded under profiles/ from the FETCH_SIZE /
     WRITE_SIZE counter runs (counters cannot be read inside a timed run)."""
-    path = ROOT / "profiles" / "decode_hbm_traffic_pmc.md"
+    path = ROOT / "profiles" / "hbm_traffic_decode_gather_pack_pmc.md"
     try:
         for line in path.read_text().splitlines():
             if line.startswith(f"traffic_bytes_per_call {name}:"):
