@@ -19,9 +19,9 @@
 //   group's G/8 adjacent lanes (DPP quad permutes and ds_swizzle).  Head sizes
 //   whose rows do not tile a wave keep the one-thread-per-word kernel.
 //
-// Both quantize with kivi_pack_word: a reciprocal per group and a
-// round-to-nearest per element, falling back to the exact division for an
-// element whose quotient sits at a rounding tie, so codes stay bit-exact.
+// Both quantize with kivi_pack_word: a reciprocal per group, a floor per
+// element, and two fmas that decide exactly, with no division and no branch,
+// whether the reference's rounded quotient reaches the next code.
 #include <mutex>
 
 #include "kvq_common.h"

@@ -143,32 +143,46 @@ __device__ __forceinline__ uint32_t kivi_quantize(float x, float mn, float scale
 }
 
 // One packed word (8 codes, code i at bits 4i) with the codes of
-// kivi_quantize but no division per element.  With d = x - mn (rounded as
-// there) and rcp = v_rcp_f32(scale) (1 ulp), v = d * rcp lies within 3e-6 of
-// d / scale for quotients below 16 (2^-23 * 16 from rcp, half an ulp of 16 from
-// the product), and the reference's floor(RN(RN(d / scale) + 0.5)) sits
-// within another 2e-6 of floor(d / scale + 0.5).  So rndne(v) -- which
-// differs from rounding half up only at a tie -- is the reference's code
-// whenever v is more than 1e-5 away from k + 0.5.  An element whose v lies
-// within 1e-5 of a tie is redone with the exact division, on its own: on bf16
-// inputs about 2e-3 of the elements do (exact ties 30 (x - mn) = (2k+1) (mx -
-// mn) are common on a 16-bit grid), and redoing whole words made a wave take
-// the division branch for most of its words.
+// kivi_quantize, exactly, with no division and no branch.
 //
-// mn <= x and scale >= (x - mn) / 15 (rounded up by at most an ulp, or the
-// 1e-6 floor) keep v inside [0, 15 + 4e-6], so rndne(v) is already a code in
-// 0..15: v_cvt_pk_u8_f32 drops each one into a byte (even codes of the word in
-// one register, odd codes in another) and a single shift-or interleaves the
-// nibbles.
+// With d = x - mn (rounded as there) and q = RN(d / scale), the reference's
+// code floor(RN(q + 0.5)) is k or k + 1 for k = floor(q).  RN(q + 0.5) is exact
+// for k >= 1, so the code is k + 1 iff q >= k + 0.5; for k = 0 the sum rounds
+// to 1 already at q = pred(0.5) = 0.5 - 2^-25 (1 - 2^-25 is a tie, to even).
+// With T_k = k + 0.5 (k >= 1) or pred(0.5) (k = 0):
+//
+//   q >= T_k  <=>  d / scale >= T_k - ulp(T_k) / 2  <=>  y >= 0,
+//   y = fma(scale * 2^-24, 2^e(T_k), fma(-scale, T_k, d))
+//
+// (round to nearest moves a quotient onto T_k from above the midpoint below
+// it; at the midpoint itself ties go to T_k for k >= 1, whose last mantissa
+// bit is 0, and d = scale * midpoint has no solution for k = 0).  2^e(T) is T
+// with its mantissa cleared, so the outer product is scale * ulp(T) / 2,
+// exact.  The inner fma is exact near the threshold: d and scale * T are
+// multiples of ulp(scale) / 2 for k >= 1 and of ulp(scale) * 2^-25 for k = 0,
+// so a difference of a few scale * ulp(T) fits in 24 bits; further away
+// |d - scale * T| dwarfs the outer term and rounding keeps its sign.  Either
+// way y has the sign of the exact d - scale * (T_k - ulp(T_k) / 2).
+//
+// k comes from v = d * rcp(scale) (v_rcp_f32, 1 ulp): v is within 5e-6 of q,
+// so floor(v) is floor(q) or one off it next to an integer, where the test
+// above, made against the neighbouring T, gives the same code.  T_k is one
+// add: k + pred(0.5) rounds to k + 0.5 for k >= 1.  v >= 0 and q < 15.5 keep
+// the codes in 0..15 with no clamp.  v_cvt_pk_u8_f32 drops each code into a
+// byte (even codes of the word in one register, odd codes in another) and a
+// single shift-or interleaves the nibbles.
 __device__ __forceinline__ uint32_t kivi_pack_word(const float (&x)[8], float mn, float scale) {
   const float rcp = __builtin_amdgcn_rcpf(scale);
+  const float s24 = scale * 0x1p-24f;
   uint32_t ev = 0, od = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float v = (x[i] - mn) * rcp;
-    float r = __builtin_rintf(v);
-    if (__builtin_expect(!(fabsf(v - r) <= 0.49999f), 0))
-      r = static_cast<float>(kivi_quantize(x[i], mn, scale));
+    const float d = x[i] - mn;
+    const float k = __builtin_floorf(d * rcp);
+    const float t = k + 0x1.fffffep-2f;
+    const float e = __int_as_float(__float_as_int(t) & 0x7f800000);
+    const float y = __builtin_fmaf(s24, e, __builtin_fmaf(-scale, t, d));
+    const float r = y >= 0.0f ? k + 1.0f : k;
     if (i % 2 == 0)
       ev = __builtin_amdgcn_cvt_pk_u8_f32(r, i / 2, ev);
     else
