@@ -179,3 +179,18 @@ def test_fma32_emulation_rounds_once():
     for i in range(n):
         want = _round32_exact(Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i])))
         assert got[i] == want, (a[i], b[i], c[i])
+
+
+def test_group_scale_division_by_15_is_exact_for_every_mantissa():
+    # kivi_group_scale: q0 = x * RN(1/15); q = fma(fma(-q0, 15, x), RN(1/15), q0)
+    # must equal IEEE x / 15 (the reference's (mx - mn) / 15) for all of a
+    # binade's 2^23 mantissas; powers of two scale every step exactly
+    x = ((np.uint32(127) << 23) | np.arange(2**23, dtype=np.uint32)).view(F)
+    rcp15 = F(1) / F(15)
+    for shift in (0, 1, 3):
+        xs = (x * F(2.0**shift)).astype(F)
+        q0 = (xs * rcp15).astype(F)
+        q = _fma32(_fma32(-q0, F(15), xs), rcp15, q0)
+        assert (q == (xs / F(15)).astype(F)).all()
+    # a planted mistake (no remainder step) does not pass
+    assert ((x * rcp15).astype(F) != (x / F(15)).astype(F)).any()

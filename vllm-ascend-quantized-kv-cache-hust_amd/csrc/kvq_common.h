@@ -127,8 +127,16 @@ __device__ __forceinline__ void store8_nt(f16* p, const float (&x)[8]) {
 }
 
 // KIVI group scale: max((mx - mn) / 15, 1e-6); the floor applies to the scale.
+// The quotient is correctly rounded without a division: q0 = x * RN(1/15),
+// then one remainder step r = fma(-q0, 15, x) (exact), q = fma(r, RN(1/15), q0).
+// Checked against IEEE x / 15 for every mantissa of a binade; every step scales
+// by powers of two, so that covers every normal x, and an x small enough for
+// subnormal steps gives a quotient far under the 1e-6 floor either way.
 __device__ __forceinline__ float kivi_group_scale(float mn, float mx) {
-  const float s = (mx - mn) / 15.0f;
+  constexpr float kRcp15 = 1.0f / 15.0f;
+  const float x = mx - mn;
+  const float q0 = x * kRcp15;
+  const float s = __builtin_fmaf(__builtin_fmaf(-q0, 15.0f, x), kRcp15, q0);
   return s < 1.0e-6f ? 1.0e-6f : s;
 }
 
