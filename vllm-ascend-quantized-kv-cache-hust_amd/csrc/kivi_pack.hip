@@ -3,8 +3,8 @@
 //
 // Key pack  (reference: pkg/ops/triton/kivi_pack.py:134-226)
 //   Head size 128 with G in {64, 128} and 16-bit input: the register form
-//   below (kivi_pack_key_wave_kernel), one wave per group, head and half of
-//   the dims.  Other geometries: one workgroup per (token group, kv head).
+//   below (kivi_pack_key_wave_kernel), one wave per group, head and quarter
+//   (G = 128) or half (G = 64) of the dims.  Other geometries: one workgroup per (token group, kv head).
 //   Thread (tc, dv) owns an 8x8
 //   tile: 8 consecutive tokens x 8 consecutive dims, read as 8 16-byte rows
 //   (16 lanes cover one 256-byte head row, fully coalesced).  Per-dim min/max
@@ -127,13 +127,15 @@ kivi_pack_key_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __restri
 }
 
 // Key pack, register form (head size 128, G in {64, 128}, 16-bit input): one
-// wave per (token group, kv head, half of the head dims).  Lane (tg, dl) holds
-// G/8 consecutive tokens (token group tg of 8) x 8 consecutive dims (dl of 8)
-// as raw 16-byte rows -- each load instruction reads 8 whole 128-byte
-// half-rows -- so the per-dim min/max is a register pass plus a three-step
-// butterfly over tg, and every output word (8 consecutive tokens of one dim)
-// is built from one lane's own registers.  No LDS, no barrier; the whole
-// group's input stays in 64 VGPRs.
+// wave per (token group, kv head, part of the head dims).  Lane (tg, dl) holds
+// consecutive tokens (token group tg) x 8 consecutive dims (dl) as raw 16-byte
+// rows -- each load instruction reads whole 64- or 128-byte row parts -- so
+// the per-dim min/max is a register pass plus a butterfly over tg, and every
+// output word (8 consecutive tokens of one dim) is built from one lane's own
+// registers.  No LDS, no barrier; the wave's share of the group stays in
+// registers.  Quarters at G = 128 give each lane 8 rows instead of 16: twice
+// the waves, so a SIMD's waves reach their arithmetic at staggered times
+// instead of all waiting on 16 loads.
 template <typename T>
 __device__ __forceinline__ void unpack8(const uint4& v, float (&x)[8]);
 template <>
@@ -153,26 +155,31 @@ __device__ __forceinline__ void unpack8<f16>(const uint4& v, float (&x)[8]) {
   for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(h[i]);
 }
 
-// Unit u = ((group * kvh) + head) * 2 + half; the whole wave calls it.
-template <typename T, typename I, int G>
+// Unit u = ((group * kvh) + head) * P + part, P = 16 / DL parts of 8 * DL dims
+// each; the whole wave calls it.  Lane (tg, dl) holds 8 dims of G * DL / 64
+// tokens: DL = 8 gives halves of the head (16 rows per lane at G = 128), DL = 4
+// quarters (8 rows per lane), twice the waves with half the loads each.
+template <typename T, typename I, int G, int DL = 8>
 __device__ __forceinline__ void key_pack_wave(const T* src_a, int64_t n_a, const T* src_b,
                                               const int64_t* __restrict__ src_index,
                                               const I* __restrict__ slots, int64_t u, int lane,
                                               int kvh, int bs, int32_t* __restrict__ kq,
                                               float* __restrict__ ks, float* __restrict__ km) {
   constexpr int D = 128;
-  constexpr int TPL = G / 8;  // tokens per lane
-  const int hf = static_cast<int>(u & 1);
-  const int h = static_cast<int>((u >> 1) % kvh);
-  const int64_t t0 = (u >> 1) / kvh * G;
+  constexpr int P = 16 / DL;
+  constexpr int TPL = G * DL / 64;  // tokens per lane
+  static_assert((DL == 4 || DL == 8) && TPL % 8 == 0, "whole words per lane");
+  const int part = static_cast<int>(u % P);
+  const int h = static_cast<int>((u / P) % kvh);
+  const int64_t t0 = (u / P) / kvh * G;
   const int64_t first = ld_index(slots, t0);
   if (first < 0) return;  // uniform across the wave
   const int64_t blk = first / bs;
   const int off = static_cast<int>(first - blk * bs);
-  const int dl = lane & 7;
-  const int tg = lane >> 3;
+  const int dl = lane % DL;
+  const int tg = lane / DL;
   const int64_t row_elems = static_cast<int64_t>(kvh) * D;
-  const int col = h * D + hf * 64 + 8 * dl;
+  const int col = h * D + part * (8 * DL) + 8 * dl;
 
   uint4 raw[TPL];
 #pragma unroll
@@ -197,9 +204,13 @@ __device__ __forceinline__ void key_pack_wave(const T* src_a, int64_t n_a, const
       }
     }
   }
-  // the 8 token groups of a dim are lanes dl + 8*tg: combine over tg
+  // the token groups of a dim are lanes dl + DL*tg: combine over tg
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
+    if constexpr (DL == 4) {
+      mn[j] = fmin_ordered(mn[j], lane_xor<4>(mn[j]));
+      mx[j] = fmax_ordered(mx[j], lane_xor<4>(mx[j]));
+    }
     mn[j] = fmin_ordered(mn[j], lane_xor<8>(mn[j]));
     mx[j] = fmax_ordered(mx[j], lane_xor<8>(mx[j]));
     mn[j] = fmin_ordered(mn[j], lane_xor<16>(mn[j]));
@@ -211,7 +222,7 @@ __device__ __forceinline__ void key_pack_wave(const T* src_a, int64_t n_a, const
 #pragma unroll
   for (int j = 0; j < 8; ++j) sc[j] = kivi_group_scale(mn[j], mx[j]);
 
-  const int64_t row_base = (blk * kvh + h) * static_cast<int64_t>(D) + hf * 64 + 8 * dl;
+  const int64_t row_base = (blk * kvh + h) * static_cast<int64_t>(D) + part * (8 * DL) + 8 * dl;
   const int wpd = bs / 8;
   uint32_t* out = reinterpret_cast<uint32_t*>(kq);
 #pragma unroll
@@ -248,7 +259,7 @@ __device__ __forceinline__ void key_pack_wave(const T* src_a, int64_t n_a, const
   }
 }
 
-template <typename T, typename I, int G>
+template <typename T, typename I, int G, int DL>
 __global__ void __launch_bounds__(256)
 kivi_pack_key_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __restrict__ src_b,
                           const int64_t* __restrict__ src_index, const I* __restrict__ slots,
@@ -256,8 +267,8 @@ kivi_pack_key_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* __r
                           float* __restrict__ ks, float* __restrict__ km) {
   const int64_t u = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (u >= units) return;  // whole wave
-  key_pack_wave<T, I, G>(src_a, n_a, src_b, src_index, slots, u, threadIdx.x & 63, kvh, bs, kq,
-                         ks, km);
+  key_pack_wave<T, I, G, DL>(src_a, n_a, src_b, src_index, slots, u, threadIdx.x & 63, kvh, bs,
+                             kq, ks, km);
 }
 
 template <typename T, typename I>
@@ -575,13 +586,15 @@ extern "C" int kvq_kivi_pack_key(const void* src_a, int64_t n_a, const void* src
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (head_size == 128 && (group_size == 64 || group_size == 128) &&
       (src_dtype == KVQ_DTYPE_BF16 || src_dtype == KVQ_DTYPE_F16)) {
-    // register form: one wave per (token group, head, half of the dims)
-    const int64_t units = num_tokens / group_size * num_kv_heads * 2;
+    // register form: one wave per (token group, head, part of the dims):
+    // quarters at G = 128 (8 rows per lane), halves at G = 64
+    const int parts = group_size == 128 ? 4 : 2;
+    const int64_t units = num_tokens / group_size * num_kv_heads * parts;
     const int64_t blocks = (units + 3) / 4;
     if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
 #define KVQ_LAUNCH_KEY_WAVE(T, GG)                                                            \
   KVQ_DISPATCH_INDEX(slot_index_type, I,                                                      \
-    hipLaunchKernelGGL((kivi_pack_key_wave_kernel<T, I, GG>),                                 \
+    hipLaunchKernelGGL((kivi_pack_key_wave_kernel<T, I, GG, GG == 128 ? 4 : 8>),               \
                        dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s,                  \
                        static_cast<const T*>(src_a), n_a, static_cast<const T*>(src_b),       \
                        src_index, static_cast<const I*>(slot_mapping), units, num_kv_heads,   \
