@@ -21,16 +21,17 @@ How each function is pinned (checked by ``tests/test_oracle.py``):
   restatement (bit-exact, element by element), the round trip against
   ``fake_quant_key``/``fake_quant_value`` (``tests/test_kivi_int4.py:561-632``),
   and hand-computed words for a tiny input.
-* ``int8_calc_scales`` / ``int8_quantize`` / ``int8_dequantize`` -- the C
+* ``int8_calc_scales`` / ``int8_quantize`` / ``int8_paged_dequant`` -- the C
   restatement with explicit bf16 round-to-nearest-even, closed forms
-  (``inv = 127/amax``), and golden vectors written by the reference's own
-  ``Int8DynamicSemantics`` (``tests/golden/``).
+  (``inv = 127/amax``), round-half-even known answers, and every positive
+  bf16 amax against the two-step ``bf16(bf16(1/amax)*127)``, which differs
+  from a single rounded division on some of them.
 * ``attention`` -- textbook softmax attention; checked against a float64
   brute-force loop and against ``torch.nn.functional.scaled_dot_product_attention``.
 * ``KiviWindowModel`` -- closed forms of the incremental rule
   (``hist_k = ((L-1)//R)*R``, ``hist_v = max(0, L-R)``;
-  ``tests/test_kivi_int4.py:1730-1734``) and golden traces written by the
-  reference mixin (``tests/golden/``).
+  ``tests/test_kivi_int4.py:1730-1734``), overwrite-without-eviction, FIFO
+  value eviction and the bulk-prefill flush.
 """
 
 from __future__ import annotations

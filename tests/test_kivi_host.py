@@ -426,6 +426,36 @@ def test_misaligned_window_flush_fails_closed_before_any_launch():
     assert impl.calls["key_pack"] == []
 
 
+def test_rejected_batch_leaves_every_mirror_unchanged():
+    """A batch whose second request fails its key flush launches nothing, and
+    the first request's window (and the row a new request took) roll back."""
+    impl = _make_impl(max_seqs=3)
+    kv = torch.randn(2 * GROUP, KVH, HEAD)
+    impl._write_kivi_cache(kv[:1], kv[:1], torch.tensor([40]), ["a"], [1])
+    # an unaligned full window for "b": its next token must flush slots 3..18
+    impl._write_kivi_cache(kv, kv, torch.arange(3, 3 + 2 * GROUP), ["b"], [2 * GROUP])
+    ring = impl._kivi_ring
+
+    def snapshot():
+        return (dict(impl.kivi_residual_req_to_row), list(impl.kivi_residual_free_rows),
+                {k: [list(x) for x in v] for k, v in ring.lane_slot.items()},
+                {k: list(v) for k, v in ring.start.items()},
+                {k: list(v) for k, v in ring.length.items()})
+
+    before = snapshot()
+    launches = {k: len(v) for k, v in impl.calls.items()}
+    batch = torch.randn(3, KVH, HEAD)
+    with pytest.raises(RuntimeError, match="aligned token groups"):
+        impl._write_kivi_cache(batch, batch, torch.tensor([41, 60, 3 + 2 * GROUP]),
+                               ["a", "c", "b"], [1, 2, 3])
+    assert snapshot() == before
+    assert {k: len(v) for k, v in impl.calls.items()} == launches
+    # the rolled-back mirror still plans the next good step from the old state
+    impl._write_kivi_cache(batch[:1], batch[:1], torch.tensor([41]), ["a"], [1])
+    row = impl._get_kivi_residual_row("a", create=False)
+    assert ring.window_slots(row, is_key=True) == [40, 41]
+
+
 def test_aligned_key_flush_reaches_kernel_hook():
     impl = _make_impl()
     key = torch.randn(GROUP, KVH, HEAD)

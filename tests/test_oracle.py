@@ -255,6 +255,21 @@ def test_int8_scales_closed_form_fp32():
     assert torch.equal(k_aq, 1.0 / k_inv)
 
 
+def test_int8_scales_two_rounding_steps_over_every_bf16_amax():
+    """``127.0 / amax`` in bf16 is reciprocal then multiply, each rounded to
+    bf16 (torch's ``__rdiv__``); a single rounded division differs on some
+    amax values, so this pins the order of the two roundings."""
+    bits = torch.arange(0x2B8D, 0x7F80, dtype=torch.int32).to(torch.int16)  # bf16(1e-12) .. inf
+    amax = bits.view(torch.bfloat16)
+    x = torch.stack([amax, -amax])  # one channel per amax value
+    k_inv, _, k_aq, _ = ref.int8_calc_scales(x, x)
+    two_step = (amax.float().reciprocal().to(torch.bfloat16).float() * 127).to(torch.bfloat16)
+    one_step = (127.0 / amax.float()).to(torch.bfloat16)
+    assert torch.equal(k_inv.flatten(), two_step)
+    assert not torch.equal(two_step, one_step)
+    assert torch.equal(k_aq.flatten(), (1.0 / two_step.float()).to(torch.bfloat16))
+
+
 def test_int8_paged_dequant_brute_force():
     g = torch.Generator().manual_seed(6)
     nb, bs, kvh, d = 5, 4, 2, 8

@@ -17,6 +17,7 @@ closed with the reference's messages.  What changes is where the work runs:
 
 from __future__ import annotations
 
+from contextlib import contextmanager
 from typing import Any
 
 import torch
@@ -288,6 +289,25 @@ class AscendKiviInt4AttentionBackendMixin:
     # window writes (ab.py:377-462, 562-674)
     # ------------------------------------------------------------------
 
+    @contextmanager
+    def _kivi_planning(self):
+        """All-or-nothing planning of one store batch.
+
+        When planning or launching raises, the ring mirror rows touched by
+        the batch get their old state back and rows the batch created are
+        released, so a caller that survives the error still sees the state
+        the device holds.
+        """
+        ring = self._ensure_kivi_residual_buffers()
+        before = set(self.kivi_residual_req_to_row)
+        try:
+            with ring.transaction():
+                yield ring
+        except BaseException:
+            for key in set(self.kivi_residual_req_to_row) - before:
+                self._release_kivi_residual_row(key)
+            raise
+
     def _execute_kivi_plan(self, plan: StorePlan, key: Any, value: Any) -> None:
         if plan.empty():
             return
@@ -325,25 +345,28 @@ class AscendKiviInt4AttentionBackendMixin:
         if values.numel() == 0 or slots.numel() == 0:
             return
         self._adopt_ring_dtype(values)
-        row = self._get_kivi_residual_row(req_key, create=True)
-        plan = StorePlan()
         slot_list = _host_list(slots)
-        self._kivi_ring.plan_store(
-            plan, row, slot_list, list(range(len(slot_list))), is_key=is_key,
-            block_size=self._get_kivi_block_size(), group_size=self.kivi_group_size,
-        )
-        self._execute_kivi_plan(plan, values if is_key else None, None if is_key else values)
+        with self._kivi_planning() as ring:
+            row = self._get_kivi_residual_row(req_key, create=True)
+            plan = StorePlan()
+            ring.plan_store(
+                plan, row, slot_list, list(range(len(slot_list))), is_key=is_key,
+                block_size=self._get_kivi_block_size(), group_size=self.kivi_group_size,
+            )
+            self._execute_kivi_plan(plan, values if is_key else None,
+                                    None if is_key else values)
 
     def _flush_kivi_residual_prefix(self, req_key: str, *, is_key: bool, count: int) -> None:
         row = self._get_kivi_residual_row(req_key, create=False)
         if row is None:
             return
-        plan = StorePlan()
-        self._kivi_ring.flush_prefix(
-            plan, row, count, is_key=is_key, block_size=self._get_kivi_block_size(),
-            group_size=self.kivi_group_size,
-        )
-        self._execute_kivi_plan(plan, None, None)
+        with self._kivi_planning() as ring:
+            plan = StorePlan()
+            ring.flush_prefix(
+                plan, row, count, is_key=is_key, block_size=self._get_kivi_block_size(),
+                group_size=self.kivi_group_size,
+            )
+            self._execute_kivi_plan(plan, None, None)
 
     def _request_spans(self, slot_mapping: Any, actual_seq_qlen: Any
                        ) -> tuple[list[tuple[int, int]], int]:
@@ -379,20 +402,21 @@ class AscendKiviInt4AttentionBackendMixin:
         slots = _host_list(slot_mapping)
         keys = self._get_kivi_req_keys(req_ids, num_reqs)
         bs, g = self._get_kivi_block_size(), self.kivi_group_size
-        plan = StorePlan()
-        for i, (start, end) in enumerate(spans):
-            if end <= start:
-                continue
-            rows = [t for t in range(start, end) if slots[t] >= 0]
-            if not rows:
-                continue
-            row = self._get_kivi_residual_row(keys[i], create=True)
-            req_slots = [slots[t] for t in rows]
-            self._kivi_ring.plan_store(plan, row, req_slots, rows, is_key=True,
-                                       block_size=bs, group_size=g)
-            self._kivi_ring.plan_store(plan, row, req_slots, rows, is_key=False,
-                                       block_size=bs, group_size=g)
-        self._execute_kivi_plan(plan, key, value)
+        with self._kivi_planning() as ring:
+            plan = StorePlan()
+            for i, (start, end) in enumerate(spans):
+                if end <= start:
+                    continue
+                rows = [t for t in range(start, end) if slots[t] >= 0]
+                if not rows:
+                    continue
+                row = self._get_kivi_residual_row(keys[i], create=True)
+                req_slots = [slots[t] for t in rows]
+                ring.plan_store(plan, row, req_slots, rows, is_key=True,
+                                block_size=bs, group_size=g)
+                ring.plan_store(plan, row, req_slots, rows, is_key=False,
+                                block_size=bs, group_size=g)
+            self._execute_kivi_plan(plan, key, value)
 
     def _write_kivi_prefill_cache(
         self, key: Any, value: Any, slot_mapping: Any, req_ids: list[str] | None,
@@ -415,28 +439,29 @@ class AscendKiviInt4AttentionBackendMixin:
         ring = self._ensure_kivi_residual_buffers()
         na = ring.rows * ring.ring_len
         self._adopt_ring_dtype(key, value)
-        plan = StorePlan()
-        for i, (start, end) in enumerate(spans):
-            if end <= start:
-                continue
-            rows = [t for t in range(start, end) if slots[t] >= 0]
-            if not rows:
-                continue
-            flush = (len(rows) // r) * r
-            if flush:
-                self._check_key_flush(key, [slots[t] for t in rows[:flush]])
-                for side in (plan.key, plan.value):
-                    side.pack_src.extend(na + t for t in rows[:flush])
-                    side.pack_slots.extend(slots[t] for t in rows[:flush])
-            if flush < len(rows):
-                row = self._get_kivi_residual_row(keys[i], create=True)
-                rest = rows[flush:]
-                rest_slots = [slots[t] for t in rest]
-                ring.plan_store(plan, row, rest_slots, rest, is_key=True, block_size=bs,
-                                group_size=g)
-                ring.plan_store(plan, row, rest_slots, rest, is_key=False, block_size=bs,
-                                group_size=g)
-        self._execute_kivi_plan(plan, key, value)
+        with self._kivi_planning():
+            plan = StorePlan()
+            for i, (start, end) in enumerate(spans):
+                if end <= start:
+                    continue
+                rows = [t for t in range(start, end) if slots[t] >= 0]
+                if not rows:
+                    continue
+                flush = (len(rows) // r) * r
+                if flush:
+                    self._check_key_flush(key, [slots[t] for t in rows[:flush]])
+                    for side in (plan.key, plan.value):
+                        side.pack_src.extend(na + t for t in rows[:flush])
+                        side.pack_slots.extend(slots[t] for t in rows[:flush])
+                if flush < len(rows):
+                    row = self._get_kivi_residual_row(keys[i], create=True)
+                    rest = rows[flush:]
+                    rest_slots = [slots[t] for t in rest]
+                    ring.plan_store(plan, row, rest_slots, rest, is_key=True, block_size=bs,
+                                    group_size=g)
+                    ring.plan_store(plan, row, rest_slots, rest, is_key=False, block_size=bs,
+                                    group_size=g)
+            self._execute_kivi_plan(plan, key, value)
 
     def _check_key_flush(self, key: Any, slots: list[int]) -> None:
         """Validation of a key flush before any launch (``ab.py:676-726``)."""

@@ -27,6 +27,7 @@ that reads every old lane before it is overwritten.
 
 from __future__ import annotations
 
+from contextlib import contextmanager
 from dataclasses import dataclass, field
 
 import torch
@@ -112,6 +113,47 @@ class KiviResidualRing:
             True: [dict() for _ in range(rows)],
             False: [dict() for _ in range(rows)],
         }
+        self._saved: dict[int, tuple] | None = None
+
+    # -- all-or-nothing planning ----------------------------------------------
+
+    @contextmanager
+    def transaction(self):
+        """Undo the mirror changes made inside the block when it raises.
+
+        A batch is planned request by request, and every request updates the
+        mirror as it goes; the launches come after the whole batch is planned.
+        When a later request is rejected (an unaligned key flush), nothing is
+        launched, so the earlier requests' mirror changes are rolled back too
+        and the mirror keeps describing what the device holds.
+        """
+        if self._saved is not None:  # nested: the outer block restores
+            yield
+            return
+        self._saved = {}
+        try:
+            yield
+        except BaseException:
+            for row, state in self._saved.items():
+                self._restore(row, state)
+            raise
+        finally:
+            self._saved = None
+
+    def _touch(self, row: int) -> None:
+        if self._saved is not None and row not in self._saved:
+            self._saved[row] = tuple(
+                (self.start[k][row], self.length[k][row], list(self.lane_slot[k][row]),
+                 dict(self.slot_lane[k][row]))
+                for k in (True, False)
+            )
+
+    def _restore(self, row: int, state: tuple) -> None:
+        for k, (start, length, ls, sl) in zip((True, False), state):
+            self.start[k][row] = start
+            self.length[k][row] = length
+            self.lane_slot[k][row] = ls
+            self.slot_lane[k][row] = sl
 
     # -- dtype ----------------------------------------------------------------
 
@@ -167,6 +209,7 @@ class KiviResidualRing:
     # -- mutation ----------------------------------------------------------
 
     def reset_row(self, row: int) -> None:
+        self._touch(row)
         for is_key in (True, False):
             self.start[is_key][row] = 0
             self.length[is_key][row] = 0
@@ -180,6 +223,7 @@ class KiviResidualRing:
         (the reference rewrites the kept entries from lane 0 on,
         ``attention_backend.py:328-356``).
         """
+        self._touch(row)
         lanes = self.lanes(row, is_key=is_key)
         ls = self.lane_slot[is_key][row]
         kept = [lane for lane in lanes if ls[lane] in keep_slots]
@@ -213,6 +257,7 @@ class KiviResidualRing:
         ``plan``; raises before any launch if a key flush would break the
         pack kernel's aligned-group contract.
         """
+        self._touch(row)
         side = plan.side(is_key)
         r = self.ring_len
         cap = self.window
@@ -263,6 +308,7 @@ class KiviResidualRing:
     def flush_prefix(self, plan: StorePlan, row: int, count: int, *, is_key: bool,
                      block_size: int, group_size: int) -> None:
         """Move the ``count`` oldest entries of a window to int4 history."""
+        self._touch(row)
         n = self.length[is_key][row]
         count = min(count, n)
         if count <= 0:
