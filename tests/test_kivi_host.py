@@ -274,6 +274,58 @@ def test_single_token_steps_plan_one_launch():
     assert seen["kp"] > 0 and seen["vp"] > 0
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_closed_form_run_plan_equals_token_replay(seed):
+    """``_plan_run`` (a run of new slots in closed form) leaves the same mirror
+    and emits the same plan as the per-token replay, over random run lengths
+    (shorter and longer than the window, several windows at once), starting
+    from windows of every fill level, several runs into one plan, and an
+    unaligned key window that both reject."""
+    from vllm_ascend_quantized_kv_cache.methods.kivi_int4.residual import (
+        KiviResidualRing,
+        StorePlan,
+    )
+
+    rng = random.Random(seed)
+    group = rng.choice([8, 16])
+    window = group * rng.choice([1, 2])
+    block = max(window, group) * rng.choice([1, 2])
+    rows = 3
+    rings = [KiviResidualRing(rows, window, 1, 8, device="cpu") for _ in range(2)]
+    pos = [0] * rows
+    base = [(rng.randrange(0, 4) + 64 * r) * block for r in range(rows)]
+
+    def state(ring):
+        return (ring.start, ring.length, ring.lane_slot, ring.slot_lane)
+
+    for _step in range(12):
+        plans = [StorePlan(), StorePlan()]
+        for _ in range(rng.randrange(1, 4)):
+            row = rng.randrange(rows)
+            n = rng.choice([2, 3, window - 1, window, window + 1, 3 * window + 5])
+            n = max(2, n)
+            slots = list(range(base[row] + pos[row], base[row] + pos[row] + n))
+            inputs = [rng.randrange(0, 500) for _ in range(n)]
+            for is_key in (True, False):
+                rings[0]._plan_run(plans[0], row, slots, inputs, is_key=is_key,
+                                   block_size=block, group_size=group)
+                rings[1]._plan_tokens(plans[1], row, slots, inputs, is_key=is_key,
+                                      block_size=block, group_size=group)
+            pos[row] += n
+        assert state(rings[0]) == state(rings[1])
+        for a, b in ((plans[0].key, plans[1].key), (plans[0].value, plans[1].value)):
+            assert a.pack_src == b.pack_src and a.pack_slots == b.pack_slots
+            assert a.ring == b.ring and a.lane_src == b.lane_src
+    # a key window that starts off a group boundary is rejected by both
+    row = 0
+    ring_a, ring_b = (KiviResidualRing(1, window, 1, 8, device="cpu") for _ in range(2))
+    slots = list(range(3, 3 + window + 1))
+    for ring, fn in ((ring_a, ring_a._plan_run), (ring_b, ring_b._plan_tokens)):
+        with pytest.raises(RuntimeError, match="aligned token groups"):
+            fn(StorePlan(), row, slots, list(range(len(slots))), is_key=True,
+               block_size=block, group_size=group)
+
+
 def test_multi_token_batch_that_reuses_a_packed_lane_is_not_one_launch():
     """Two tokens into a full value window: the second lands on the lane the
     first evicted and packed, so the plan must keep packs before ring writes."""

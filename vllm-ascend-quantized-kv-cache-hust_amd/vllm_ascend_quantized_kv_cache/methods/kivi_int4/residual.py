@@ -256,8 +256,75 @@ class KiviResidualRing:
         slot ``slots[i]``.  Updates the mirror and appends the device work to
         ``plan``; raises before any launch if a key flush would break the
         pack kernel's aligned-group contract.
+
+        A run of distinct slots none of which the window holds (a prompt
+        chunk, a decode token) is planned in closed form (``_plan_run``);
+        anything else replays token by token (``_plan_tokens``).  Both give
+        the same plan and mirror.
         """
         self._touch(row)
+        if len(slots) > 1 and self.slot_lane[is_key][row].keys().isdisjoint(slots) \
+                and len(set(slots)) == len(slots):
+            self._plan_run(plan, row, slots, input_rows, is_key=is_key,
+                           block_size=block_size, group_size=group_size)
+        else:
+            self._plan_tokens(plan, row, slots, input_rows, is_key=is_key,
+                              block_size=block_size, group_size=group_size)
+
+    def _plan_run(self, plan: StorePlan, row: int, slots: list[int], input_rows: list[int], *,
+                  is_key: bool, block_size: int, group_size: int) -> None:
+        """``plan_store`` for new, distinct slots without a per-token walk.
+
+        With ``l0`` entries in the window and ``n`` new ones, the per-token
+        rules evict ``((l0 + n - 1) // R) * R`` entries on the key side (whole
+        windows) and ``max(0, l0 + n - R)`` on the value side (one per token
+        past a full window), oldest first; every eviction moves the start one
+        lane per evicted entry, and the survivors stay contiguous from the
+        start.  New tokens evicted inside the run are packed straight from the
+        input and never written to the ring.
+        """
+        side = plan.side(is_key)
+        r, cap = self.ring_len, self.window
+        na, base = self.rows * r, row * r
+        ls = self.lane_slot[is_key][row]
+        sl = self.slot_lane[is_key][row]
+        n = len(slots)
+        s0, l0 = self.start[is_key][row], self.length[is_key][row]
+        evict = ((l0 + n - 1) // cap) * cap if is_key else max(0, l0 + n - cap)
+        ev_old = [(s0 + j) % r for j in range(min(evict, l0))]
+        ev_new = evict - len(ev_old)
+        if evict:
+            ev_slots = [ls[lane] for lane in ev_old] + list(slots[:ev_new])
+            if is_key:
+                for w in range(0, evict, cap):
+                    if key_slot_groups_error(ev_slots[w:w + cap], block_size=block_size,
+                                             group_size=group_size) is not None:
+                        raise RuntimeError(
+                            "KIVI key flush requires contiguous aligned token groups."
+                        )
+            side.pack_src.extend(side.lane_src.get(base + lane, base + lane) for lane in ev_old)
+            side.pack_src.extend(na + irow for irow in input_rows[:ev_new])
+            side.pack_slots.extend(ev_slots)
+            for lane in ev_old:
+                sl.pop(ls[lane], None)
+                ls[lane] = -1
+                side.ring.pop(base + lane, None)
+                side.lane_src.pop(base + lane, None)
+        start = (s0 + evict) % r
+        kept_old = l0 - len(ev_old)
+        for j in range(ev_new, n):
+            lane = (start + kept_old + j - ev_new) % r
+            slot, irow = slots[j], input_rows[j]
+            ls[lane] = slot
+            sl[slot] = lane
+            side.lane_src[base + lane] = na + irow
+            side.ring[base + lane] = irow
+        self.start[is_key][row] = start
+        self.length[is_key][row] = kept_old + n - ev_new
+
+    def _plan_tokens(self, plan: StorePlan, row: int, slots: list[int], input_rows: list[int],
+                     *, is_key: bool, block_size: int, group_size: int) -> None:
+        """``plan_store`` token by token: the reference's loop (``ab.py:411-462``)."""
         side = plan.side(is_key)
         r = self.ring_len
         cap = self.window
