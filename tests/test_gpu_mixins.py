@@ -27,6 +27,7 @@ from vllm_ascend_quantized_kv_cache.methods.int8_dynamic.attention_backend impor
     AscendInt8AttentionBackendMixin,
 )
 from vllm_ascend_quantized_kv_cache.methods.kivi_int4 import attention_backend as ab
+from vllm_ascend_quantized_kv_cache.methods.kivi_int4.byte_cache import KiviByteCacheLayout
 
 pytestmark = pytest.mark.gpu
 
@@ -44,16 +45,12 @@ def _make_kivi(device, *, head, kvh, hq, group, residual, block, num_blocks, row
     impl.enable_kivi = True
     impl.kivi_group_size, impl.kivi_residual_length = group, residual
     impl.kivi_max_num_seqs = rows
-    z = dict(device=device)
-    caches = (
-        torch.zeros(num_blocks, kvh, head, block // 8, dtype=torch.int32, **z),
-        torch.ones(num_blocks, kvh, head, block // group, **z),
-        torch.zeros(num_blocks, kvh, head, block // group, **z),
-        torch.zeros(num_blocks, block, kvh, head // 8, dtype=torch.int32, **z),
-        torch.ones(num_blocks, block, kvh, head // group, **z),
-        torch.zeros(num_blocks, block, kvh, head // group, **z),
-    )
-    impl._bind_kivi_cache(caches)
+    # the host's form: two uint8 page buffers the mixin slices into six views
+    layout = KiviByteCacheLayout(num_blocks, block, kvh, head, group)
+    kbuf = torch.zeros((num_blocks, block, kvh, layout.bytes_per_token_head),
+                       dtype=torch.uint8, device=device)
+    impl._bind_kivi_cache((kbuf, torch.zeros_like(kbuf)))
+    assert impl.k_quant_cache.data_ptr() == kbuf.data_ptr()
     return impl
 
 
