@@ -15,7 +15,8 @@
  *   - Calls are asynchronous on `stream`, run entirely on it, and are
  *     thread-safe.  The only state the library keeps is per device: cached
  *     device limits (LDS per workgroup, resident workgroups per kernel),
- *     filled on first use.
+ *     filled on first use, and the static scratch array of
+ *     kvq_kivi_decode_attn_noalloc (with its device address).
  *
  * Reference paths are relative to /root/reference with
  * pkg/ = src/vllm_ascend_quantized_kv_cache/; each entry point names the
@@ -45,7 +46,11 @@ enum {
   KVQ_OK = 0,
   KVQ_ERR_INVALID = -1,     /* bad pointer, dtype or size */
   KVQ_ERR_GEOMETRY = -2,    /* geometry the kernels do not support */
+  KVQ_ERR_SCRATCH = -3,     /* work larger than the library's static scratch */
 };
+
+/* Size of the static device scratch behind kvq_kivi_decode_attn_noalloc. */
+#define KVQ_DECODE_SCRATCH_BYTES (32ll << 20)
 
 /* ABI version: bumped whenever a signature below changes. */
 int kvq_abi_version(void);
@@ -174,6 +179,29 @@ int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batch, int num_
                          const int32_t* pieces, int64_t num_pieces,
                          const void* ring_k, const void* ring_v, int ring_dtype, int ring_len,
                          void* workspace, void* out, void* stream);
+
+/* kvq_kivi_decode_attn without a workspace argument: the split-K partials go
+ * to a static device array of KVQ_DECODE_SCRATCH_BYTES (32 MiB) that each GPU
+ * the library runs on holds until the process ends; the call allocates
+ * nothing (no hipMalloc, no library allocation).  Work lists whose partials
+ * (kvq_kivi_decode_workspace_bytes) exceed it return KVQ_ERR_SCRATCH before
+ * anything is launched.  The stream must belong to the calling thread's
+ * current device.  Every call on one GPU shares that GPU's array and leaves
+ * the last call's partials in it: calls that overlap on one GPU (two streams,
+ * or two threads) race and must be serialized by the caller.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). */
+int kvq_kivi_decode_attn_noalloc(const void* query, int q_dtype, int64_t batch, int num_heads,
+                                 int num_kv_heads, int head_size, float scale,
+                                 const int32_t* k_quant, const float* k_scale,
+                                 const float* k_mn, const int32_t* v_quant,
+                                 const float* v_scale, const float* v_mn, int64_t num_blocks,
+                                 int block_size, int group_size, const int32_t* block_table,
+                                 int64_t max_blocks, const int32_t* seq_meta,
+                                 const int32_t* work, int64_t num_work, const int32_t* pieces,
+                                 int64_t num_pieces, const void* ring_k, const void* ring_v,
+                                 int ring_dtype, int ring_len, void* out, void* stream);
 
 /* ---- dense attention ----------------------------------------------------- */
 

@@ -20,6 +20,8 @@
 // the QK dot products lane-per-position, the PV accumulation lane-per-dim.
 // Each work item leaves (m, l, o[D]) per query head in the workspace (m in
 // the log2 domain); the combine kernel merges a request's items.
+#include <mutex>
+
 #include "kvq_common.h"
 #include "kvq_decode.h"
 
@@ -486,4 +488,64 @@ extern "C" int kvq_kivi_decode_attn(const void* query, int q_dtype, int64_t batc
   }
   return kvq::launch_decode_combine(q_dtype, batch, num_heads, head_size, seq_meta, 8, 6, ws_o,
                                     ws_ml, out, s);
+}
+
+// ---- allocation-free decode --------------------------------------------------
+// kvq_kivi_decode_attn_noalloc keeps its split-K partials in a file-scope
+// device array instead of a caller workspace.  Each device holds its own copy
+// at its own address from module load until the process ends.  Host code must
+// never pass `scratch` itself to a kernel (its host-side name is a stand-in,
+// not a device address): it uses the address hipGetSymbolAddress returns,
+// resolved once per device with that device current.
+
+namespace {
+
+__device__ __align__(256) float scratch[KVQ_DECODE_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch` (the calling thread's current device).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return KVQ_ERR_INVALID;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (!p) return KVQ_ERR_INVALID;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KVQ_OK;
+}
+
+}  // namespace
+
+extern "C" int kvq_kivi_decode_attn_noalloc(
+    const void* query, int q_dtype, int64_t batch, int num_heads, int num_kv_heads,
+    int head_size, float scale, const int32_t* k_quant, const float* k_scale, const float* k_mn,
+    const int32_t* v_quant, const float* v_scale, const float* v_mn, int64_t num_blocks,
+    int block_size, int group_size, const int32_t* block_table, int64_t max_blocks,
+    const int32_t* seq_meta, const int32_t* work, int64_t num_work, const int32_t* pieces,
+    int64_t num_pieces, const void* ring_k, const void* ring_v, int ring_dtype, int ring_len,
+    void* out, void* stream) {
+  if (batch == 0) return KVQ_OK;
+  if (num_work <= 0 || num_heads <= 0 || head_size <= 0) return KVQ_ERR_INVALID;
+  // every partial (m, l, o) of the work list must fit the static array
+  if (num_work > KVQ_DECODE_SCRATCH_BYTES ||
+      kvq::decode_workspace_bytes(num_work, num_heads, head_size) > KVQ_DECODE_SCRATCH_BYTES)
+    return KVQ_ERR_SCRATCH;
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != KVQ_OK) return rc;
+  return kvq_kivi_decode_attn(query, q_dtype, batch, num_heads, num_kv_heads, head_size, scale,
+                              k_quant, k_scale, k_mn, v_quant, v_scale, v_mn, num_blocks,
+                              block_size, group_size, block_table, max_blocks, seq_meta, work,
+                              num_work, pieces, num_pieces, ring_k, ring_v, ring_dtype, ring_len,
+                              ws, out, stream);
 }

@@ -52,6 +52,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_P, _I, _I64, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _P, _I64,
          _P, _P, _I64, _P, _I64, _P, _P, _I, _I, _P, _P, _P],
     ),
+    "kvq_kivi_decode_attn_noalloc": (
+        _I,
+        [_P, _I, _I64, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _P, _I64,
+         _P, _P, _I64, _P, _I64, _P, _P, _I, _I, _P, _P],
+    ),
     "kvq_prefill_attn": (
         _I, [_P, _P, _P, _I, _P, _P, _I64, _I64, _I, _I, _I, _F, _I, _P, _P]
     ),
@@ -76,6 +81,9 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
 
 KVQ_ERR_INVALID = -1
 KVQ_ERR_GEOMETRY = -2
+KVQ_ERR_SCRATCH = -3
+#: static device scratch of kvq_kivi_decode_attn_noalloc (include/kvq_hip.h)
+KVQ_DECODE_SCRATCH_BYTES = 32 << 20
 
 
 def library_path() -> Path:
@@ -153,6 +161,11 @@ def check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what}: the HIP kernel rejected its arguments (invalid).")
     if rc == KVQ_ERR_GEOMETRY:
         raise RuntimeError(f"{what}: geometry not supported by the HIP kernels.")
+    if rc == KVQ_ERR_SCRATCH:
+        raise RuntimeError(
+            f"{what}: the work list needs more than the {KVQ_DECODE_SCRATCH_BYTES >> 20} MiB "
+            "static scratch; use the entry point that takes a workspace."
+        )
     raise RuntimeError(f"{what}: HIP launch failed with hipError_t {rc}.")
 
 
