@@ -365,12 +365,112 @@ def bench_kivi_decode(torch, dev, *, b, hq, kvh, d, g, r, bs, lens, steps, warmu
     return res
 
 
+def bench_kivi_forward(torch, dev, *, lens, hq, kvh, d, g, r, bs, steps, warmup, seed):
+    """Config-3 decode steps through the KIVI mixin's ``forward()``, the way a
+    host calls it: the step's metadata (device ``slot_mapping`` and block
+    table, host ``seq_lens_list``) goes in, and the mixin plans on the host,
+    copies its plans to the device and launches the store, decode and
+    combine.  Timed by the host clock around ``steps`` back-to-back steps
+    (with one synchronisation at the end), so host planning and any device
+    synchronisation inside ``forward()`` are included."""
+    from types import SimpleNamespace
+
+    from vllm_ascend_quantized_kv_cache.methods.kivi_int4 import attention_backend as ab
+    from vllm_ascend_quantized_kv_cache.methods.kivi_int4.byte_cache import KiviByteCacheLayout
+
+    class Impl(ab.AscendKiviInt4AttentionBackendMixin):
+        pass
+
+    b = len(lens)
+    total = steps + warmup
+    impl = Impl()
+    impl.num_heads, impl.num_kv_heads, impl.head_size, impl.scale = hq, kvh, d, d ** -0.5
+    impl._init_kivi_state(None)
+    impl.enable_kivi = True
+    impl.kivi_group_size, impl.kivi_residual_length, impl.kivi_max_num_seqs = g, r, b
+    nblk = [-(-(n + total) // bs) for n in lens]
+    nb = sum(nblk) + 8
+    layout = KiviByteCacheLayout(nb, bs, kvh, d, g)
+    kbuf = torch.zeros((nb, bs, kvh, layout.bytes_per_token_head), dtype=torch.uint8, device=dev)
+    vbuf = torch.zeros_like(kbuf)
+    kv_cache = (kbuf, vbuf)
+    impl._bind_kivi_cache(kv_cache)
+    gen = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(nb, generator=gen)
+    table = torch.zeros((b, max(nblk)), dtype=torch.int64)
+    used = 0
+    for i, n in enumerate(nblk):
+        table[i, :n] = perm[used:used + n]
+        used += n
+    key_scales = torch.exp(torch.randn((kvh, d), generator=gen)).to(dev)
+    gdev = torch.Generator(device=dev).manual_seed(seed + 1)
+    reqs = [f"req{i}" for i in range(b)]
+    pos = torch.arange(max(lens) + total)
+
+    def slots(i, p0, p1):
+        return table[i][pos[p0:p1] // bs] * bs + pos[p0:p1] % bs
+
+    for i, n in enumerate(lens):
+        k = (torch.randn((n, kvh, d), generator=gdev, device=dev) * key_scales).to(torch.bfloat16)
+        v = torch.randn((n, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
+        impl._write_kivi_cache(k, v, slots(i, 0, n).to(dev), [reqs[i]], [n])
+    table_dev = table.to(dev)
+    new_k = (torch.randn((total, b, kvh, d), generator=gdev, device=dev)
+             * key_scales).to(torch.bfloat16)
+    new_v = torch.randn((total, b, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
+    qs = torch.randn((total, b, hq, d), generator=gdev, device=dev).to(torch.bfloat16)
+    out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=dev)
+    mds = []
+    cur = list(lens)
+    for _ in range(total):
+        sm = torch.stack([slots(i, n, n + 1)[0] for i, n in enumerate(cur)]).to(dev)
+        cur = [n + 1 for n in cur]
+        mds.append(SimpleNamespace(attn_state=SimpleNamespace(name="DecodeOnly"), causal=True,
+                                   finished_req_ids=None, seq_lens_list=list(cur),
+                                   slot_mapping=sm, block_tables=table_dev, req_ids=reqs,
+                                   num_actual_tokens=b))
+    torch.cuda.synchronize()
+
+    def step(j):
+        impl.forward(None, qs[j], new_k[j], new_v[j], kv_cache, mds[j], out)
+
+    for j in range(warmup):
+        step(j)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for j in range(warmup, total):
+        step(j)
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / steps * 1e6
+    del impl, kbuf, vbuf, new_k, new_v, qs
+    torch.cuda.empty_cache()
+    return {"us_per_step": us}
+
+
+def cpu_info() -> dict:
+    """Cores this process may run on and the CPU model (from /proc/cpuinfo)."""
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cores": cores, "os_cpu_count": os.cpu_count(), "cpu_model": model}
+
+
 def cpu_baseline_decode(torch, st, q, seqs, *, hq, kvh, d, g, bs, scale, sample=32):
     """Oracle (reference algorithm in torch-CPU) on ``sample`` of the sequences
     (the whole config-3 batch by default: about 3 s per run, 4 runs)."""
     from oracle import kvq_oracle as ref
 
-    threads = min(16, os.cpu_count() or 1)
+    info = cpu_info()
+    threads = info["cores"]
     torch.set_num_threads(threads)
     caches = tuple(t.cpu() for t in st.caches)
     idx = list(range(min(sample, len(seqs))))
@@ -402,6 +502,8 @@ def cpu_baseline_decode(torch, st, q, seqs, *, hq, kvh, d, g, bs, scale, sample=
         "value": round(nbytes / t / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
+        "cpu_model": info["cpu_model"],
+        "os_cpu_count": info["os_cpu_count"],
         "kind": "port",
         "sample": (
             f"{len(idx)} of {len(seqs)} config-3 sequences ({sum(lens)} tokens): oracle "
@@ -416,71 +518,106 @@ def cpu_baseline_decode(torch, st, q, seqs, *, hq, kvh, d, g, bs, scale, sample=
 # ---------------------------------------------------------------------------
 
 
-def bench_pack_gather(torch, dev, *, reps=10, seed=0):
-    """Config 4 geometry: pack a 2048-token chunk per request, gather 10240 tokens."""
+def bench_pack_gather(torch, dev, *, reps=12, seed=0, sets=4):
+    """Config 4 geometry: pack a 2048-token chunk per request, gather 10240 tokens.
+
+    ``sets`` independent caches and chunk inputs are used in turn -- 268 MB of
+    chunk K/V for the pack and 380 MB of int4 pages for the gather over the
+    four sets -- so no timed call finds its inputs in the 256 MB MALL from the
+    previous call of the same set.
+    """
     from vllm_ascend_quantized_kv_cache.ops.kivi_gather import gather_dequant_with_residual
     from vllm_ascend_quantized_kv_cache.ops.kivi_pack import pack_key_rows, pack_value_rows
 
     b, kvh, d, g, r, bs = 8, 8, 128, 128, 128, 128
     lens = [10240] * b
+    chunk = 2048
     gen = torch.Generator().manual_seed(seed)
     key_scales = torch.exp(torch.randn((kvh, d), generator=gen)).to(dev)
-    st = KiviState(torch, dev, lens, kvh=kvh, d=d, g=g, r=r, bs=bs, spare_steps=1, seed=seed,
-                   key_scales=key_scales)
-    s = st.layout.bytes_per_token_head
-    kq, ks, km, vq, vs, vm = st.caches
-    # pack: the last 2048 positions of every request (whole key groups)
-    chunk = 2048
-    gdev = torch.Generator(device=dev).manual_seed(seed + 3)
-    key = (torch.randn((b * chunk, kvh, d), generator=gdev, device=dev) * key_scales).to(torch.bfloat16)
-    value = torch.randn((b * chunk, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
-    slots = torch.cat([st.slots(i, 8192, 10240) for i in range(b)])
-
-    def pack():
-        pack_key_rows(key, None, None, slots, kq, ks, km, g)
-        pack_value_rows(value, None, None, slots, vq, vs, vm, g)
-
-    sustain(torch, pack)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        pack()
-    e1.record()
-    torch.cuda.synchronize()
-    pack_ms = e0.elapsed_time(e1) / reps
-    pack_bytes = b * chunk * kvh * 2 * (2 * d + s)
-
-    # gather: all 10240 tokens of each request, residual tail overlaid
-    seqs = st.decode_seqs()
-    meta = torch.tensor([[q.ring_row, q.k_first, q.seq_len - q.k_hist, q.v_first,
-                          q.seq_len - q.v_hist] for q in seqs], dtype=torch.int32, device=dev)
+    runs = []
+    for i in range(sets):
+        st = KiviState(torch, dev, lens, kvh=kvh, d=d, g=g, r=r, bs=bs, spare_steps=1,
+                       seed=seed + 17 * i, key_scales=key_scales)
+        gdev = torch.Generator(device=dev).manual_seed(seed + 3 + 17 * i)
+        key = (torch.randn((b * chunk, kvh, d), generator=gdev, device=dev)
+               * key_scales).to(torch.bfloat16)
+        value = torch.randn((b * chunk, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
+        # pack: the last 2048 positions of every request (whole key groups)
+        slots = torch.cat([st.slots(j, 8192, 10240) for j in range(b)])
+        seqs = st.decode_seqs()
+        meta = torch.tensor([[q.ring_row, q.k_first, q.seq_len - q.k_hist, q.v_first,
+                              q.seq_len - q.v_hist] for q in seqs], dtype=torch.int32, device=dev)
+        runs.append(dict(st=st, key=key, value=value, slots=slots, seqs=seqs, meta=meta))
+    s = runs[0]["st"].layout.bytes_per_token_head
     cu_list = [0]
     for n in lens:
         cu_list.append(cu_list[-1] + n)
     cu = torch.tensor(cu_list, dtype=torch.int64, device=dev)
     total = cu_list[-1]
 
-    def gather():
-        return gather_dequant_with_residual(st.caches, st.table, cu, total, torch.bfloat16, g,
-                                            meta, st.ring.key, st.ring.value)
+    def pack(k):
+        x = runs[k % sets]
+        kq, ks, km, vq, vs, vm = x["st"].caches
+        pack_key_rows(x["key"], None, None, x["slots"], kq, ks, km, g)
+        pack_value_rows(x["value"], None, None, x["slots"], vq, vs, vm, g)
 
-    sustain(torch, gather)
-    e0.record()
-    for _ in range(reps):
-        gather()
-    e1.record()
-    torch.cuda.synchronize()
-    gather_ms = e0.elapsed_time(e1) / reps
+    def gather(k):
+        x = runs[k % sets]
+        return gather_dequant_with_residual(x["st"].caches, x["st"].table, cu, total,
+                                            torch.bfloat16, g, x["meta"], x["st"].ring.key,
+                                            x["st"].ring.value)
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn):
+        sustain(torch, lambda: [fn(k) for k in range(sets)])
+        e0.record()
+        for k in range(reps):
+            fn(k)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    pack_ms = timed(pack)
+    pack_bytes = b * chunk * kvh * 2 * (2 * d + s)
+    gather_ms = timed(gather)
+    seqs = runs[0]["seqs"]
     hist = sum(q.k_hist + q.v_hist for q in seqs)
     res_t = sum(2 * q.seq_len - q.k_hist - q.v_hist for q in seqs)
     gather_bytes = hist * kvh * (s + 2 * d) + res_t * kvh * d * 4
+    del runs
+    torch.cuda.empty_cache()
+    return {
+        "pack_ms": pack_ms,
+        "pack_gbs": pack_bytes / pack_ms / 1e6,
+        "gather_ms": gather_ms,
+        "gather_gbs": gather_bytes / gather_ms / 1e6,
+        "sets": sets,
+    }
 
-    # causal MFMA attention of the 2048-token chunk (kv positions 8192..10239)
-    # over the gathered 10240-token K/V of each request
+
+def bench_prefill_attention(torch, dev, *, reps=10, seed=0):
+    """Config 4's causal MFMA attention: the 2048-token chunk of each of 8
+    requests (kv positions 8192..10239) over its gathered 10240-token K/V."""
     from vllm_ascend_quantized_kv_cache.ops.attention import prefill_attention
+    from vllm_ascend_quantized_kv_cache.ops.kivi_gather import gather_dequant_with_residual
 
-    hq = 40
-    dk, dv = gather()
+    b, hq, kvh, d, g, r, bs = 8, 40, 8, 128, 128, 128, 128
+    lens = [10240] * b
+    chunk = 2048
+    gen = torch.Generator().manual_seed(seed)
+    key_scales = torch.exp(torch.randn((kvh, d), generator=gen)).to(dev)
+    st = KiviState(torch, dev, lens, kvh=kvh, d=d, g=g, r=r, bs=bs, spare_steps=1, seed=seed,
+                   key_scales=key_scales)
+    seqs = st.decode_seqs()
+    meta = torch.tensor([[q.ring_row, q.k_first, q.seq_len - q.k_hist, q.v_first,
+                          q.seq_len - q.v_hist] for q in seqs], dtype=torch.int32, device=dev)
+    cu = torch.tensor([0] + [sum(lens[:i + 1]) for i in range(b)], dtype=torch.int64,
+                      device=dev)
+    dk, dv = gather_dequant_with_residual(st.caches, st.table, cu, sum(lens), torch.bfloat16, g,
+                                          meta, st.ring.key, st.ring.value)
+    del st
+    gdev = torch.Generator(device=dev).manual_seed(seed + 3)
     q = torch.randn((b * chunk, hq, d), generator=gdev, device=dev).to(torch.bfloat16)
     q_lens, kv_lens = [chunk] * b, list(lens)
     attn_out = torch.empty_like(q)
@@ -489,6 +626,7 @@ def bench_pack_gather(torch, dev, *, reps=10, seed=0):
         prefill_attention(q, dk, dv, q_lens, kv_lens, d ** -0.5, True, out=attn_out)
 
     sustain(torch, attend)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
         attend()
@@ -498,16 +636,9 @@ def bench_pack_gather(torch, dev, *, reps=10, seed=0):
     # causally valid (query, key) pairs x heads x (QK + PV) x 2 flops x D
     pairs = sum(sum(range(n - m + 1, n + 1)) for m, n in zip(q_lens, kv_lens))
     attn_flops = 4 * d * hq * pairs
-    del st, key, value, dk, dv, q, attn_out
+    del dk, dv, q, attn_out
     torch.cuda.empty_cache()
-    return {
-        "pack_ms": pack_ms,
-        "pack_gbs": pack_bytes / pack_ms / 1e6,
-        "gather_ms": gather_ms,
-        "gather_gbs": gather_bytes / gather_ms / 1e6,
-        "attn_ms": attn_ms,
-        "attn_tflops": attn_flops / attn_ms / 1e9,
-    }
+    return {"attn_ms": attn_ms, "attn_tflops": attn_flops / attn_ms / 1e9}
 
 
 def bench_int8_decode(torch, dev, *, reps=20, seed=0, layers=2):
@@ -623,6 +754,9 @@ def bench_int8_ops(torch, dev, *, reps=10, seed=0):
 # ---------------------------------------------------------------------------
 
 
+EXTRA_LEGS = ("forward", "config4", "config4attn", "config2", "config2ops", "config5")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -631,6 +765,12 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-config5", action="store_true")
+    ap.add_argument("--legs", default=",".join(EXTRA_LEGS),
+                    help="comma list of extra legs to run after the headline: "
+                         + ", ".join(EXTRA_LEGS))
+    ap.add_argument("--only", default=None,
+                    help="run only this one extra leg and print its numbers (no headline "
+                         "line); for counter runs of a single workload")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 512 MiB device-to-device 5 times (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -663,6 +803,18 @@ def main() -> int:
     b, hq, kvh, d, g, r, bs = 32, 40, 8, 128, 128, 128, 128
     gen = torch.Generator().manual_seed(0)
     lens = torch.randint(2048, 16385, (b,), generator=gen).tolist()
+    legs = [x for x in args.legs.split(",") if x]
+    if args.no_config5:
+        legs = [x for x in legs if x != "config5"]
+    for x in legs + ([args.only] if args.only else []):
+        if x not in EXTRA_LEGS:
+            print(f"unknown leg {x!r}; choose from {', '.join(EXTRA_LEGS)}", file=sys.stderr)
+            return 2
+    if args.only:
+        res = run_leg(torch, dev, args.only, lens, args)
+        print(json.dumps({"leg": args.only, **res}), flush=True)
+        return 0
+
     log(f"config3: {b} seqs, L in [{min(lens)}, {max(lens)}], mean {sum(lens) / b:.0f}")
     # two layers' caches (0.34 GB each) in turn: one layer alone would fit
     # most of its pages in the 256 MB MALL between consecutive calls
@@ -675,37 +827,8 @@ def main() -> int:
 
     extra = {}
     if not args.no_extras:
-        pg = bench_pack_gather(torch, dev)
-        extra["config4_pack"] = {"ms": round(pg["pack_ms"], 4), "gbs": round(pg["pack_gbs"], 1),
-                                 "frac": round(pg["pack_gbs"] / HBM_PEAK_GBS, 4)}
-        extra["config4_gather"] = {"ms": round(pg["gather_ms"], 4),
-                                   "gbs": round(pg["gather_gbs"], 1),
-                                   "frac": round(pg["gather_gbs"] / HBM_PEAK_GBS, 4)}
-        extra["config4_prefill_attn"] = {"ms": round(pg["attn_ms"], 4),
-                                         "tflops": round(pg["attn_tflops"], 1),
-                                         "frac": round(pg["attn_tflops"] / MFMA_PEAK_TFLOPS, 4)}
-        log(f"config4: pack {pg['pack_gbs']:.0f} GB/s, gather {pg['gather_gbs']:.0f} GB/s, "
-            f"attention {pg['attn_tflops']:.0f} TFLOP/s")
-        i8 = bench_int8_decode(torch, dev)
-        extra["config2_int8_decode"] = {k: round(v, 4) for k, v in i8.items()}
-        i8ops = bench_int8_ops(torch, dev)
-        for k, v in i8ops.items():
-            extra[f"config2_int8_{k}"] = v
-        log("config2: " + ", ".join(f"{k} {v['gbs']:.0f} GB/s" for k, v in i8ops.items()))
-        log(f"config2: int8 decode {i8['us_per_layer']:.1f} us ({i8['gbs']:.0f} GB/s)")
-        if not args.no_config5:
-            # one layer: 10.8 GB of pages, far past any cache
-            c5 = bench_kivi_decode(
-                torch, dev, b=256, hq=64, kvh=8, d=128, g=64, r=128, bs=128,
-                lens=[32768] * 256, steps=5, warmup=2, seed=5, want_cpu=False, label="config5",
-            )
-            extra["config5_int4_decode"] = {
-                "us_per_layer": round(c5["decode_ms"] * 1e3, 1),
-                "gbs": round(c5["decode_gbs"], 1),
-                "frac": round(c5["decode_gbs"] / HBM_PEAK_GBS, 4),
-                "step_us": round(c5["step_ms"] * 1e3, 1),
-            }
-            log(f"config5: decode {c5['decode_ms'] * 1e3:.1f} us ({c5['decode_gbs']:.0f} GB/s)")
+        for leg in legs:
+            extra.update(run_leg(torch, dev, leg, lens, args))
 
     line = {
         "metric": METRIC,
@@ -745,6 +868,56 @@ def main() -> int:
         line["cpu_baseline"] = c
     print(json.dumps(line), flush=True)
     return 0
+
+
+def run_leg(torch, dev, leg: str, lens: list[int], args) -> dict:
+    """One extra leg; returns its entries for the JSON line's ``extra``."""
+    out = {}
+    if leg == "forward":
+        fw = bench_kivi_forward(torch, dev, lens=lens, hq=40, kvh=8, d=128, g=128, r=128,
+                                bs=128, steps=args.steps, warmup=args.warmup, seed=11)
+        out["config3_forward"] = {"us_per_step": round(fw["us_per_step"], 1)}
+        log(f"config3: forward() {fw['us_per_step']:.1f} us per step (host clock)")
+    elif leg == "config4":
+        pg = bench_pack_gather(torch, dev)
+        out["config4_pack"] = {"ms": round(pg["pack_ms"], 4), "gbs": round(pg["pack_gbs"], 1),
+                               "frac": round(pg["pack_gbs"] / HBM_PEAK_GBS, 4),
+                               "input_sets": pg["sets"]}
+        out["config4_gather"] = {"ms": round(pg["gather_ms"], 4),
+                                 "gbs": round(pg["gather_gbs"], 1),
+                                 "frac": round(pg["gather_gbs"] / HBM_PEAK_GBS, 4),
+                                 "input_sets": pg["sets"]}
+        log(f"config4: pack {pg['pack_gbs']:.0f} GB/s, gather {pg['gather_gbs']:.0f} GB/s "
+            f"({pg['sets']} input sets in turn)")
+    elif leg == "config4attn":
+        at = bench_prefill_attention(torch, dev)
+        out["config4_prefill_attn"] = {"ms": round(at["attn_ms"], 4),
+                                       "tflops": round(at["attn_tflops"], 1),
+                                       "frac": round(at["attn_tflops"] / MFMA_PEAK_TFLOPS, 4)}
+        log(f"config4: attention {at['attn_tflops']:.0f} TFLOP/s")
+    elif leg == "config2":
+        i8 = bench_int8_decode(torch, dev)
+        out["config2_int8_decode"] = {k: round(v, 4) for k, v in i8.items()}
+        log(f"config2: int8 decode {i8['us_per_layer']:.1f} us ({i8['gbs']:.0f} GB/s)")
+    elif leg == "config2ops":
+        i8ops = bench_int8_ops(torch, dev)
+        for k, v in i8ops.items():
+            out[f"config2_int8_{k}"] = v
+        log("config2: " + ", ".join(f"{k} {v['gbs']:.0f} GB/s" for k, v in i8ops.items()))
+    elif leg == "config5":
+        # one layer: 10.8 GB of pages, far past any cache
+        c5 = bench_kivi_decode(
+            torch, dev, b=256, hq=64, kvh=8, d=128, g=64, r=128, bs=128,
+            lens=[32768] * 256, steps=5, warmup=2, seed=5, want_cpu=False, label="config5",
+        )
+        out["config5_int4_decode"] = {
+            "us_per_layer": round(c5["decode_ms"] * 1e3, 1),
+            "gbs": round(c5["decode_gbs"], 1),
+            "frac": round(c5["decode_gbs"] / HBM_PEAK_GBS, 4),
+            "step_us": round(c5["step_ms"] * 1e3, 1),
+        }
+        log(f"config5: decode {c5['decode_ms'] * 1e3:.1f} us ({c5['decode_gbs']:.0f} GB/s)")
+    return out
 
 
 if __name__ == "__main__":
