@@ -47,6 +47,15 @@ enum {
   KVQ_ERR_INVALID = -1,     /* bad pointer, dtype or size */
   KVQ_ERR_GEOMETRY = -2,    /* geometry the kernels do not support */
   KVQ_ERR_SCRATCH = -3,     /* work larger than the library's static scratch */
+  KVQ_ERR_CAPACITY = -4,    /* output arrays too small for the plan */
+};
+
+/* Decode work plans (kvq_plan_kivi_decode). */
+enum {
+  KVQ_PLAN_DEFAULT = 0,       /* pieces when the work fills the chip once, else paired splits */
+  KVQ_PLAN_PIECES = 1,        /* equal-cost pieces (one or more rounds) */
+  KVQ_PLAN_SPLIT = 2,         /* int4 ranges every split_tokens positions */
+  KVQ_PLAN_SPLIT_PAIRED = 3,  /* as SPLIT, each range as an even/odd-chunk pair */
 };
 
 /* Size of the static device scratch behind kvq_kivi_decode_attn_noalloc. */
@@ -202,6 +211,43 @@ int kvq_kivi_decode_attn_noalloc(const void* query, int q_dtype, int64_t batch, 
                                  const int32_t* work, int64_t num_work, const int32_t* pieces,
                                  int64_t num_pieces, const void* ring_k, const void* ring_v,
                                  int ring_dtype, int ring_len, void* out, void* stream);
+
+/* Host-side (no GPU call): the work list, and pieces, of kvq_kivi_decode_attn
+ * for a batch, written into caller arrays (plain host memory; pinned memory
+ * lets the caller copy the plan to the device without a synchronisation).
+ *   seqs      int32 [batch, 6] = {seq_len, k_hist, v_hist, ring_row,
+ *             k_first_lane, v_first_lane} (the seq_meta columns it fills)
+ *   seq_meta  int32 [batch, 8]; work int32 [cap_work, 4];
+ *   pieces    int32 [cap_pieces + 1] (KVQ_PLAN_PIECES / DEFAULT)
+ *   mode      KVQ_PLAN_*; split_tokens for the SPLIT modes; tail_cost = the
+ *             cost of one residual-window position in int4 positions
+ * Returns the number of work items, *num_pieces (0 for split plans), or
+ * KVQ_ERR_INVALID / KVQ_ERR_CAPACITY.  Replaces the per-step decode planning
+ * a host does before _forward_kivi_paged_decode_attention
+ * (pkg/methods/kivi_int4/attention_backend.py:1193-1230): which positions
+ * read int4 pages and which the residual window, split over the chip. */
+int64_t kvq_plan_kivi_decode(const int32_t* seqs, int64_t batch, int num_kv_heads, int cu_count,
+                             int mode, int64_t split_tokens, double tail_cost, int32_t* seq_meta,
+                             int32_t* work, int64_t cap_work, int32_t* pieces,
+                             int64_t cap_pieces, int64_t* num_pieces);
+
+/* kvq_kivi_store with its counts and jobs in one device buffer, sized for
+ * capacities: plan (int64, device) = [n_key_pack, n_value_pack, n_key_ring,
+ * n_value_ring, key pack src[cap_key_pack], key pack slot[cap_key_pack],
+ * value pack src[cap_value_pack], value pack slot[cap_value_pack], key ring
+ * src[cap_ring], key ring dst[cap_ring], value ring src[cap_ring], value ring
+ * dst[cap_ring]].  The grid covers the capacities and each wave reads the
+ * counts, so one launch, captured once in a HIP graph, serves every step
+ * whose plan the host copies into the buffer before it runs.  Same
+ * preconditions and geometry as kvq_kivi_store.  Replaces, like
+ * kvq_kivi_store, a step of _store_kivi_residual_entries
+ * (pkg/methods/kivi_int4/attention_backend.py:411-462). */
+int kvq_kivi_store_planned(const void* key_input, const void* value_input, void* ring_k,
+                           void* ring_v, int64_t ring_rows, int dtype, int num_kv_heads,
+                           int head_size, int group_size, int block_size, const int64_t* plan,
+                           int64_t cap_key_pack, int64_t cap_value_pack, int64_t cap_ring,
+                           int32_t* k_quant, float* k_scale, float* k_mn, int32_t* v_quant,
+                           float* v_scale, float* v_mn, void* stream);
 
 /* ---- dense attention ----------------------------------------------------- */
 

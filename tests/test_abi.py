@@ -14,7 +14,8 @@ ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "kvq_hip.h"
 PKG = ROOT / "vllm-ascend-quantized-kv-cache-hust_amd" / "vllm_ascend_quantized_kv_cache"
 
-_C_TO_CTYPES = {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float}
+_C_TO_CTYPES = {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float,
+                "double": ctypes.c_double}
 
 
 def _declarations() -> dict[str, tuple[str, list[str]]]:

@@ -1,0 +1,217 @@
+# SPDX-License-Identifier: Apache-2.0
+"""The planned KIVI decode step on the GPU: sync-free, and capturable.
+
+* ``forward(DecodeOnly)`` through the planned step (one pinned plan, the
+  planned store, the fused decode) leaves the same int4 pages and rings as
+  the general path (per-request planning, the one-launch store) and gives
+  the same output, over steps that flush key windows and evict values;
+* with the host's copies of ``slot_mapping`` and ``block_tables`` in the
+  metadata, a step reads nothing back from the device;
+* the step's two launches captured once in a HIP graph, replayed over many
+  steps (each after the host stages that step's plan), match an eager twin
+  bit for bit and the oracle's fp32 attention over the reference dequant.
+"""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from oracle import kvq_oracle as ref
+from tests._cpu_kernels import windows_from_meta
+from vllm_ascend_quantized_kv_cache.methods.kivi_int4 import attention_backend as ab
+from vllm_ascend_quantized_kv_cache.methods.kivi_int4.byte_cache import KiviByteCacheLayout
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(atol=1e-2, rtol=1e-2)
+
+
+def _impl(device, *, hq, kvh, d, g, r, nb, bs, rows, general=False):
+    class Impl(ab.AscendKiviInt4AttentionBackendMixin):
+        pass
+
+    impl = Impl()
+    impl.num_heads, impl.num_kv_heads, impl.head_size, impl.scale = hq, kvh, d, d ** -0.5
+    impl._init_kivi_state(None)
+    impl.enable_kivi = True
+    impl.kivi_group_size, impl.kivi_residual_length, impl.kivi_max_num_seqs = g, r, rows
+    layout = KiviByteCacheLayout(nb, bs, kvh, d, g)
+    kbuf = torch.zeros((nb, bs, kvh, layout.bytes_per_token_head), dtype=torch.uint8,
+                       device=device)
+    impl._bind_kivi_cache((kbuf, torch.zeros_like(kbuf)))
+    if general:
+        # the same GPU launch, installed as an instance hook: the planned step
+        # stands aside and forward takes the general path
+        impl._launch_kivi_decode = impl._launch_kivi_decode
+    return impl
+
+
+class _Case:
+    """Requests with int4 history and windows, identical on every impl built."""
+
+    def __init__(self, device, *, b=6, hq=40, kvh=8, d=128, g=128, r=128, bs=128, steps=140,
+                 seed=0):
+        gen = torch.Generator().manual_seed(seed)
+        self.device, self.b, self.hq, self.kvh, self.d, self.g, self.r, self.bs = (
+            device, b, hq, kvh, d, g, r, bs)
+        self.lens = torch.randint(200, 1500, (b,), generator=gen).tolist()
+        nblk = [-(-(n + steps + 1) // bs) for n in self.lens]
+        self.nb = sum(nblk) + 4
+        perm = torch.randperm(self.nb, generator=gen)
+        self.table = torch.zeros((b, max(nblk)), dtype=torch.int64)
+        used = 0
+        for i, n in enumerate(nblk):
+            self.table[i, :n] = perm[used:used + n]
+            used += n
+        self.table_dev = self.table.to(device)
+        scales = torch.exp(torch.randn((kvh, d), generator=gen))
+        self.keys = [(torch.randn(n + steps, kvh, d, generator=gen) * scales).to(torch.bfloat16)
+                     for n in self.lens]
+        self.values = [torch.randn(n + steps, kvh, d, generator=gen).to(torch.bfloat16)
+                       for n in self.lens]
+        self.queries = torch.randn(steps, b, hq, d, generator=gen).to(torch.bfloat16)
+        self.reqs = [f"r{i}" for i in range(b)]
+
+    def slot(self, i, p):
+        return int(self.table[i, p // self.bs]) * self.bs + p % self.bs
+
+    def build(self, **kw):
+        impl = _impl(self.device, hq=self.hq, kvh=self.kvh, d=self.d, g=self.g, r=self.r,
+                     nb=self.nb, bs=self.bs, rows=self.b, **kw)
+        for i, n in enumerate(self.lens):
+            sl = torch.tensor([self.slot(i, p) for p in range(n)], device=self.device)
+            impl._write_kivi_cache(self.keys[i][:n].to(self.device),
+                                   self.values[i][:n].to(self.device), sl, [self.reqs[i]], [n],
+                                   [n])
+        return impl
+
+    def step(self, j, *, host_copies=True):
+        """(metadata, q, k, v) of decode step j (each request gains token n + j)."""
+        pos = [n + j for n in self.lens]
+        sm = torch.tensor([self.slot(i, p) for i, p in enumerate(pos)])
+        md = SimpleNamespace(attn_state=SimpleNamespace(name="DecodeOnly"), causal=True,
+                             finished_req_ids=None, seq_lens_list=[p + 1 for p in pos],
+                             slot_mapping=sm.to(self.device), block_tables=self.table_dev,
+                             req_ids=self.reqs, num_actual_tokens=self.b)
+        if host_copies:
+            md.slot_mapping_cpu = sm
+            md.block_tables_cpu = self.table
+        k = torch.stack([self.keys[i][p] for i, p in enumerate(pos)]).to(self.device)
+        v = torch.stack([self.values[i][p] for i, p in enumerate(pos)]).to(self.device)
+        return md, self.queries[j].to(self.device), k, v
+
+    def oracle(self, impl, j, out):
+        """The oracle's attention for step j from the GPU state after it."""
+        caches = tuple(t.cpu() for t in impl._kivi_caches())
+        lens = [n + j + 1 for n in self.lens]
+        meta = impl._ring_meta_rows(lens, self.reqs)
+        ring = impl._kivi_ring
+        cpu_ring = SimpleNamespace(_kivi_ring=SimpleNamespace(
+            key=ring.key.cpu(), value=ring.value.cpu(), ring_len=ring.ring_len))
+        wk, wv = windows_from_meta(cpu_ring, meta, lens)
+        dk, dv = ref.dequant_gather(*caches, self.table, torch.tensor(lens), torch.float32,
+                                    self.g)
+        dk = ref.overlay_residual(dk, lens, wk)
+        dv = ref.overlay_residual(dv, lens, wv)
+        want = ref.attention(self.queries[j], dk, dv, [1] * self.b, lens, self.d ** -0.5, True)
+        torch.testing.assert_close(out.float().cpu(), want, **TOL)
+
+
+def _same_state(a, b):
+    for x, y in zip(a._kivi_caches(), b._kivi_caches()):
+        assert torch.equal(x, y), "int4 pages differ"
+    ra, rb = a._kivi_ring, b._kivi_ring
+    assert ra.state() == rb.state()
+    assert torch.equal(ra.key, rb.key) and torch.equal(ra.value, rb.value)
+
+
+@pytest.mark.parametrize("g", [128, 64])
+def test_planned_decode_step_equals_general_path(gpu_device, g):
+    case = _Case(gpu_device, g=g, r=128, steps=135, seed=1 if g == 128 else 2)
+    fast, general = case.build(), case.build(general=True)
+    for j in range(135):  # a key window flushes for every request
+        outs = []
+        for impl in (fast, general):
+            md, q, k, v = case.step(j)
+            out = torch.zeros((case.b, case.hq, case.d), dtype=torch.bfloat16, device=gpu_device)
+            impl.forward(None, q, k, v, None, md, out)
+            outs.append(out)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1]), f"step {j}"
+        if j % 45 == 0 or j == 134:
+            _same_state(fast, general)
+            case.oracle(fast, j, outs[0])
+    assert fast._kivi_step_bufs is not None and general._kivi_step_bufs is None
+    assert fast.kivi_host_reads == 0
+
+
+def test_planned_decode_step_reads_nothing_back(gpu_device):
+    case = _Case(gpu_device, steps=4, seed=3)
+    impl = case.build()
+    md, q, k, v = case.step(0)
+    out = torch.zeros((case.b, case.hq, case.d), dtype=torch.bfloat16, device=gpu_device)
+    impl.forward(None, q, k, v, None, md, out)  # first call sizes the buffers
+    # the steps' metadata and inputs, built (and copied to the device) by the
+    # host runner before the steps run
+    steps = [case.step(j) for j in (1, 2)]
+    torch.cuda.synchronize()
+    probe = torch.ones(4, device=gpu_device)
+    prev = torch.cuda.get_sync_debug_mode()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        try:
+            probe.cpu()
+            detects = False
+        except RuntimeError:
+            detects = True
+        for md, q, k, v in steps:
+            impl.forward(None, q, k, v, None, md, out)
+    finally:
+        torch.cuda.set_sync_debug_mode(prev)
+    torch.cuda.synchronize()
+    assert impl.kivi_host_reads == 0
+    case.oracle(impl, 2, out)
+    if not detects:
+        pytest.skip("this torch build does not flag synchronising calls; host reads counted only")
+    # without host copies the mixin reads the two tensors back, once each
+    md, q, k, v = case.step(3, host_copies=False)
+    impl.forward(None, q, k, v, None, md, out)
+    assert impl.kivi_host_reads == 2
+
+
+def test_decode_step_graph_replays_match_eager_twin_and_oracle(gpu_device):
+    """Capture store + decode + combine once; replay it for 131 steps (key
+    windows flush inside replays), each step's plan staged by the host
+    between replays, with the program's own eager work in between."""
+    steps = 131
+    case = _Case(gpu_device, steps=steps, seed=4)
+    graphed, eager = case.build(), case.build()
+    gstep = graphed.kivi_decode_graph(case.b, max_blocks=case.table.shape[1])
+    q_s = torch.zeros((case.b, case.hq, case.d), dtype=torch.bfloat16, device=gpu_device)
+    k_s = torch.zeros((case.b, case.kvh, case.d), dtype=torch.bfloat16, device=gpu_device)
+    v_s = torch.zeros_like(k_s)
+    out_s = torch.zeros_like(q_s)
+    graph = None
+    for j in range(steps):
+        md, q, k, v = case.step(j)
+        q_s.copy_(q)
+        k_s.copy_(k)
+        v_s.copy_(v)
+        gstep.prepare(md, k_s, v_s)
+        if graph is None:
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                gstep.launch(q_s, k_s, v_s, out_s)
+        graph.replay()
+        out = torch.zeros_like(q_s)
+        eager.forward(None, q, k, v, None, md, out)
+        torch.cuda.synchronize()
+        assert torch.equal(out_s, out), f"replay {j} differs from the eager step"
+        if j in (0, 1, 64, steps - 1):
+            _same_state(graphed, eager)
+            case.oracle(graphed, j, out_s)
+    assert graphed.kivi_host_reads == 0

@@ -64,8 +64,7 @@ def _assert_same_state(gpu, cpu):
     for a, b in zip(gpu._kivi_caches(), cpu._kivi_caches()):
         assert torch.equal(a.cpu(), b), "packed history differs"
     rg, rc = gpu._kivi_ring, cpu._kivi_ring
-    assert rg.length == rc.length and rg.start == rc.start
-    assert rg.lane_slot == rc.lane_slot
+    assert rg.state() == rc.state()
     assert torch.equal(rg.key.cpu(), rc.key) and torch.equal(rg.value.cpu(), rc.value)
 
 

@@ -13,6 +13,7 @@ from __future__ import annotations
 import random
 from types import SimpleNamespace
 
+import numpy as np
 import pytest
 import torch
 
@@ -296,7 +297,7 @@ def test_closed_form_run_plan_equals_token_replay(seed):
     base = [(rng.randrange(0, 4) + 64 * r) * block for r in range(rows)]
 
     def state(ring):
-        return (ring.start, ring.length, ring.lane_slot, ring.slot_lane)
+        return ring.state()
 
     for _step in range(12):
         plans = [StorePlan(), StorePlan()]
@@ -324,6 +325,81 @@ def test_closed_form_run_plan_equals_token_replay(seed):
         with pytest.raises(RuntimeError, match="aligned token groups"):
             fn(StorePlan(), row, slots, list(range(len(slots))), is_key=True,
                block_size=block, group_size=group)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_decode_step_plan_equals_token_replay(seed):
+    """``plan_decode_step`` (one token per request, the whole batch at once)
+    leaves the same mirror and emits the same jobs as ``plan_store`` token by
+    token, over steps that fill windows, flush key windows and evict values,
+    with requests joining at different lengths; an unaligned key window is
+    rejected with no row changed."""
+    from vllm_ascend_quantized_kv_cache.methods.kivi_int4.residual import (
+        KiviResidualRing,
+        StorePlan,
+    )
+
+    rng = random.Random(seed)
+    group = rng.choice([8, 16])
+    window = group * rng.choice([1, 2, 3])
+    block = 2 * window
+    rows = 6
+    fast, slow = (KiviResidualRing(rows, window, 1, 8, device="cpu") for _ in range(2))
+    pos = [rng.randrange(0, 3 * window) if r % 2 else 0 for r in range(rows)]
+    base = [(64 * r + 1) * block for r in range(rows)]
+    for r in range(rows):  # earlier tokens, written as one run
+        if pos[r]:
+            slots = list(range(base[r], base[r] + pos[r]))
+            for ring in (fast, slow):
+                for k in (True, False):
+                    ring.plan_store(StorePlan(), r, slots, list(range(pos[r])), is_key=k,
+                                    block_size=block, group_size=group,
+                                    positions=list(range(pos[r])))
+    for _ in range(3 * window + 5):
+        batch = sorted(rng.sample(range(rows), rng.randrange(1, rows + 1)))
+        rws = np.asarray(batch, dtype=np.int64)
+        slots = np.asarray([base[r] + pos[r] for r in batch], dtype=np.int64)
+        p = np.asarray([pos[r] for r in batch], dtype=np.int64)
+        jobs = fast.plan_decode_step(rws, slots, p, np.arange(len(batch)), block_size=block,
+                                     group_size=group)
+        assert jobs is not None
+        plan = StorePlan()
+        for i, r in enumerate(batch):
+            for k in (True, False):
+                slow.plan_store(plan, r, [int(slots[i])], [i], is_key=k, block_size=block,
+                                group_size=group, positions=[pos[r]])
+        assert fast.state() == slow.state()
+        for k in (True, False):
+            assert np.array_equal(fast.lane_pos[k], slow.lane_pos[k])
+        assert jobs.key_pack_src.tolist() == plan.key.pack_src
+        assert jobs.key_pack_slot.tolist() == plan.key.pack_slots
+        assert jobs.value_pack_src.tolist() == plan.value.pack_src
+        assert jobs.value_pack_slot.tolist() == plan.value.pack_slots
+        assert dict(zip(jobs.key_ring_dst.tolist(), jobs.key_ring_src.tolist())) == plan.key.ring
+        assert dict(zip(jobs.value_ring_dst.tolist(),
+                        jobs.value_ring_src.tolist())) == plan.value.ring
+        for r in batch:
+            pos[r] += 1
+    # a held slot, or a repeated row, is left to the per-token path
+    r0 = np.asarray([0], dtype=np.int64)
+    held = np.asarray([base[0] + pos[0] - 1], dtype=np.int64)
+    assert fast.plan_decode_step(r0, held, held - base[0], r0, block_size=block,
+                                 group_size=group) is None
+    assert fast.plan_decode_step(np.asarray([1, 1]), np.asarray([7, 8]), np.asarray([0, 1]),
+                                 np.asarray([0, 1]), block_size=block, group_size=group) is None
+    # a full key window that starts off a group boundary: rejected, nothing changed
+    bad = KiviResidualRing(2, window, 1, 8, device="cpu")
+    for r in range(2):
+        sl = list(range(3 + 64 * block * r, 3 + 64 * block * r + window))
+        for k in (True, False):
+            bad.plan_store(StorePlan(), r, sl, list(range(window)), is_key=k, block_size=block,
+                           group_size=group)
+    before = bad.state()
+    with pytest.raises(RuntimeError, match="aligned token groups"):
+        bad.plan_decode_step(np.asarray([0, 1]), np.asarray([3 + window, 64 * block + 3 + window]),
+                             np.asarray([window, window]), np.asarray([0, 1]), block_size=block,
+                             group_size=group)
+    assert bad.state() == before
 
 
 def test_multi_token_batch_that_reuses_a_packed_lane_is_not_one_launch():
@@ -490,9 +566,7 @@ def test_rejected_batch_leaves_every_mirror_unchanged():
 
     def snapshot():
         return (dict(impl.kivi_residual_req_to_row), list(impl.kivi_residual_free_rows),
-                {k: [list(x) for x in v] for k, v in ring.lane_slot.items()},
-                {k: list(v) for k, v in ring.start.items()},
-                {k: list(v) for k, v in ring.length.items()})
+                ring.state())
 
     before = snapshot()
     launches = {k: len(v) for k, v in impl.calls.items()}

@@ -60,21 +60,29 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found; the ROCm toolchain is required to build libkvq_hip.so")
 
 
+#: host-only sources (planning code with no GPU part), built with the host compiler
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{INCLUDE}", f"-I{CSRC}"]
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
     hipcc = _hipcc()
-    sources = sorted(CSRC.glob("*.hip"))
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     obj_dir = HERE / "_build"
     obj_dir.mkdir(exist_ok=True)
     OUT_DIR.mkdir(parents=True, exist_ok=True)
 
     def compile_one(src: Path) -> Path:
         obj = obj_dir / (src.stem + ".o")
-        cmd = [hipcc, *COMMON_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+        if src.suffix == ".cpp":
+            cmd = [shutil.which("g++") or "g++", *HOST_FLAGS, "-c", str(src), "-o", str(obj)]
+        else:
+            cmd = [hipcc, *COMMON_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o",
+                   str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
+            raise RuntimeError(f"compile failed on {src.name}:\n{res.stdout}\n{res.stderr}")
         return obj
 
     workers = jobs or min(len(sources), os.cpu_count() or 4, 8)

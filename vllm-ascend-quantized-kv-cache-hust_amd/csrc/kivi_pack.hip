@@ -489,11 +489,16 @@ kivi_pack_value_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* _
 // value pack slot | key ring src | key ring dst | value ring src | value ring
 // dst.  The ring is read (pack sources) and written (ring rows) by the same
 // grid, so its pointers are not restrict-qualified.
-template <typename T, int G>
+//
+// PLANNED: the grid and the job sections are sized by capacities (c0..c3) and
+// the actual counts are read from the device (jobs[0..3], sections from
+// jobs + 4 at capacity offsets), so one captured launch serves every step;
+// waves past a count exit at once.
+template <typename T, int G, bool PLANNED>
 __global__ void __launch_bounds__(256)
 kivi_store_kernel(T* ring_k, T* ring_v, int64_t n_ring, const T* __restrict__ in_k,
-                  const T* __restrict__ in_v, const int64_t* __restrict__ jobs, int64_t nkp,
-                  int64_t nvp, int64_t nkr, int64_t nvr, int64_t kblocks, int64_t vblocks,
+                  const T* __restrict__ in_v, const int64_t* __restrict__ jobs, int64_t c0,
+                  int64_t c1, int64_t c2, int64_t c3, int64_t kblocks, int64_t vblocks,
                   FastDiv kvh_div, int bs, int32_t* __restrict__ kq, float* __restrict__ ks,
                   float* __restrict__ km, int32_t* __restrict__ vq, float* __restrict__ vs,
                   float* __restrict__ vm) {
@@ -503,19 +508,38 @@ kivi_store_kernel(T* ring_k, T* ring_v, int64_t n_ring, const T* __restrict__ in
   const int64_t row_elems = static_cast<int64_t>(kvh) * D;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  // counts and the eight job sections
+  int64_t nkp = c0, nvp = c1, nkr = c2, nvr = c3;
+  const int64_t* kp_src = jobs;
+  if constexpr (PLANNED) {
+    nkp = min(jobs[0], c0);
+    nvp = min(jobs[1], c1);
+    nkr = min(jobs[2], c2);
+    nvr = min(jobs[3], c3);
+    kp_src = jobs + 4;
+  }
+  const int64_t* kp_slot = kp_src + c0;
+  const int64_t* vp_src = kp_slot + c0;
+  const int64_t* vp_slot = vp_src + c1;
+  const int64_t* kr_src = vp_slot + c1;
+  const int64_t* kr_dst = kr_src + c2;
+  const int64_t* vr_src = kr_dst + c2;
+  const int64_t* vr_dst = vr_src + c3;
   int64_t b = blockIdx.x;
   if (b < kblocks) {
     const int64_t u = b * 4 + wave;
     if (u < nkp / G * kvh * 2)
-      key_pack_wave<T, int64_t, G>(ring_k, n_ring, in_k, jobs, jobs + nkp, u, lane, kvh, bs, kq,
+      key_pack_wave<T, int64_t, G>(ring_k, n_ring, in_k, kp_src, kp_slot, u, lane, kvh, bs, kq,
                                    ks, km);
     return;
   }
   b -= kblocks;
   if (b < vblocks) {
-    const int64_t* vsrc = jobs + 2 * nkp;
-    const int64_t* vslot = vsrc + nvp;
+    const int64_t* vsrc = vp_src;
+    const int64_t* vslot = vp_slot;
     const int64_t rows = nvp * kvh;  // the host keeps this below 2^31
+    // a wave whose first row is past the end has nothing to store (uniform)
+    if ((b * 4 + wave) * (64 / WPR) >= rows) return;
     const int64_t r = (b * 4 + wave) * (64 / WPR) + lane / WPR;
     const int64_t rc = r < rows ? r : rows - 1;  // past the end: read the last row, store nothing
     const uint32_t t = kvh_div.div(static_cast<uint32_t>(rc));
@@ -534,10 +558,8 @@ kivi_store_kernel(T* ring_k, T* ring_v, int64_t n_ring, const T* __restrict__ in
   const int64_t e = (c - i * per_row) * 8;
   const bool key = i < nkr;
   const int64_t j = key ? i : i - nkr;
-  const int64_t n = key ? nkr : nvr;
-  const int64_t* rs = jobs + 2 * (nkp + nvp) + (key ? 0 : 2 * nkr);
-  const T* src = (key ? in_k : in_v) + rs[j] * row_elems + e;
-  T* dst = (key ? ring_k : ring_v) + rs[n + j] * row_elems + e;
+  const T* src = (key ? in_k : in_v) + (key ? kr_src : vr_src)[j] * row_elems + e;
+  T* dst = (key ? ring_k : ring_v) + (key ? kr_dst : vr_dst)[j] * row_elems + e;
   *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
 }
 
@@ -741,12 +763,60 @@ extern "C" int kvq_kivi_store(const void* key_input, const void* value_input, vo
   hipStream_t s = static_cast<hipStream_t>(stream);
   const FastDiv kdiv = FastDiv::make(static_cast<uint32_t>(num_kv_heads));
 #define KVQ_LAUNCH_STORE(T, GG)                                                               \
-  hipLaunchKernelGGL((kivi_store_kernel<T, GG>), dim3(static_cast<unsigned>(blocks)),         \
+  hipLaunchKernelGGL((kivi_store_kernel<T, GG, false>), dim3(static_cast<unsigned>(blocks)),  \
                      dim3(256), 0, s, static_cast<T*>(ring_k), static_cast<T*>(ring_v),        \
                      ring_rows, static_cast<const T*>(key_input),                              \
                      static_cast<const T*>(value_input), jobs, n_key_pack, n_value_pack,       \
                      n_key_ring, n_value_ring, kblocks, vblocks, kdiv, block_size, k_quant,    \
                      k_scale, k_mn, v_quant, v_scale, v_mn)
+  if (dtype == KVQ_DTYPE_BF16) {
+    if (group_size == 128) { KVQ_LAUNCH_STORE(bf16, 128); } else { KVQ_LAUNCH_STORE(bf16, 64); }
+  } else {
+    if (group_size == 128) { KVQ_LAUNCH_STORE(f16, 128); } else { KVQ_LAUNCH_STORE(f16, 64); }
+  }
+#undef KVQ_LAUNCH_STORE
+  KVQ_LAUNCH_CHECK();
+  return KVQ_OK;
+}
+
+extern "C" int kvq_kivi_store_planned(const void* key_input, const void* value_input,
+                                      void* ring_k, void* ring_v, int64_t ring_rows, int dtype,
+                                      int num_kv_heads, int head_size, int group_size,
+                                      int block_size, const int64_t* plan,
+                                      int64_t cap_key_pack, int64_t cap_value_pack,
+                                      int64_t cap_ring, int32_t* k_quant, float* k_scale,
+                                      float* k_mn, int32_t* v_quant, float* v_scale,
+                                      float* v_mn, void* stream) {
+  if (cap_key_pack < 0 || cap_value_pack < 0 || cap_ring < 0 || ring_rows < 0)
+    return KVQ_ERR_INVALID;
+  if (!plan || !ring_k || !ring_v || !key_input || !value_input || !k_quant || !k_scale ||
+      !k_mn || !v_quant || !v_scale || !v_mn)
+    return KVQ_ERR_INVALID;
+  if (!kivi_geometry_ok(num_kv_heads, head_size, group_size, block_size))
+    return KVQ_ERR_GEOMETRY;
+  if (head_size != 128 || (group_size != 64 && group_size != 128) ||
+      (dtype != KVQ_DTYPE_BF16 && dtype != KVQ_DTYPE_F16))
+    return KVQ_ERR_GEOMETRY;
+  if (cap_key_pack % group_size) return KVQ_ERR_INVALID;
+  if (cap_value_pack * num_kv_heads >= 0x7fffffff) return KVQ_ERR_INVALID;
+  const int64_t kunits = cap_key_pack / group_size * num_kv_heads * 2;
+  const int64_t kblocks = (kunits + 3) / 4;
+  const int64_t vunits = (cap_value_pack * num_kv_heads + 3) / 4;  // 4 rows per wave
+  const int64_t vblocks = (vunits + 3) / 4;
+  const int64_t rchunks = 2 * cap_ring * num_kv_heads * (head_size / 8);
+  const int64_t rblocks = (rchunks + 255) / 256;
+  const int64_t blocks = kblocks + vblocks + rblocks;
+  if (blocks == 0) return KVQ_OK;
+  if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const FastDiv kdiv = FastDiv::make(static_cast<uint32_t>(num_kv_heads));
+#define KVQ_LAUNCH_STORE(T, GG)                                                               \
+  hipLaunchKernelGGL((kivi_store_kernel<T, GG, true>), dim3(static_cast<unsigned>(blocks)),   \
+                     dim3(256), 0, s, static_cast<T*>(ring_k), static_cast<T*>(ring_v),        \
+                     ring_rows, static_cast<const T*>(key_input),                              \
+                     static_cast<const T*>(value_input), plan, cap_key_pack, cap_value_pack,   \
+                     cap_ring, cap_ring, kblocks, vblocks, kdiv, block_size, k_quant, k_scale, \
+                     k_mn, v_quant, v_scale, v_mn)
   if (dtype == KVQ_DTYPE_BF16) {
     if (group_size == 128) { KVQ_LAUNCH_STORE(bf16, 128); } else { KVQ_LAUNCH_STORE(bf16, 64); }
   } else {

@@ -1,0 +1,210 @@
+// SPDX-License-Identifier: Apache-2.0
+// Host-side work planning for the fused KIVI INT4 decode (no GPU code).
+//
+// The decode kernel takes a work list -- items of (request, position range,
+// kind) -- and optionally "pieces", runs of consecutive items that one wave
+// per (piece, kv head) walks in a single pass.  This file builds both from
+// each request's decode geometry, the part of the reference's decode step
+// (pkg/methods/kivi_int4/attention_backend.py:1193-1230) that decides which
+// positions read int4 pages and which read the residual window.  It runs on
+// the host every decode step and every layer, so it is native code: a
+// config-3 batch (32 requests, ~300 items) plans in a few microseconds.
+//
+// Request geometry, int32 [batch, 6]:
+//   {seq_len, k_hist, v_hist, ring_row, k_first_lane, v_first_lane}
+// Output seq_meta, int32 [batch, 8]: the geometry plus {first_work, num_work}.
+// Work items, int32 [num_work, 4]: {request, pos_begin, pos_end, kind}
+//   kind 0: both sides int4; kind 1: the mixed-source tail (64 positions per
+//   item in split plans); kinds 2 / 3: the even / odd 64-position chunks of
+//   an int4 range, issued as a pair at indices 2P, 2P + 1.
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+
+#include "kvq_hip.h"
+
+namespace {
+
+constexpr int kWavesPerCu = 8;          // decode waves resident per CU
+constexpr double kPieceMaxCost = 4096;  // int4 positions per piece before a second round
+constexpr int kTailItemTokens = 64;     // positions per tail item in split plans
+
+struct Planner {
+  const int32_t* seqs;
+  int64_t batch;
+  int32_t* meta;
+  int32_t* work;
+  int64_t cap_work;
+  int64_t n = 0;
+  bool overflow = false;
+
+  int64_t hist_both(int64_t b) const {
+    const int32_t* s = seqs + 6 * b;
+    return std::max<int64_t>(0, std::min({s[1], s[2], s[0]}));
+  }
+  void add(int64_t b, int64_t p, int64_t e, int kind) {
+    if (n >= cap_work) {
+      overflow = true;
+      return;
+    }
+    int32_t* w = work + 4 * n++;
+    w[0] = static_cast<int32_t>(b);
+    w[1] = static_cast<int32_t>(p);
+    w[2] = static_cast<int32_t>(e);
+    w[3] = kind;
+  }
+  void close(int64_t b, int64_t first) {
+    const int32_t* s = seqs + 6 * b;
+    int32_t* m = meta + 8 * b;
+    for (int i = 0; i < 6; ++i) m[i] = s[i];
+    m[6] = static_cast<int32_t>(first);
+    m[7] = static_cast<int32_t>(n - first);
+  }
+};
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int64_t slots_for(int kvh, int cu_count) {
+  return std::max<int64_t>(1, static_cast<int64_t>(cu_count) * kWavesPerCu / std::max(1, kvh));
+}
+
+// Cost of the whole batch in int4-position units: int4 ranges in 64-position
+// tiles, tail positions at `tail_cost` each.
+double total_cost(const Planner& pl, double tail_cost) {
+  double total = 0;
+  for (int64_t b = 0; b < pl.batch; ++b) {
+    const int64_t end_a = pl.hist_both(b);
+    total += static_cast<double>(ceil_div(end_a, 64) * 64) +
+             static_cast<double>(pl.seqs[6 * b] - end_a) * tail_cost;
+  }
+  return total;
+}
+
+// Fixed split: int4 ranges every `split` positions (paired: two items per
+// range of 2 * split, kinds 2 and 3), then tail items of 64 positions.
+void plan_split(Planner& pl, int64_t split, bool paired) {
+  split = std::max<int64_t>(128, ceil_div(split, 128) * 128);
+  for (int64_t b = 0; b < pl.batch; ++b) {
+    const int64_t first = pl.n;
+    const int64_t seq_len = pl.seqs[6 * b];
+    const int64_t end_a = pl.hist_both(b);
+    if (paired && end_a > 0 && pl.n % 2) pl.add(b, 0, 0, 1);  // pairs start at even indices
+    for (int64_t p = 0; p < end_a;) {
+      if (paired) {
+        const int64_t e = std::min(end_a, p + 2 * split);
+        pl.add(b, p, e, 2);
+        pl.add(b, p, e, 3);
+        p = e;
+      } else {
+        const int64_t e = std::min(end_a, p + split);
+        pl.add(b, p, e, 0);
+        p = e;
+      }
+    }
+    for (int64_t p = end_a; p < seq_len;) {
+      const int64_t e = std::min(seq_len, p + kTailItemTokens);
+      pl.add(b, p, e, 1);
+      p = e;
+    }
+    if (seq_len == 0) pl.add(b, 0, 0, 1);
+    pl.close(b, first);
+  }
+}
+
+// Equal-cost pieces: every request's positions laid end to end (int4 in
+// 64-position tiles, tail in 32-position steps at `tail_cost` per position),
+// cut where the running cost crosses a multiple of total / slots.
+int64_t plan_pieces(Planner& pl, int kvh, int cu_count, double tail_cost, int32_t* pieces,
+                    int64_t cap_pieces) {
+  int64_t slots = slots_for(kvh, cu_count);
+  const double total = total_cost(pl, tail_cost);
+  slots *= std::max<int64_t>(
+      1, static_cast<int64_t>(std::ceil(total / (static_cast<double>(slots) * kPieceMaxCost))));
+  const double step = std::max(64.0, total / static_cast<double>(slots));
+  int64_t np = 0;
+  auto push = [&](int64_t v) {
+    if (np >= cap_pieces + 1) {
+      pl.overflow = true;
+      return;
+    }
+    pieces[np++] = static_cast<int32_t>(v);
+  };
+  push(0);
+  double cum = 0.0, cut = step;
+  // close the piece once the running cost reaches the cut
+  auto after = [&](double unit) {
+    if (cum >= cut - unit / 2 && np < slots && pl.n > pieces[np - 1]) {
+      push(pl.n);
+      while (cut - unit / 2 <= cum) cut += step;
+    }
+  };
+  for (int64_t b = 0; b < pl.batch && !pl.overflow; ++b) {
+    const int64_t first = pl.n;
+    const int64_t seq_len = pl.seqs[6 * b];
+    const int64_t end_a = pl.hist_both(b);
+    for (int64_t p = 0; p < end_a;) {
+      const int64_t tiles =
+          std::max<int64_t>(1, static_cast<int64_t>((cut - cum) / 64.0 + 0.5));
+      const int64_t e = std::min(end_a, p + 64 * tiles);
+      pl.add(b, p, e, 0);
+      cum += static_cast<double>(ceil_div(e - p, 64) * 64);
+      p = e;
+      after(64.0);
+    }
+    const double unit = 32 * tail_cost;
+    for (int64_t p = end_a; p < seq_len;) {
+      const int64_t k = std::max<int64_t>(1, static_cast<int64_t>((cut - cum) / unit + 0.5)) * 32;
+      const int64_t e = std::min(seq_len, p + k);
+      pl.add(b, p, e, 1);
+      cum += static_cast<double>(e - p) * tail_cost;
+      p = e;
+      after(unit);
+    }
+    if (seq_len == 0) pl.add(b, 0, 0, 1);
+    pl.close(b, first);
+  }
+  if (pl.n > pieces[np - 1]) push(pl.n);
+  return np - 1;
+}
+
+}  // namespace
+
+extern "C" int64_t kvq_plan_kivi_decode(const int32_t* seqs, int64_t batch, int num_kv_heads,
+                                        int cu_count, int mode, int64_t split_tokens,
+                                        double tail_cost, int32_t* seq_meta, int32_t* work,
+                                        int64_t cap_work, int32_t* pieces, int64_t cap_pieces,
+                                        int64_t* num_pieces) {
+  if (batch < 0 || (batch > 0 && (!seqs || !seq_meta || !work)) || !num_pieces ||
+      num_kv_heads <= 0 || cu_count <= 0 || cap_work < 0 || tail_cost <= 0)
+    return KVQ_ERR_INVALID;
+  *num_pieces = 0;
+  Planner pl{seqs, batch, seq_meta, work, cap_work};
+  if (mode == KVQ_PLAN_DEFAULT) {
+    const int64_t slots = slots_for(num_kv_heads, cu_count);
+    if (total_cost(pl, tail_cost) <= static_cast<double>(slots) * kPieceMaxCost) {
+      mode = KVQ_PLAN_PIECES;
+    } else {
+      // paired items: each wave still takes split_tokens int4 positions
+      int64_t positions = 0;
+      for (int64_t b = 0; b < batch; ++b) positions += seqs[6 * b];
+      const int64_t per_item = ceil_div(ceil_div(positions, slots), 128) * 128;
+      split_tokens = std::min<int64_t>(4096, std::max<int64_t>(256, per_item));
+      mode = KVQ_PLAN_SPLIT_PAIRED;
+    }
+  }
+  switch (mode) {
+    case KVQ_PLAN_PIECES:
+      if (!pieces || cap_pieces <= 0) return KVQ_ERR_INVALID;
+      *num_pieces = plan_pieces(pl, num_kv_heads, cu_count, tail_cost, pieces, cap_pieces);
+      break;
+    case KVQ_PLAN_SPLIT:
+    case KVQ_PLAN_SPLIT_PAIRED:
+      if (split_tokens <= 0) return KVQ_ERR_INVALID;
+      plan_split(pl, split_tokens, mode == KVQ_PLAN_SPLIT_PAIRED);
+      break;
+    default:
+      return KVQ_ERR_INVALID;
+  }
+  if (pl.overflow) return KVQ_ERR_CAPACITY;
+  return pl.n;
+}

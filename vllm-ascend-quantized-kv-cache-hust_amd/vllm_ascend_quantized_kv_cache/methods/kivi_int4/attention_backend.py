@@ -20,6 +20,7 @@ from __future__ import annotations
 from contextlib import contextmanager
 from typing import Any
 
+import numpy as np
 import torch
 
 from .byte_cache import kivi_byte_cache_layout, kivi_caches_from_byte_tensors
@@ -95,6 +96,10 @@ class AscendKiviInt4AttentionBackendMixin:
         self.kivi_residual_req_to_row: dict[str, int] = {}
         self.kivi_residual_row_to_req: list[str | None] = []
         self.kivi_residual_free_rows: list[int] = []
+        # device-to-host reads of step metadata (0 while the host supplies
+        # its own copies of slot_mapping and block_tables)
+        self.kivi_host_reads = 0
+        self._kivi_step_bufs = None
 
     def _validate_kivi_geometry(self) -> None:
         validate_kivi_geometry(
@@ -387,11 +392,25 @@ class AscendKiviInt4AttentionBackendMixin:
             prev = q_end
         return spans, len(actual_seq_qlen)
 
+    @staticmethod
+    def _span_positions(start: int, end: int, rows: list[int], seq_lens: Any,
+                        i: int) -> list[int] | None:
+        """Positions of a request's tokens when its length is known: the
+        step's ``end - start`` tokens are the request's last ones."""
+        if seq_lens is None or i >= len(seq_lens):
+            return None
+        first = int(seq_lens[i]) - (end - start)
+        return [first + t - start for t in rows]
+
     def _write_kivi_cache(
         self, key: Any, value: Any, slot_mapping: Any, req_ids: list[str] | None,
-        actual_seq_qlen: list[int] | Any,
+        actual_seq_qlen: list[int] | Any, seq_lens: Any = None,
     ) -> None:
-        """Token-by-token residual writes for every request of the step (``ab.py:562-606``)."""
+        """Token-by-token residual writes for every request of the step (``ab.py:562-606``).
+
+        ``seq_lens`` (optional) gives each request's length after the step, so
+        the mirror records every window token's position.
+        """
         if key is None or value is None or slot_mapping is None:
             return
         spans, num_reqs = self._request_spans(slot_mapping, actual_seq_qlen)
@@ -412,15 +431,16 @@ class AscendKiviInt4AttentionBackendMixin:
                     continue
                 row = self._get_kivi_residual_row(keys[i], create=True)
                 req_slots = [slots[t] for t in rows]
+                pos = self._span_positions(start, end, rows, seq_lens, i)
                 ring.plan_store(plan, row, req_slots, rows, is_key=True,
-                                block_size=bs, group_size=g)
+                                block_size=bs, group_size=g, positions=pos)
                 ring.plan_store(plan, row, req_slots, rows, is_key=False,
-                                block_size=bs, group_size=g)
+                                block_size=bs, group_size=g, positions=pos)
             self._execute_kivi_plan(plan, key, value)
 
     def _write_kivi_prefill_cache(
         self, key: Any, value: Any, slot_mapping: Any, req_ids: list[str] | None,
-        actual_seq_qlen: list[int] | Any,
+        actual_seq_qlen: list[int] | Any, seq_lens: Any = None,
     ) -> None:
         """Bulk prefill: ``floor(n/R)*R`` tokens straight to history, the rest to the window.
 
@@ -457,10 +477,11 @@ class AscendKiviInt4AttentionBackendMixin:
                     row = self._get_kivi_residual_row(keys[i], create=True)
                     rest = rows[flush:]
                     rest_slots = [slots[t] for t in rest]
+                    pos = self._span_positions(start, end, rest, seq_lens, i)
                     ring.plan_store(plan, row, rest_slots, rest, is_key=True, block_size=bs,
-                                    group_size=g)
+                                    group_size=g, positions=pos)
                     ring.plan_store(plan, row, rest_slots, rest, is_key=False, block_size=bs,
-                                    group_size=g)
+                                    group_size=g, positions=pos)
             self._execute_kivi_plan(plan, key, value)
 
     def _check_key_flush(self, key: Any, slots: list[int]) -> None:
@@ -635,42 +656,83 @@ class AscendKiviInt4AttentionBackendMixin:
     # per-step window sync (ab.py:813-836)
     # ------------------------------------------------------------------
 
+    def _host_table(self, block_table: Any) -> np.ndarray:
+        """The block table as a host int64 array (one device read when the
+        caller hands over a device tensor)."""
+        if isinstance(block_table, torch.Tensor):
+            if block_table.device.type != "cpu":
+                self.kivi_host_reads += 1
+                block_table = block_table.cpu()
+            return block_table.numpy().astype(np.int64, copy=False)
+        return np.asarray(block_table, dtype=np.int64)
+
+    def _host_array(self, attn_metadata: Any, name: str) -> np.ndarray:
+        """A metadata field as a host array, preferring the host's own copy
+        ``<name>_cpu`` (vLLM builds every step's slot mapping and block
+        table on the host before copying them to the device), so that a
+        step reads nothing back from the device."""
+        host = getattr(attn_metadata, f"{name}_cpu", None)
+        x = host if host is not None else getattr(attn_metadata, name)
+        if isinstance(x, torch.Tensor):
+            if x.device.type != "cpu":
+                self.kivi_host_reads += 1
+                x = x.cpu()
+            return x.numpy()
+        return np.asarray(x)
+
     def _sync_kivi_residual_windows(
         self, block_table: Any, seq_lens: list[int], req_ids: list[str] | None,
         finished_req_ids: set[str] | None = None,
     ) -> None:
-        """Release finished rows and drop window entries a request no longer owns."""
+        """Release finished rows and drop window entries a request no longer owns.
+
+        An entry is live when the first table column holding its block, times
+        the block size plus its offset, is below the request's length
+        (``ab.py:813-836``).  Entries whose recorded position still maps to
+        their slot are live (``KiviResidualRing.suspect_rows``); only the
+        windows with other entries are checked entry by entry.
+        """
         keys = self._get_kivi_req_keys(req_ids, len(seq_lens))
         if finished_req_ids:
             self._release_finished_kivi_residual_rows({str(r) for r in finished_req_ids})
         ring = self._ensure_kivi_residual_buffers()
         bs = self._get_kivi_block_size()
-        table: list[list[int]] | None = None
-        for i, n in enumerate(seq_lens):
-            row = self._get_kivi_residual_row(keys[i], create=False)
-            if row is None:
-                continue
-            if ring.length[True][row] == 0 and ring.length[False][row] == 0:
-                continue
-            if table is None:
-                table = (block_table.to("cpu", torch.long).tolist()
-                         if isinstance(block_table, torch.Tensor)
-                         else [list(r) for r in block_table])
-            cols: dict[int, int] = {}
-            for c, blk in enumerate(table[i] if i < len(table) else []):
-                if int(blk) >= 0 and int(blk) not in cols:
-                    cols[int(blk)] = c
-            n = int(n)
+        idx, rows = [], []
+        for i, key in enumerate(keys):
+            row = self.kivi_residual_req_to_row.get(key)
+            if row is not None and (ring.length[True][row] or ring.length[False][row]):
+                idx.append(i)
+                rows.append(row)
+        if not rows:
+            return
+        table = self._host_table(block_table)
+        lens = np.asarray([int(seq_lens[i]) for i in idx], dtype=np.int64)
+        sub = np.full((len(idx), max(1, table.shape[1] if table.ndim == 2 else 1)), -1,
+                      dtype=np.int64)
+        for j, i in enumerate(idx):
+            if i < len(table):
+                sub[j, : table.shape[1]] = table[i]
+        for j in ring.suspect_rows(np.asarray(rows), lens, sub, bs).tolist():
+            self._check_window_entries(rows[j], sub[j], int(lens[j]), bs)
 
-            def live(slot: int) -> bool:
+    def _check_window_entries(self, row: int, table_row: np.ndarray, n: int, bs: int) -> None:
+        """The reference's per-entry liveness rule for one request's windows;
+        live entries get their position recorded, dead ones are dropped."""
+        ring = self._kivi_ring
+        cols: dict[int, int] = {}
+        for c, blk in enumerate(table_row.tolist()):
+            if blk >= 0 and blk not in cols:
+                cols[blk] = c
+        for is_key in (True, False):
+            keep = set()
+            for lane in ring.lanes(row, is_key=is_key):
+                slot = int(ring.lane_slot[is_key][row, lane])
                 c = cols.get(slot // bs)
-                return c is not None and c * bs + slot % bs < n
-
-            for is_key in (True, False):
-                held = ring.window_slots(row, is_key=is_key)
-                keep = {s for s in held if live(s)}
-                if len(keep) != len(held):
-                    self._compact_kivi_window(row, keep, is_key=is_key)
+                if c is not None and c * bs + slot % bs < n:
+                    keep.add(slot)
+                    ring.lane_pos[is_key][row, lane] = c * bs + slot % bs
+            if len(keep) != int(ring.length[is_key][row]):
+                self._compact_kivi_window(row, keep, is_key=is_key)
 
     def _clear_stale_kivi_residual_entries(self, req_key: str, live_slots: set[int], *,
                                            is_key: bool) -> None:
@@ -698,17 +760,22 @@ class AscendKiviInt4AttentionBackendMixin:
     # gather + overlay (ab.py:849-935)
     # ------------------------------------------------------------------
 
-    def _ring_meta_rows(self, seq_lens: list[int], req_keys: list[str]) -> list[list[int]]:
+    def _request_rows(self, req_keys: list[str]) -> np.ndarray:
+        """Ring row per request, -1 for requests without one."""
+        get = self.kivi_residual_req_to_row.get
+        return np.asarray([get(k, -1) for k in req_keys], dtype=np.int64)
+
+    def _ring_meta_rows(self, seq_lens: list[int], req_keys: list[str]) -> np.ndarray:
+        """``[row, k_first, k_tail, v_first, v_tail]`` per request (int32)."""
         ring = self._kivi_ring
-        meta = []
-        for i, n in enumerate(seq_lens):
-            row = self._get_kivi_residual_row(req_keys[i], create=False)
-            if row is None:
-                meta.append([0, 0, 0, 0, 0])
-                continue
-            kt, kf = ring.tail(row, int(n), is_key=True)
-            vt, vf = ring.tail(row, int(n), is_key=False)
-            meta.append([row, kf, kt, vf, vt])
+        lens = np.asarray([int(n) for n in seq_lens], dtype=np.int64)
+        rows = self._request_rows(req_keys)
+        meta = np.zeros((lens.size, 5), dtype=np.int32)
+        have = rows >= 0
+        if have.any():
+            kt, kf = ring.tails(rows[have], lens[have], is_key=True)
+            vt, vf = ring.tails(rows[have], lens[have], is_key=False)
+            meta[have] = np.stack([rows[have], kf, kt, vf, vt], axis=1)
         return meta
 
     def _gather_dequant_kivi_paged_cache(
@@ -728,7 +795,7 @@ class AscendKiviInt4AttentionBackendMixin:
             num_blocks=self.k_quant_cache.shape[0], block_size=self._get_kivi_block_size(),
         )
         keys = self._get_kivi_req_keys(req_ids, batch)
-        meta = torch.tensor(self._ring_meta_rows(lens, keys), dtype=torch.int32).to(dev)
+        meta = torch.from_numpy(self._ring_meta_rows(lens, keys)).to(dev)
         cu = [0]
         for n in lens:
             cu.append(cu[-1] + n)
@@ -739,21 +806,29 @@ class AscendKiviInt4AttentionBackendMixin:
     # attention paths (ab.py:937-1392)
     # ------------------------------------------------------------------
 
+    def _decode_seq_array(self, seq_lens: Any, req_keys: list[str]) -> np.ndarray:
+        """Decode geometry per request, int32 ``[B, 6]`` = ``{seq_len, k_hist,
+        v_hist, ring_row, k_first, v_first}`` (no ring row: all int4)."""
+        ring = self._kivi_ring
+        lens = np.asarray([int(n) for n in seq_lens], dtype=np.int64)
+        rows = self._request_rows(req_keys)
+        out = np.zeros((lens.size, 6), dtype=np.int32)
+        out[:, 0] = out[:, 1] = out[:, 2] = lens
+        have = rows >= 0
+        if have.any():
+            kt, kf = ring.tails(rows[have], lens[have], is_key=True)
+            vt, vf = ring.tails(rows[have], lens[have], is_key=False)
+            out[have, 1] = lens[have] - kt
+            out[have, 2] = lens[have] - vt
+            out[have, 3] = rows[have]
+            out[have, 4] = kf
+            out[have, 5] = vf
+        return out
+
     def _decode_seqs(self, seq_lens: list[int], req_keys: list[str]) -> list:
         from ...ops.kivi_decode import DecodeSeq
 
-        ring = self._kivi_ring
-        seqs = []
-        for i, n in enumerate(seq_lens):
-            n = int(n)
-            row = self._get_kivi_residual_row(req_keys[i], create=False)
-            if row is None:
-                seqs.append(DecodeSeq(n, n, n))
-                continue
-            kt, kf = ring.tail(row, n, is_key=True)
-            vt, vf = ring.tail(row, n, is_key=False)
-            seqs.append(DecodeSeq(n, n - kt, n - vt, row, kf, vf))
-        return seqs
+        return [DecodeSeq(*map(int, r)) for r in self._decode_seq_array(seq_lens, req_keys)]
 
     def _is_kivi_chunked_prefill_all_new(self, attn_metadata: Any) -> bool:
         qlen = attn_metadata.actual_seq_lengths_q
@@ -820,6 +895,7 @@ class AscendKiviInt4AttentionBackendMixin:
             self._write_kivi_prefill_cache(
                 key[:n], value[:n], attn_metadata.slot_mapping[:n], req_ids,
                 attn_metadata.actual_seq_lengths_q,
+                KiviInt4Semantics.cu_seqlens_to_seq_lens(attn_metadata.actual_seq_lengths_q),
             )
             return self._forward_kivi_prefill(query, key, value, attn_metadata, output)
 
@@ -832,10 +908,14 @@ class AscendKiviInt4AttentionBackendMixin:
 
         seq_lens = attn_metadata.seq_lens_list
         if state == "DecodeOnly":
+            if self._kivi_step_enabled(query, key, value):
+                done = self._forward_kivi_decode_step(query, key, value, attn_metadata, output)
+                if done is not None:
+                    return done
             if key is not None and value is not None and actual(key) > 0:
                 n = actual(key)
                 self._write_kivi_cache(key[:n], value[:n], attn_metadata.slot_mapping[:n],
-                                       req_ids, list(range(1, len(seq_lens) + 1)))
+                                       req_ids, list(range(1, len(seq_lens) + 1)), seq_lens)
             self._sync_kivi_residual_windows(attn_metadata.block_tables, seq_lens, req_ids,
                                              finished)
             return self._forward_kivi_paged_decode_attention(
@@ -852,13 +932,14 @@ class AscendKiviInt4AttentionBackendMixin:
                     self._write_kivi_cache(
                         key[:nd], value[:nd], slot_mapping[:nd],
                         None if req_ids is None else req_ids[:ndr], list(range(1, ndr + 1)),
+                        seq_lens[:ndr],
                     )
                 if nd < n:
                     pq = [int(attn_metadata.actual_seq_lengths_q[i]) - nd
                           for i in range(ndr, len(attn_metadata.actual_seq_lengths_q))]
                     self._write_kivi_prefill_cache(
                         key[nd:n], value[nd:n], slot_mapping[nd:n],
-                        None if req_ids is None else req_ids[ndr:], pq,
+                        None if req_ids is None else req_ids[ndr:], pq, seq_lens[ndr:],
                     )
             self._sync_kivi_residual_windows(attn_metadata.block_tables, seq_lens, req_ids,
                                              finished)
@@ -867,7 +948,7 @@ class AscendKiviInt4AttentionBackendMixin:
         if key is not None and value is not None and actual(key) > 0:
             n = actual(key)
             self._write_kivi_cache(key[:n], value[:n], attn_metadata.slot_mapping[:n], req_ids,
-                                   attn_metadata.actual_seq_lengths_q)
+                                   attn_metadata.actual_seq_lengths_q, seq_lens)
         self._sync_kivi_residual_windows(attn_metadata.block_tables, seq_lens, req_ids,
                                          finished)
         dense_k, dense_v = self._gather_dequant_kivi_paged_cache(
@@ -876,6 +957,141 @@ class AscendKiviInt4AttentionBackendMixin:
         return self._forward_kivi_dense_attention(
             query, dense_k, dense_v, seq_lens, qlen, attn_metadata.causal, output
         )
+
+    # ------------------------------------------------------------------
+    # decode step from a host plan (sync-free, capturable launches)
+    # ------------------------------------------------------------------
+
+    def _kivi_step_enabled(self, query: Any, key: Any, value: Any) -> bool:
+        """The planned decode step applies: GPU tensors, none of the launch
+        hooks replaced, and a geometry the planned store and the pieces
+        decode cover."""
+        from .decode_step import step_geometry_ok
+
+        hooks = ("_launch_kivi_key_pack", "_launch_kivi_value_pack",
+                 "_launch_kivi_key_pack_rows", "_launch_kivi_value_pack_rows",
+                 "_launch_kivi_ring_write", "_launch_kivi_store", "_launch_kivi_decode")
+        if any(_hook_replaced(self, h) for h in hooks):
+            return False
+        if not isinstance(query, torch.Tensor) or query.device.type != "cuda":
+            return False
+        self._check_kivi_cache_bound()
+        if key is not None and value is not None:
+            self._adopt_ring_dtype(key, value)
+        else:
+            self._ensure_kivi_residual_buffers()
+        return step_geometry_ok(self, query)
+
+    def _plan_kivi_decode_step(self, attn_metadata: Any, key: Any, value: Any, *,
+                               allow_compaction: bool = True):
+        """Host half of a decode step: ``(jobs, seqs, block_table)`` or ``None``.
+
+        Validates the block table, replays the window rules for one token per
+        request on the mirror (``KiviResidualRing.plan_decode_step``) and
+        returns the store jobs, the decode geometry (int32 ``[B, 6]``) and the
+        device block table.  Reads nothing from the device when the metadata
+        carries host copies (``slot_mapping_cpu``, ``block_tables_cpu``).
+
+        Returns ``None`` with nothing changed when the step needs the general
+        path: several tokens for a request, padding slots, a slot that does
+        not follow the table at the request's last position, or a window
+        entry that may no longer be live (its check, and any compaction,
+        belongs after the store, which the general path orders).
+        """
+        from ...ops.kivi_layout import check_gather_metadata_host
+
+        ring = self._ensure_kivi_residual_buffers()
+        bs = self._get_kivi_block_size()
+        lens = np.asarray([int(x) for x in attn_metadata.seq_lens_list], dtype=np.int64)
+        b = lens.size
+        keys = self._get_kivi_req_keys(getattr(attn_metadata, "req_ids", None), b)
+        table = self._host_array(attn_metadata, "block_tables")[:b].astype(np.int64, copy=False)
+        check_gather_metadata_host(table, lens.tolist(), max_blocks=table.shape[1],
+                                   num_blocks=self.k_quant_cache.shape[0], block_size=bs)
+        n = 0
+        if key is not None and value is not None:
+            n = min(int(getattr(attn_metadata, "num_actual_tokens", key.shape[0])), key.shape[0])
+        slots = pos = None
+        if n:
+            if n != b:
+                return None
+            slots = self._host_array(attn_metadata, "slot_mapping")[:n].astype(np.int64)
+            pos = lens - 1
+            col = pos // bs
+            if (slots < 0).any() or (pos < 0).any() or (col >= table.shape[1]).any():
+                return None
+            if ((table[np.arange(b), col] != slots // bs).any()
+                    or (slots % bs != pos % bs).any()):
+                return None
+        rows = self._request_rows(keys)
+        have = rows >= 0
+        if have.any() and ring.suspect_rows(rows[have], lens[have], table[have], bs).size:
+            if not allow_compaction:
+                raise RuntimeError(
+                    "KIVI decode step: a window entry may no longer be live; run this "
+                    "step eagerly (forward) so its check follows the store."
+                )
+            return None
+        jobs = None
+        if n:
+            with self._kivi_planning():
+                rows = np.asarray([self._get_kivi_residual_row(k, create=True) for k in keys],
+                                  dtype=np.int64)
+                jobs = ring.plan_decode_step(rows, slots, pos, np.arange(b, dtype=np.int64),
+                                             block_size=bs, group_size=self.kivi_group_size)
+            if jobs is None:
+                if not allow_compaction:
+                    raise RuntimeError("KIVI decode step: a slot is already held; run eagerly.")
+                return None
+        seqs = self._decode_seq_array(lens, keys)
+        return jobs, seqs, attn_metadata.block_tables[:b]
+
+    def _forward_kivi_decode_step(self, query: Any, key: Any, value: Any, attn_metadata: Any,
+                                  output: Any) -> Any:
+        """The decode step as two launches over one staged plan, or ``None``
+        (nothing changed) when it needs the general path."""
+        from ...ops.kivi_decode import _cu_count
+        from .decode_step import DecodeStepBuffers, KiviDecodeLauncher, eager_capacities
+
+        plan = self._plan_kivi_decode_step(attn_metadata, key, value)
+        if plan is None:
+            return None
+        jobs, seqs, table_dev = plan
+        b = seqs.shape[0]
+        dev = query.device
+        cu = _cu_count(dev)
+        work_cap, pieces_cap = eager_capacities(b, self.num_kv_heads, cu, seqs)
+        bufs = self._kivi_step_bufs
+        if bufs is None or not bufs.fits(b, work_cap, pieces_cap):
+            # grow with headroom so a serving loop settles on one buffer
+            bufs = DecodeStepBuffers(dev, batch=max(b, 2 * (bufs.batch if bufs else 0), 8),
+                                     window=self.kivi_residual_length, num_heads=self.num_heads,
+                                     head_size=self.head_size, work_cap=2 * work_cap,
+                                     pieces_cap=2 * pieces_cap)
+            self._kivi_step_bufs = bufs
+        from ...ops import _native
+
+        staged = bufs.stage(jobs, seqs, num_kv_heads=self.num_kv_heads, cu_count=cu,
+                            mode=_native.KVQ_PLAN_DEFAULT, fixed=False)
+        launcher = KiviDecodeLauncher(self)
+        if jobs is not None:
+            ring = self._kivi_ring
+            kin = key[:b].reshape(b, self.num_kv_heads, self.head_size).to(ring.dtype).contiguous()
+            vin = value[:b].reshape(b, self.num_kv_heads, self.head_size).to(ring.dtype).contiguous()
+            launcher.store(bufs, staged, kin, vin)
+        q = query[:b].reshape(b, self.num_heads, self.head_size).contiguous()
+        out = output[:b].view(b, self.num_heads, self.head_size)
+        table = table_dev.to(device=dev, dtype=torch.int32).contiguous()
+        launcher.decode(bufs, staged, q, table, out)
+        return output
+
+    def kivi_decode_graph(self, batch: int, *, max_blocks: int, rounds: int = 1):
+        """A ``KiviDecodeGraph`` for this layer: the decode step's launches,
+        capturable once in a HIP graph and replayed every step after
+        ``prepare`` stages that step's plan."""
+        from .decode_step import KiviDecodeGraph
+
+        return KiviDecodeGraph(self, batch, max_blocks=max_blocks, rounds=rounds)
 
     def _forward_kivi_paged_decode_attention(
         self, query: Any, block_table: Any, seq_lens: list[int], req_ids: list[str] | None,

@@ -17,6 +17,13 @@ A row has ``R + 1`` lanes for a window of ``R`` tokens: the free lane is where
 the next token goes, so a step that evicts and appends never writes the lane
 it packs, and the whole step can run as one launch.
 
+The mirror is a set of numpy arrays (start, length, slot and token position
+per lane), so a decode step -- one new token for each of a batch of requests
+-- is planned for the whole batch at once (``plan_decode_step``), and the
+per-step check that every window entry is still live needs a per-entry look
+only where the token's recorded position no longer maps to its slot
+(``suspect_rows``).
+
 Replaying a batch of tokens yields a ``StorePlan``: packed-history writes
 (sources are old ring lanes or rows of this step's input) and final ring-lane
 writes.  ``execute`` issues them as one launch when no ring write of the batch
@@ -30,9 +37,13 @@ from __future__ import annotations
 from contextlib import contextmanager
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from ...ops.kivi_layout import key_slot_groups_error
+
+_SIDES = (True, False)
+_FLUSH_ERROR = "KIVI key flush requires contiguous aligned token groups."
 
 
 @dataclass
@@ -79,10 +90,33 @@ class StorePlan:
         return jobs, (len(k.pack_src), len(v.pack_src), len(k.ring), len(v.ring))
 
 
+@dataclass
+class StepJobs:
+    """A decode step's store work (one token per request), as int64 arrays.
+
+    Pack sources index ``[ring rows ; input rows]``; ring sources are input
+    rows and ring destinations ring rows.  No ring destination is a pack
+    source of the same side, so the whole step is one launch.
+    """
+
+    key_pack_src: np.ndarray
+    key_pack_slot: np.ndarray
+    value_pack_src: np.ndarray
+    value_pack_slot: np.ndarray
+    key_ring_src: np.ndarray
+    key_ring_dst: np.ndarray
+    value_ring_src: np.ndarray
+    value_ring_dst: np.ndarray
+
+
 class KiviResidualRing:
     """Ring tensors ``[rows, R + 1, KVH, D]`` (keys, values) plus their host mirror.
 
     ``window`` is the residual length ``R``; ``ring_len = R + 1`` lanes per row.
+    Mirror arrays, per side (``True`` = keys): ``start[side][row]``,
+    ``length[side][row]``, ``lane_slot[side][row, lane]`` (-1 when free) and
+    ``lane_pos[side][row, lane]`` (the token's position in its request, -1
+    when the writer did not know it).
     """
 
     def __init__(
@@ -105,14 +139,10 @@ class KiviResidualRing:
         self.key = torch.zeros((rows, ring_len, num_kv_heads, head_size), dtype=dtype, device=device)
         self.value = torch.zeros_like(self.key)
         self.written = False
-        self.start = {True: [0] * rows, False: [0] * rows}
-        self.length = {True: [0] * rows, False: [0] * rows}
-        self.lane_slot = {True: [[-1] * ring_len for _ in range(rows)],
-                          False: [[-1] * ring_len for _ in range(rows)]}
-        self.slot_lane: dict[bool, list[dict[int, int]]] = {
-            True: [dict() for _ in range(rows)],
-            False: [dict() for _ in range(rows)],
-        }
+        self.start = {s: np.zeros(rows, dtype=np.int64) for s in _SIDES}
+        self.length = {s: np.zeros(rows, dtype=np.int64) for s in _SIDES}
+        self.lane_slot = {s: np.full((rows, ring_len), -1, dtype=np.int64) for s in _SIDES}
+        self.lane_pos = {s: np.full((rows, ring_len), -1, dtype=np.int64) for s in _SIDES}
         self._saved: dict[int, tuple] | None = None
 
     # -- all-or-nothing planning ----------------------------------------------
@@ -143,17 +173,25 @@ class KiviResidualRing:
     def _touch(self, row: int) -> None:
         if self._saved is not None and row not in self._saved:
             self._saved[row] = tuple(
-                (self.start[k][row], self.length[k][row], list(self.lane_slot[k][row]),
-                 dict(self.slot_lane[k][row]))
-                for k in (True, False)
+                (int(self.start[k][row]), int(self.length[k][row]),
+                 self.lane_slot[k][row].copy(), self.lane_pos[k][row].copy())
+                for k in _SIDES
             )
 
     def _restore(self, row: int, state: tuple) -> None:
-        for k, (start, length, ls, sl) in zip((True, False), state):
+        for k, (start, length, ls, lp) in zip(_SIDES, state):
             self.start[k][row] = start
             self.length[k][row] = length
             self.lane_slot[k][row] = ls
-            self.slot_lane[k][row] = sl
+            self.lane_pos[k][row] = lp
+
+    def state(self) -> tuple:
+        """The whole mirror as nested tuples of ints (for comparisons)."""
+        return tuple(
+            (tuple(self.start[k].tolist()), tuple(self.length[k].tolist()),
+             tuple(map(tuple, self.lane_slot[k].tolist())))
+            for k in _SIDES
+        )
 
     # -- dtype ----------------------------------------------------------------
 
@@ -184,16 +222,16 @@ class KiviResidualRing:
 
     def lanes(self, row: int, *, is_key: bool) -> list[int]:
         """Occupied lanes of ``row`` in FIFO order (wrapping past R)."""
-        n = self.length[is_key][row]
-        s = self.start[is_key][row]
+        n = int(self.length[is_key][row])
+        s = int(self.start[is_key][row])
         return [(s + i) % self.ring_len for i in range(n)]
 
     def window_slots(self, row: int, *, is_key: bool) -> list[int]:
         ls = self.lane_slot[is_key][row]
-        return [ls[lane] for lane in self.lanes(row, is_key=is_key)]
+        return [int(ls[lane]) for lane in self.lanes(row, is_key=is_key)]
 
     def holds(self, row: int, slot: int, *, is_key: bool) -> bool:
-        return slot in self.slot_lane[is_key][row]
+        return bool((self.lane_slot[is_key][row] == slot).any())
 
     def tail(self, row: int, seq_len: int, *, is_key: bool) -> tuple[int, int]:
         """``(tail_len, first_lane)`` of the overlay for a sequence of ``seq_len``.
@@ -201,20 +239,74 @@ class KiviResidualRing:
         The last ``min(seq_len, len)`` window entries replace the sequence's
         last positions (``attention_backend.py:899-923``).
         """
-        n = self.length[is_key][row]
-        t = min(seq_len, n)
-        first = (self.start[is_key][row] + n - t) % self.ring_len
+        n = int(self.length[is_key][row])
+        t = min(int(seq_len), n)
+        first = (int(self.start[is_key][row]) + n - t) % self.ring_len
         return t, first
+
+    def tails(self, rows: np.ndarray, seq_lens: np.ndarray, *, is_key: bool
+              ) -> tuple[np.ndarray, np.ndarray]:
+        """``tail`` for many rows at once: ``(tail_len, first_lane)`` arrays."""
+        n = self.length[is_key][rows]
+        t = np.minimum(seq_lens, n)
+        first = (self.start[is_key][rows] + n - t) % self.ring_len
+        return t, first
+
+    def suspect_rows(self, rows: np.ndarray, seq_lens: np.ndarray, table: np.ndarray,
+                     block_size: int) -> np.ndarray:
+        """Indices into ``rows`` whose windows need the per-entry liveness check.
+
+        An entry written at position ``p`` with slot ``s`` is live for the
+        reference (``attention_backend.py:813-836``: the first column holding
+        ``s``'s block, times the block size plus ``s``'s offset, is below the
+        sequence length) whenever ``p < seq_len`` and the request's table
+        still has ``s``'s block at column ``p // block_size``: that column is
+        then the first holder or comes after it.  Rows where some entry fails
+        this test (or has no recorded position) are returned; every entry of
+        the other rows is live.
+        """
+        if rows.size == 0:
+            return np.zeros(0, dtype=np.int64)
+        suspect = np.zeros(rows.shape[0], dtype=bool)
+        maxb = table.shape[1]
+        n = seq_lens[:, None]
+        req = np.arange(rows.shape[0])[:, None]
+        for k in _SIDES:
+            ls = self.lane_slot[k][rows]
+            lp = self.lane_pos[k][rows]
+            occ = ls >= 0
+            col = lp // block_size
+            ok = (lp >= 0) & (lp < n) & (col < maxb)
+            tb = table[req, np.clip(col, 0, maxb - 1)]
+            ok &= tb == ls // block_size
+            suspect |= (occ & ~ok).any(axis=1)
+        return np.flatnonzero(suspect)
 
     # -- mutation ----------------------------------------------------------
 
+    def load_row(self, row: int, *, is_key: bool, slots: list[int],
+                 positions: list[int] | None = None) -> None:
+        """Describe a window the caller wrote to lanes ``0..len(slots)-1`` itself
+        (a state restored or built outside the store path)."""
+        n = len(slots)
+        if n > self.window:
+            raise ValueError(f"a window holds at most {self.window} tokens, got {n}")
+        self._touch(row)
+        self.start[is_key][row] = 0
+        self.length[is_key][row] = n
+        self.lane_slot[is_key][row] = -1
+        self.lane_pos[is_key][row] = -1
+        self.lane_slot[is_key][row, :n] = slots
+        if positions is not None:
+            self.lane_pos[is_key][row, :n] = positions
+
     def reset_row(self, row: int) -> None:
         self._touch(row)
-        for is_key in (True, False):
+        for is_key in _SIDES:
             self.start[is_key][row] = 0
             self.length[is_key][row] = 0
-            self.lane_slot[is_key][row] = [-1] * self.ring_len
-            self.slot_lane[is_key][row] = {}
+            self.lane_slot[is_key][row] = -1
+            self.lane_pos[is_key][row] = -1
 
     def keep_only(self, row: int, keep_slots: set[int], *, is_key: bool) -> list[tuple[int, int]]:
         """Drop lanes whose slot is not in ``keep_slots``; compact to lane 0.
@@ -226,17 +318,18 @@ class KiviResidualRing:
         self._touch(row)
         lanes = self.lanes(row, is_key=is_key)
         ls = self.lane_slot[is_key][row]
-        kept = [lane for lane in lanes if ls[lane] in keep_slots]
+        lp = self.lane_pos[is_key][row]
+        kept = [lane for lane in lanes if int(ls[lane]) in keep_slots]
         if len(kept) == len(lanes):
             return []
-        slots = [ls[lane] for lane in kept]
+        slots = ls[kept].copy()
+        pos = lp[kept].copy()
         self.start[is_key][row] = 0
         self.length[is_key][row] = len(kept)
-        new_ls = [-1] * self.ring_len
-        for i, s in enumerate(slots):
-            new_ls[i] = s
-        self.lane_slot[is_key][row] = new_ls
-        self.slot_lane[is_key][row] = {s: i for i, s in enumerate(slots)}
+        ls[:] = -1
+        lp[:] = -1
+        ls[: len(kept)] = slots
+        lp[: len(kept)] = pos
         return [(i, src) for i, src in enumerate(kept) if i != src]
 
     def plan_store(
@@ -249,13 +342,15 @@ class KiviResidualRing:
         is_key: bool,
         block_size: int,
         group_size: int,
+        positions: list[int] | None = None,
     ) -> None:
         """Replay ``_store_kivi_residual_entries`` for one request and side.
 
         ``input_rows[i]`` is the row (in the step's input) of the token with
-        slot ``slots[i]``.  Updates the mirror and appends the device work to
-        ``plan``; raises before any launch if a key flush would break the
-        pack kernel's aligned-group contract.
+        slot ``slots[i]``, and ``positions[i]`` its position in the request
+        when the caller knows it.  Updates the mirror and appends the device
+        work to ``plan``; raises before any launch if a key flush would break
+        the pack kernel's aligned-group contract.
 
         A run of distinct slots none of which the window holds (a prompt
         chunk, a decode token) is planned in closed form (``_plan_run``);
@@ -263,16 +358,28 @@ class KiviResidualRing:
         the same plan and mirror.
         """
         self._touch(row)
-        if len(slots) > 1 and self.slot_lane[is_key][row].keys().isdisjoint(slots) \
-                and len(set(slots)) == len(slots):
-            self._plan_run(plan, row, slots, input_rows, is_key=is_key,
+        if len(slots) > 1 and len(set(slots)) == len(slots) and not np.isin(
+                self.lane_slot[is_key][row], slots).any():
+            self._plan_run(plan, row, slots, input_rows, positions, is_key=is_key,
                            block_size=block_size, group_size=group_size)
         else:
-            self._plan_tokens(plan, row, slots, input_rows, is_key=is_key,
+            self._plan_tokens(plan, row, slots, input_rows, positions, is_key=is_key,
                               block_size=block_size, group_size=group_size)
 
-    def _plan_run(self, plan: StorePlan, row: int, slots: list[int], input_rows: list[int], *,
-                  is_key: bool, block_size: int, group_size: int) -> None:
+    def _evict(self, side: SideWrites, row: int, ev: list[int], *, is_key: bool) -> None:
+        base = row * self.ring_len
+        ls = self.lane_slot[is_key][row]
+        side.pack_src.extend(side.lane_src.get(base + lane, base + lane) for lane in ev)
+        side.pack_slots.extend(int(ls[lane]) for lane in ev)
+        for lane in ev:
+            side.ring.pop(base + lane, None)
+            side.lane_src.pop(base + lane, None)
+        ls[ev] = -1
+        self.lane_pos[is_key][row, ev] = -1
+
+    def _plan_run(self, plan: StorePlan, row: int, slots: list[int], input_rows: list[int],
+                  positions: list[int] | None = None, *, is_key: bool, block_size: int,
+                  group_size: int) -> None:
         """``plan_store`` for new, distinct slots without a per-token walk.
 
         With ``l0`` entries in the window and ``n`` new ones, the per-token
@@ -287,43 +394,38 @@ class KiviResidualRing:
         r, cap = self.ring_len, self.window
         na, base = self.rows * r, row * r
         ls = self.lane_slot[is_key][row]
-        sl = self.slot_lane[is_key][row]
+        lp = self.lane_pos[is_key][row]
         n = len(slots)
-        s0, l0 = self.start[is_key][row], self.length[is_key][row]
+        if positions is None:
+            positions = [-1] * n
+        s0, l0 = int(self.start[is_key][row]), int(self.length[is_key][row])
         evict = ((l0 + n - 1) // cap) * cap if is_key else max(0, l0 + n - cap)
         ev_old = [(s0 + j) % r for j in range(min(evict, l0))]
         ev_new = evict - len(ev_old)
         if evict:
-            ev_slots = [ls[lane] for lane in ev_old] + list(slots[:ev_new])
+            ev_slots = [int(ls[lane]) for lane in ev_old] + list(slots[:ev_new])
             if is_key:
                 for w in range(0, evict, cap):
                     if key_slot_groups_error(ev_slots[w:w + cap], block_size=block_size,
                                              group_size=group_size) is not None:
-                        raise RuntimeError(
-                            "KIVI key flush requires contiguous aligned token groups."
-                        )
-            side.pack_src.extend(side.lane_src.get(base + lane, base + lane) for lane in ev_old)
+                        raise RuntimeError(_FLUSH_ERROR)
+            self._evict(side, row, ev_old, is_key=is_key)
             side.pack_src.extend(na + irow for irow in input_rows[:ev_new])
-            side.pack_slots.extend(ev_slots)
-            for lane in ev_old:
-                sl.pop(ls[lane], None)
-                ls[lane] = -1
-                side.ring.pop(base + lane, None)
-                side.lane_src.pop(base + lane, None)
+            side.pack_slots.extend(slots[:ev_new])
         start = (s0 + evict) % r
         kept_old = l0 - len(ev_old)
         for j in range(ev_new, n):
             lane = (start + kept_old + j - ev_new) % r
-            slot, irow = slots[j], input_rows[j]
-            ls[lane] = slot
-            sl[slot] = lane
-            side.lane_src[base + lane] = na + irow
-            side.ring[base + lane] = irow
+            ls[lane] = slots[j]
+            lp[lane] = positions[j]
+            side.lane_src[base + lane] = na + input_rows[j]
+            side.ring[base + lane] = input_rows[j]
         self.start[is_key][row] = start
         self.length[is_key][row] = kept_old + n - ev_new
 
     def _plan_tokens(self, plan: StorePlan, row: int, slots: list[int], input_rows: list[int],
-                     *, is_key: bool, block_size: int, group_size: int) -> None:
+                     positions: list[int] | None = None, *, is_key: bool, block_size: int,
+                     group_size: int) -> None:
         """``plan_store`` token by token: the reference's loop (``ab.py:411-462``)."""
         side = plan.side(is_key)
         r = self.ring_len
@@ -331,71 +433,122 @@ class KiviResidualRing:
         na = self.rows * r
         base = row * r
         ls = self.lane_slot[is_key][row]
-        sl = self.slot_lane[is_key][row]
-
-        def source(lane: int) -> int:  # where the lane's current content lives
-            return side.lane_src.get(base + lane, base + lane)
-
-        for slot, irow in zip(slots, input_rows):
-            lane = sl.get(slot)
-            if lane is not None:
+        lp = self.lane_pos[is_key][row]
+        if positions is None:
+            positions = [-1] * len(slots)
+        for slot, irow, pos in zip(slots, input_rows, positions):
+            held = np.flatnonzero(ls == slot)
+            if held.size:
+                lane = int(held[0])
                 side.lane_src[base + lane] = na + irow
                 side.ring[base + lane] = irow
                 continue
             while self.length[is_key][row] >= cap:
                 count = cap if is_key else 1
                 ev = self.lanes(row, is_key=is_key)[:count]
-                ev_slots = [ls[lane] for lane in ev]
                 if is_key:
-                    err = key_slot_groups_error(ev_slots, block_size=block_size,
-                                                group_size=group_size)
+                    err = key_slot_groups_error([int(ls[lane]) for lane in ev],
+                                                block_size=block_size, group_size=group_size)
                     if err is not None:
-                        raise RuntimeError(
-                            "KIVI key flush requires contiguous aligned token groups."
-                        )
-                side.pack_src.extend(source(lane) for lane in ev)
-                side.pack_slots.extend(ev_slots)
-                for lane in ev:
-                    sl.pop(ls[lane], None)
-                    ls[lane] = -1
-                    side.ring.pop(base + lane, None)
-                    side.lane_src.pop(base + lane, None)
+                        raise RuntimeError(_FLUSH_ERROR)
+                self._evict(side, row, ev, is_key=is_key)
                 # the start moves past the evicted lanes even when the window
                 # empties, so the append below lands on the lane that was free
                 # before this flush, never on one it packs
                 self.length[is_key][row] -= count
                 self.start[is_key][row] = (self.start[is_key][row] + count) % r
-            tail = (self.start[is_key][row] + self.length[is_key][row]) % r
+            tail = int((self.start[is_key][row] + self.length[is_key][row]) % r)
             ls[tail] = slot
-            sl[slot] = tail
+            lp[tail] = pos
             side.lane_src[base + tail] = na + irow
             side.ring[base + tail] = irow
             self.length[is_key][row] += 1
+
+    def plan_decode_step(self, rows: np.ndarray, slots: np.ndarray, positions: np.ndarray,
+                         input_rows: np.ndarray, *, block_size: int,
+                         group_size: int) -> StepJobs | None:
+        """One new token for each of a batch of requests, planned for the whole
+        batch at once; ``None`` (nothing changed) when the batch does not fit
+        the closed form -- repeated rows, or a slot a window already holds --
+        and the caller replays it token by token instead.
+
+        For each row and side the per-token rule is: a full window evicts
+        (keys: the whole window, checked for aligned groups first; values:
+        the oldest lane), then the token goes to lane ``start + length``.
+        Every key window is checked before any row changes, so a rejected
+        batch leaves the mirror as it was.
+        """
+        if rows.size == 0 or np.unique(rows).size != rows.size:
+            return None
+        for k in _SIDES:
+            if (self.lane_slot[k][rows] == slots[:, None]).any():
+                return None
+        r, cap = self.ring_len, self.window
+        full_k = self.length[True][rows] >= cap
+        fk = rows[full_k]
+        k_lanes = (self.start[True][fk][:, None] + np.arange(cap)) % r
+        k_ev = self.lane_slot[True][fk[:, None], k_lanes]
+        if fk.size and not self._aligned_windows(k_ev, block_size, group_size):
+            raise RuntimeError(_FLUSH_ERROR)
+        # nothing below raises, so no row needs a snapshot for a rollback
+        # keys: flush whole windows
+        kp_src = (fk[:, None] * r + k_lanes).ravel()
+        kp_slot = k_ev.ravel()
+        self.lane_slot[True][fk[:, None], k_lanes] = -1
+        self.lane_pos[True][fk[:, None], k_lanes] = -1
+        self.start[True][fk] = (self.start[True][fk] + cap) % r
+        self.length[True][fk] = 0
+        # values: evict the oldest lane of each full window
+        fv = rows[self.length[False][rows] >= cap]
+        v_lane = self.start[False][fv]
+        vp_src = fv * r + v_lane
+        vp_slot = self.lane_slot[False][fv, v_lane].copy()
+        self.lane_slot[False][fv, v_lane] = -1
+        self.lane_pos[False][fv, v_lane] = -1
+        self.start[False][fv] = (v_lane + 1) % r
+        self.length[False][fv] -= 1
+        # the new token goes to lane start + length on both sides
+        dst = {}
+        for k in _SIDES:
+            tail = (self.start[k][rows] + self.length[k][rows]) % r
+            self.lane_slot[k][rows, tail] = slots
+            self.lane_pos[k][rows, tail] = positions
+            self.length[k][rows] += 1
+            dst[k] = rows * r + tail
+        src = input_rows.astype(np.int64)
+        return StepJobs(kp_src.astype(np.int64), kp_slot.astype(np.int64),
+                        vp_src.astype(np.int64), vp_slot.astype(np.int64), src, dst[True], src,
+                        dst[False])
+
+    @staticmethod
+    def _aligned_windows(windows: np.ndarray, block_size: int, group_size: int) -> bool:
+        """Every row of ``windows`` passes ``key_slot_groups_error``."""
+        n, w = windows.shape
+        if (windows < 0).any() or w % group_size:
+            return False
+        g = windows.reshape(n, w // group_size, group_size)
+        if not (np.diff(g, axis=2) == 1).all():
+            return False
+        if (g[:, :, 0] % group_size).any():
+            return False
+        return bool((g[:, :, 0] // block_size == g[:, :, -1] // block_size).all())
 
     def flush_prefix(self, plan: StorePlan, row: int, count: int, *, is_key: bool,
                      block_size: int, group_size: int) -> None:
         """Move the ``count`` oldest entries of a window to int4 history."""
         self._touch(row)
-        n = self.length[is_key][row]
+        n = int(self.length[is_key][row])
         count = min(count, n)
         if count <= 0:
             return
         ev = self.lanes(row, is_key=is_key)[:count]
         ls = self.lane_slot[is_key][row]
-        ev_slots = [ls[lane] for lane in ev]
         if is_key:
-            err = key_slot_groups_error(ev_slots, block_size=block_size, group_size=group_size)
+            err = key_slot_groups_error([int(ls[lane]) for lane in ev], block_size=block_size,
+                                        group_size=group_size)
             if err is not None or count % group_size:
-                raise RuntimeError("KIVI key flush requires contiguous aligned token groups.")
-        side = plan.side(is_key)
-        base = row * self.ring_len
-        side.pack_src.extend(side.lane_src.get(base + lane, base + lane) for lane in ev)
-        side.pack_slots.extend(ev_slots)
-        for lane in ev:
-            self.slot_lane[is_key][row].pop(ls[lane], None)
-            ls[lane] = -1
-            side.ring.pop(base + lane, None)
-            side.lane_src.pop(base + lane, None)
+                raise RuntimeError(_FLUSH_ERROR)
+        self._evict(plan.side(is_key), row, ev, is_key=is_key)
         self.length[is_key][row] = n - count
         self.start[is_key][row] = (self.start[is_key][row] + count) % self.ring_len
 
@@ -437,7 +590,7 @@ class KiviResidualRing:
                         self.written = True
                     return
         inputs = {True: key_input, False: value_input}
-        for is_key in (True, False):
+        for is_key in _SIDES:
             side = plan.side(is_key)
             if not side.pack_slots:
                 continue
@@ -448,7 +601,7 @@ class KiviResidualRing:
             idx = torch.tensor(side.pack_src, dtype=torch.int64).to(dev, non_blocking=True)
             slots = torch.tensor(side.pack_slots, dtype=torch.int64).to(dev, non_blocking=True)
             (pack_key if is_key else pack_value)(flat, inp, idx, slots)
-        for is_key in (True, False):
+        for is_key in _SIDES:
             side = plan.side(is_key)
             if not side.ring:
                 continue
@@ -458,4 +611,4 @@ class KiviResidualRing:
             self.written = True
 
 
-__all__ = ["KiviResidualRing", "SideWrites", "StorePlan"]
+__all__ = ["KiviResidualRing", "SideWrites", "StepJobs", "StorePlan"]

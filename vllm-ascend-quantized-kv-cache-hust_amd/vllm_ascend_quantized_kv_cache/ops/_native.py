@@ -23,6 +23,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I = ctypes.c_int
 _F = ctypes.c_float
+_D = ctypes.c_double
 
 #: name -> (restype, argtypes); must match include/kvq_hip.h
 SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
@@ -57,6 +58,14 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_P, _I, _I64, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _P, _I64,
          _P, _P, _I64, _P, _I64, _P, _P, _I, _I, _P, _P],
     ),
+    "kvq_plan_kivi_decode": (
+        _I64, [_P, _I64, _I, _I, _I, _I64, _D, _P, _P, _I64, _P, _I64, _P]
+    ),
+    "kvq_kivi_store_planned": (
+        _I,
+        [_P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _I64, _I64, _I64,
+         _P, _P, _P, _P, _P, _P, _P],
+    ),
     "kvq_prefill_attn": (
         _I, [_P, _P, _P, _I, _P, _P, _I64, _I64, _I, _I, _I, _F, _I, _P, _P]
     ),
@@ -82,6 +91,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
 KVQ_ERR_INVALID = -1
 KVQ_ERR_GEOMETRY = -2
 KVQ_ERR_SCRATCH = -3
+KVQ_ERR_CAPACITY = -4
+KVQ_PLAN_DEFAULT, KVQ_PLAN_PIECES, KVQ_PLAN_SPLIT, KVQ_PLAN_SPLIT_PAIRED = 0, 1, 2, 3
 #: static device scratch of kvq_kivi_decode_attn_noalloc (include/kvq_hip.h)
 KVQ_DECODE_SCRATCH_BYTES = 32 << 20
 
@@ -161,6 +172,8 @@ def check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what}: the HIP kernel rejected its arguments (invalid).")
     if rc == KVQ_ERR_GEOMETRY:
         raise RuntimeError(f"{what}: geometry not supported by the HIP kernels.")
+    if rc == KVQ_ERR_CAPACITY:
+        raise RuntimeError(f"{what}: the plan does not fit the arrays it was given.")
     if rc == KVQ_ERR_SCRATCH:
         raise RuntimeError(
             f"{what}: the work list needs more than the {KVQ_DECODE_SCRATCH_BYTES >> 20} MiB "

@@ -10,8 +10,8 @@ ints, so planning costs no device synchronisation.
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
-import math
 
 import numpy as np
 import torch
@@ -49,10 +49,60 @@ class DecodeSeq:
 
 def choose_split_tokens(total_positions: int, num_kv_heads: int, cu_count: int = 256) -> int:
     """Positions per work item: about 8 waves per CU, in [256, 4096], /128."""
-    target_items = max(1, (cu_count * 8) // max(1, num_kv_heads))
+    target_items = max(1, (cu_count * WAVES_PER_CU) // max(1, num_kv_heads))
     per_item = -(-total_positions // target_items)
     per_item = -(-per_item // 128) * 128
     return int(min(4096, max(256, per_item)))
+
+
+def seq_array(seqs: list[DecodeSeq]) -> np.ndarray:
+    """The planner's request geometry, int32 ``[B, 6]``."""
+    out = np.empty((len(seqs), 6), dtype=np.int32)
+    for i, s in enumerate(seqs):
+        out[i] = (s.seq_len, s.k_hist, s.v_hist, s.ring_row, s.k_first, s.v_first)
+    return out
+
+
+def work_capacity(batch: int, num_kv_heads: int, cu_count: int, total_positions: int) -> int:
+    """An upper bound on the items any plan of a batch can hold."""
+    slots = max(1, cu_count * WAVES_PER_CU // max(1, num_kv_heads))
+    rounds = 1 + total_positions // (slots * int(PIECE_MAX_COST)) + 1
+    # pieces cut a request at most once per piece boundary; split plans make
+    # at most two items per 128 int4 positions (pairs) and a tail item per 64
+    # positions, plus up to three per request at range ends
+    return 2 * slots * rounds + 3 * batch + 2 * (total_positions // 64) + 8
+
+
+def plan_into(seqs: np.ndarray, num_kv_heads: int, cu_count: int, mode: int, *,
+              split_tokens: int = 0, tail_cost: float = TAIL_POSITION_COST,
+              meta: np.ndarray, work: np.ndarray, pieces: np.ndarray | None) -> tuple[int, int]:
+    """Run the native planner into caller arrays; ``(num_work, num_pieces)``.
+
+    ``seqs`` int32 ``[B, 6]``; ``meta`` int32 ``[B, 8]``; ``work`` int32
+    ``[cap, 4]``; ``pieces`` int32 ``[cap_p + 1]`` (pinned views let the
+    caller copy the plan to the device without a synchronisation).
+    """
+    npieces = ctypes.c_int64(0)
+    n = _native.lib().kvq_plan_kivi_decode(
+        seqs.ctypes.data, seqs.shape[0], num_kv_heads, cu_count, mode, int(split_tokens),
+        float(tail_cost), meta.ctypes.data, work.ctypes.data, work.shape[0],
+        None if pieces is None else pieces.ctypes.data,
+        0 if pieces is None else pieces.shape[0] - 1, ctypes.byref(npieces),
+    )
+    _native.check(int(n) if n < 0 else 0, "kvq_plan_kivi_decode")
+    return int(n), int(npieces.value)
+
+
+def _plan(seqs: list[DecodeSeq], num_kv_heads: int, cu_count: int, mode: int,
+          split_tokens: int = 0, tail_cost: float = TAIL_POSITION_COST):
+    arr = seq_array(seqs)
+    cap = work_capacity(len(seqs), num_kv_heads, cu_count, int(arr[:, 0].sum()) if len(seqs) else 0)
+    meta = np.zeros((len(seqs), 8), dtype=np.int32)
+    work = np.zeros((cap, 4), dtype=np.int32)
+    pieces = np.zeros(cap + 1, dtype=np.int32)
+    n, npc = plan_into(arr, num_kv_heads, cu_count, mode, split_tokens=split_tokens,
+                       tail_cost=tail_cost, meta=meta, work=work, pieces=pieces)
+    return meta, work[:n].copy(), (pieces[: npc + 1].copy() if npc else None)
 
 
 def plan_decode_work(
@@ -61,49 +111,18 @@ def plan_decode_work(
     """``(seq_meta int32 [B, 8], work int32 [W, 4])`` for the decode kernel.
 
     Kind-0 items cover positions where both sides are int4 (split every
-    ``split_tokens``); kind-1 items cover the rest (at most two residual
-    windows long).  Every request owns at least one item, contiguous in the
-    list.  ``paired``: each int4 range of ``2 * split_tokens`` positions is
-    two items, kind 2 (its even 64-position chunks) at an even index and kind
-    3 (its odd chunks) right after, which the kernel runs side by side on one
-    XCD so the two share every key line (a request that would start a pair at
-    an odd index opens with an empty kind-1 item).
+    ``split_tokens``, rounded up to a multiple of 128); kind-1 items cover the
+    rest in 64-position items.  Every request owns at least one item,
+    contiguous in the list.  ``paired``: each int4 range of ``2 *
+    split_tokens`` positions is two items, kind 2 (its even 64-position
+    chunks) at an even index and kind 3 (its odd chunks) right after, which
+    the kernel runs side by side on one XCD so the two share every key line
+    (a request that would start a pair at an odd index opens with an empty
+    kind-1 item).  Planned natively (``kvq_plan_kivi_decode``).
     """
-    # int4 items start on 128-token boundaries, so paired items split on
-    # 64-position chunks and the MFMA kernel's tiles stay inside pages and
-    # key groups
-    split_tokens = max(128, -(-int(split_tokens) // 128) * 128)
-    meta = np.zeros((len(seqs), 8), dtype=np.int32)
-    work: list[tuple[int, int, int, int]] = []
-    for b, s in enumerate(seqs):
-        first = len(work)
-        end_a = max(0, min(s.k_hist, s.v_hist, s.seq_len))
-        p = 0
-        if paired and end_a > 0 and len(work) % 2:
-            work.append((b, 0, 0, 1))
-        while p < end_a:
-            if paired:
-                e = min(end_a, p + 2 * split_tokens)
-                work.append((b, p, e, 2))
-                work.append((b, p, e, 3))
-            else:
-                e = min(end_a, p + split_tokens)
-                work.append((b, p, e, 0))
-            p = e
-        # the mixed-source tail (at most two residual windows) in 64-position
-        # items, so tails of different requests and heads run side by side
-        p = end_a
-        while p < s.seq_len:
-            e = min(s.seq_len, p + TAIL_ITEM_TOKENS)
-            work.append((b, p, e, 1))
-            p = e
-        if s.seq_len == 0:
-            work.append((b, 0, 0, 1))
-        meta[b] = (
-            s.seq_len, s.k_hist, s.v_hist, s.ring_row, s.k_first, s.v_first,
-            first, len(work) - first,
-        )
-    return meta, np.asarray(work, dtype=np.int32).reshape(-1, 4)
+    mode = _native.KVQ_PLAN_SPLIT_PAIRED if paired else _native.KVQ_PLAN_SPLIT
+    meta, work, _ = _plan(seqs, 1, 1, mode, split_tokens=split_tokens)
+    return meta, work
 
 
 def plan_decode_pieces(
@@ -122,61 +141,11 @@ def plan_decode_pieces(
     head) then fills the chip a whole number of times and every wave of a
     round ends at about the same time.  A cut inside a request splits it into
     items (int4 items start on multiples of 64); ``pieces[k]`` is the first
-    item of piece ``k``.  The items follow ``plan_decode_work``'s rules, so
-    the list is valid with or without the pieces.
+    item of piece ``k``.  Planned natively (``kvq_plan_kivi_decode``).
     """
-    slots = max(1, cu_count * WAVES_PER_CU // max(1, num_kv_heads))
-    spans = []
-    total = 0.0
-    for s in seqs:
-        end_a = max(0, min(s.k_hist, s.v_hist, s.seq_len))
-        spans.append(end_a)
-        total += -(-end_a // 64) * 64 + (s.seq_len - end_a) * tail_cost
-    slots *= max(1, math.ceil(total / (slots * PIECE_MAX_COST)))
-    step = max(64.0, total / slots)
-    meta = np.zeros((len(seqs), 8), dtype=np.int32)
-    work: list[tuple[int, int, int, int]] = []
-    pieces = [0]
-    cum = 0.0
-    cut = step
-
-    def after(unit: float) -> None:  # close the piece once the cost reaches the cut
-        nonlocal cut
-        if cum >= cut - unit / 2 and len(pieces) < slots and len(work) > pieces[-1]:
-            pieces.append(len(work))
-            while cut - unit / 2 <= cum:
-                cut += step
-
-    for b, s in enumerate(seqs):
-        first = len(work)
-        end_a = spans[b]
-        p = 0
-        while p < end_a:
-            tiles = max(1, int((cut - cum) / 64.0 + 0.5))
-            e = min(end_a, p + 64 * tiles)
-            work.append((b, p, e, 0))
-            cum += -(-(e - p) // 64) * 64
-            p = e
-            after(64.0)
-        p = end_a
-        unit = 32 * tail_cost
-        while p < s.seq_len:
-            n = max(1, int((cut - cum) / unit + 0.5)) * 32
-            e = min(s.seq_len, p + n)
-            work.append((b, p, e, 1))
-            cum += (e - p) * tail_cost
-            p = e
-            after(unit)
-        if s.seq_len == 0:
-            work.append((b, 0, 0, 1))
-        meta[b] = (
-            s.seq_len, s.k_hist, s.v_hist, s.ring_row, s.k_first, s.v_first,
-            first, len(work) - first,
-        )
-    if len(work) > pieces[-1]:
-        pieces.append(len(work))
-    return (meta, np.asarray(work, dtype=np.int32).reshape(-1, 4),
-            np.asarray(pieces, dtype=np.int32))
+    meta, work, pieces = _plan(seqs, num_kv_heads, cu_count, _native.KVQ_PLAN_PIECES,
+                               tail_cost=tail_cost)
+    return meta, work, (pieces if pieces is not None else np.zeros(1, dtype=np.int32))
 
 
 def plan_decode(
@@ -194,19 +163,7 @@ def plan_decode(
     fill the last round's gaps (measured on 256 x 32K tokens, unpaired: 2.63
     ms against 2.71 ms for pieces).
     """
-    slots = max(1, cu_count * WAVES_PER_CU // max(1, num_kv_heads))
-    total = 0.0
-    for s in seqs:
-        end_a = max(0, min(s.k_hist, s.v_hist, s.seq_len))
-        total += -(-end_a // 64) * 64 + (s.seq_len - end_a) * TAIL_POSITION_COST
-    if total <= slots * PIECE_MAX_COST:
-        return plan_decode_pieces(seqs, num_kv_heads, cu_count)
-    # paired items: each wave still takes split_tokens int4 positions
-    meta, work = plan_decode_work(
-        seqs, choose_split_tokens(sum(s.seq_len for s in seqs), num_kv_heads, cu_count),
-        paired=True,
-    )
-    return meta, work, None
+    return _plan(seqs, num_kv_heads, cu_count, _native.KVQ_PLAN_DEFAULT)
 
 
 def kivi_decode_attention(

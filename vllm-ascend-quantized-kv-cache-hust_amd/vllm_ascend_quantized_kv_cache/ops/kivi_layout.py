@@ -7,6 +7,7 @@ match on them), so a bad layout fails before any kernel is launched.
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 
@@ -165,7 +166,7 @@ def _check_seq_lens(seq_lens: torch.Tensor, batch_size: int) -> None:
 
 
 def check_gather_metadata_host(
-    block_table_rows: list[list[int]] | None,
+    block_table_rows: list[list[int]] | np.ndarray | None,
     seq_lens: list[int],
     *,
     max_blocks: int,
@@ -181,12 +182,28 @@ def check_gather_metadata_host(
         )
     if block_table_rows is None:
         return
-    for row, length in zip(block_table_rows, seq_lens):
-        live = row[: -(-length // block_size)] if length > 0 else []
-        if any(b < 0 for b in live):
+    try:
+        table = np.asarray(block_table_rows, dtype=np.int64)
+    except ValueError:  # ragged rows
+        table = None
+    if table is None or table.ndim != 2:
+        for row, length in zip(block_table_rows, seq_lens):
+            live = row[: -(-length // block_size)] if length > 0 else []
+            if any(b < 0 for b in live):
+                raise RuntimeError("KIVI block_table has invalid block ids for live tokens.")
+            if any(b >= num_blocks for b in live):
+                raise RuntimeError("KIVI block_table references blocks outside the int4 cache.")
+        return
+    n = min(table.shape[0], len(seq_lens))
+    lens = np.asarray(seq_lens[:n], dtype=np.int64)
+    live = np.arange(table.shape[1])[None, :] < -(-lens // block_size)[:, None]
+    neg = ((table[:n] < 0) & live).any(axis=1)
+    out = ((table[:n] >= num_blocks) & live).any(axis=1)
+    bad = np.flatnonzero(neg | out)
+    if bad.size:  # the first offending request, checked as the reference checks it
+        if neg[bad[0]]:
             raise RuntimeError("KIVI block_table has invalid block ids for live tokens.")
-        if any(b >= num_blocks for b in live):
-            raise RuntimeError("KIVI block_table references blocks outside the int4 cache.")
+        raise RuntimeError("KIVI block_table references blocks outside the int4 cache.")
 
 
 def _check_dequant_gather_metadata(
