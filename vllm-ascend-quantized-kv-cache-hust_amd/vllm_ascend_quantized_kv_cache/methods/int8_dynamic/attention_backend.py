@@ -18,6 +18,7 @@ from __future__ import annotations
 
 from typing import Any
 
+import numpy as np
 import torch
 
 
@@ -66,12 +67,20 @@ class AscendInt8AttentionBackendMixin:
 
         state = _state(attn_metadata)
         float_key = float_value = None
+        step = False
         if key is not None and value is not None:
             if state != "DecodeOnly":
                 float_key, float_value = key, value
             self._prepare_int8_scales(layer, key, value)
             n = min(int(getattr(attn_metadata, "num_actual_tokens", key.shape[0])), key.shape[0])
-            self._write_int8_cache(key[:n], value[:n], attn_metadata.slot_mapping[:n], layer)
+            # a decode step of one token per request writes its tokens inside
+            # the planned step (slots from the staged plan)
+            step = (state == "DecodeOnly" and self._int8_step_enabled(query)
+                    and n == len(attn_metadata.seq_lens_list))
+            if not step:
+                self._write_int8_cache(key[:n], value[:n], attn_metadata.slot_mapping[:n], layer)
+        elif state == "DecodeOnly" and getattr(layer, "_int8_scales_ready", False):
+            step = self._int8_step_enabled(query)
 
         if getattr(attn_metadata, "model_runner_type", None) == "pooling" and not getattr(
             attn_metadata, "causal", True
@@ -85,6 +94,9 @@ class AscendInt8AttentionBackendMixin:
                 "carry key/value to calibrate them."
             )
         if state == "DecodeOnly":
+            if step:
+                return self._forward_int8_decode_step(query, key, value, attn_metadata, output,
+                                                      layer)
             return self._forward_int8_decode(query, attn_metadata, output, layer)
         if state == "ChunkedPrefill":
             return self._forward_int8_chunked_prefill(
@@ -149,6 +161,67 @@ class AscendInt8AttentionBackendMixin:
         if got is not out:
             out.copy_(got)
         return output
+
+    # -- decode step from a host plan (sync-free, capturable launches) -----
+
+    def _int8_step_enabled(self, query: Any) -> bool:
+        """The planned INT8 step applies: the step's tensors are on the GPU."""
+        return isinstance(query, torch.Tensor) and query.device.type == "cuda" and (
+            self.key_cache is not None and self.key_cache.device.type == "cuda")
+
+    def _int8_host_slots(self, attn_metadata: Any, n: int) -> np.ndarray:
+        """The step's slots as host int64, from the host's copy when present."""
+        host = getattr(attn_metadata, "slot_mapping_cpu", None)
+        x = host if host is not None else attn_metadata.slot_mapping
+        if isinstance(x, torch.Tensor):
+            if x.device.type != "cpu":
+                self.int8_host_reads = getattr(self, "int8_host_reads", 0) + 1
+                x = x.cpu()
+            x = x.numpy()
+        return np.asarray(x[:n], dtype=np.int64)
+
+    def _forward_int8_decode_step(self, query: Any, key: Any, value: Any, attn_metadata: Any,
+                                  output: Any, layer: Any) -> Any:
+        """Quantize + scatter, fused decode and combine over one staged plan."""
+        from ...ops.kivi_decode import choose_split_tokens
+        from .decode_step import Int8StepBuffers, launch_int8_step
+
+        lens = [int(x) for x in attn_metadata.seq_lens_list]
+        b = len(lens)
+        if b == 0:
+            return output
+        bs = self.key_cache.shape[1]
+        table = attn_metadata.block_tables[:b]
+        if max(lens) > table.shape[1] * bs or min(lens) < 0:
+            raise ValueError(
+                f"int8_decode_attention: a sequence length exceeds its block table "
+                f"({max(lens)} > {table.shape[1]} x {bs})"
+            )
+        split = choose_split_tokens(sum(lens), self.num_kv_heads)
+        need = b + sum(-(-n // split) for n in lens)
+        bufs = getattr(self, "_int8_step_bufs", None)
+        if bufs is None or bufs.batch < b or bufs.work_cap < need:
+            bufs = Int8StepBuffers(query.device, batch=max(b, 2 * (bufs.batch if bufs else 0)),
+                                   work_cap=2 * need, num_heads=self.num_heads,
+                                   head_size=self.head_size)
+            self._int8_step_bufs = bufs
+        slots = None if key is None else self._int8_host_slots(attn_metadata, b)
+        count = bufs.stage(slots, lens, split, fixed=False)
+        kvh, d = self.num_kv_heads, self.head_size
+        k = None if key is None else key[:b].reshape(b, kvh, d).contiguous()
+        v = None if value is None else value[:b].reshape(b, kvh, d).to(k.dtype).contiguous()
+        out = output[:b].view(b, self.num_heads, d)
+        launch_int8_step(self, bufs, layer, query[:b].reshape(b, self.num_heads, d).contiguous(),
+                         k, v, table.to(torch.int32).contiguous(), count, out)
+        return output
+
+    def int8_decode_graph(self, layer: Any, batch: int, *, max_blocks: int):
+        """An ``Int8DecodeGraph`` for this layer (calibrated scales, bound
+        cache): the decode step's launches, capturable once in a HIP graph
+        and replayed every step after ``prepare`` stages that step's plan."""
+        from .decode_step import Int8DecodeGraph
+
+        return Int8DecodeGraph(self, layer, batch, max_blocks=max_blocks)
 
     def _dense_attention(self, q: Any, k: Any, v: Any, q_lens: list[int], kv_lens: list[int],
                          causal: bool, out: Any) -> Any:
