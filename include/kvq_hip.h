@@ -317,6 +317,39 @@ int kvq_int8_decode_attn(const void* query, int dtype, int64_t batch, int num_he
                          const int32_t* seq_meta, const int32_t* work, int64_t num_work,
                          void* workspace, void* out, void* stream);
 
+/* ---- fp8_per_token_head ------------------------------------------------- */
+
+/* Quantize [num_tokens, KVH, D] K/V (D % 4 == 0, D <= 512; D <= 256 when
+ * D % 8 != 0) to OCP E4M3 codes with one fp32 scale per (token, head) and
+ * write them by slot into k_data/v_data [NB, Bs, KVH, D] bytes and
+ * k_scale/v_scale [NB, Bs, KVH] fp32:
+ *   scale = max(amax|x| / 448, 1e-6), code = e4m3fn(clamp(x / scale, +-448))
+ * with IEEE division and round to nearest even.  Negative slots (padding)
+ * and slots >= NB*Bs are skipped.
+ * Replaces the host store kernel _per_token_head_store_kernel and its wrapper
+ * fp8_per_token_head_store (pkg/ops/triton/per_token_head_store.py:141-294),
+ * with the arithmetic of Fp8PerTokenHeadSemantics.quantize
+ * (pkg/methods/fp8_per_token_head/semantics.py:52-61). */
+int kvq_fp8_pth_store(const void* key, const void* value, int dtype,
+                      const void* slot_mapping, int slot_index_type, int64_t num_tokens,
+                      int num_kv_heads, int head_size, uint8_t* k_data, float* k_scale,
+                      uint8_t* v_data, float* v_scale, int64_t num_blocks, int block_size,
+                      void* stream);
+
+/* Paged E4M3 -> dense TND [cu_seqlens[batch], KVH, D] of out_dtype:
+ * x = float(code) * scale in fp32, then rounded to out_dtype.  Rows of request
+ * b are [cu_seqlens[b], cu_seqlens[b+1]); block ids < 0 read page 0 and ids
+ * >= num_blocks read the last page (callers check live ids on the host).
+ * The read path of Fp8PerTokenHeadSemantics.dequantize
+ * (pkg/methods/fp8_per_token_head/semantics.py:63-65) over the byte layout of
+ * pkg/methods/fp8_per_token_head/byte_cache.py:13-27; the reference has no
+ * device read path for this scheme. */
+int kvq_fp8_pth_gather(const uint8_t* k_data, const float* k_scale, const uint8_t* v_data,
+                       const float* v_scale, int64_t num_blocks, int block_size,
+                       int num_kv_heads, int head_size, const void* block_table,
+                       int block_index_type, int64_t max_blocks, const int64_t* cu_seqlens,
+                       int64_t batch, void* out_k, void* out_v, int out_dtype, void* stream);
+
 /* ---- self-test ---------------------------------------------------------- */
 
 /* One v_mfma_f32_16x16x32_f16 with the operand/result lane mapping the decode

@@ -380,6 +380,83 @@ def int8_paged_dequant(
 
 
 # ---------------------------------------------------------------------------
+# f4: fp8_per_token_head (E4M3 codes, one fp32 scale per (token, head))
+# ---------------------------------------------------------------------------
+
+FP8_E4M3_MAX = 448.0
+
+
+def fp8_pth_scale(x: torch.Tensor) -> torch.Tensor:
+    """``[T, KVH, D] -> [T, KVH, 1]``: ``max(amax|x| / 448, 1e-6)`` in fp32;
+    pkg/methods/fp8_per_token_head/semantics.py:52-55."""
+    amax = x.to(torch.float32).abs().amax(dim=-1, keepdim=True)
+    return (amax / FP8_E4M3_MAX).clamp(min=1e-6)
+
+
+def fp8_pth_quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(codes uint8 [T, KVH, D], scale fp32 [T, KVH, 1])``: the E4M3 bytes of
+    ``clamp(x / scale, -448, 448)`` (torch's e4m3fn cast, round to nearest
+    even); semantics.py:57-61."""
+    scale = fp8_pth_scale(x)
+    q = (x.to(torch.float32) / scale).clamp(-FP8_E4M3_MAX, FP8_E4M3_MAX)
+    return q.to(torch.float8_e4m3fn).view(torch.uint8), scale
+
+
+def fp8_pth_dequantize(codes: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """``float(code) * scale`` in fp32; semantics.py:63-65."""
+    return codes.view(torch.float8_e4m3fn).to(torch.float32) * scale
+
+
+def fp8_pth_store(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    slots: torch.Tensor,
+    k_data: torch.Tensor,
+    k_scale: torch.Tensor,
+    v_data: torch.Tensor,
+    v_scale: torch.Tensor,
+) -> None:
+    """Quantize ``[T, KVH, D]`` K/V and write codes and scales by slot into the
+    ``[NB, Bs, KVH, D]`` / ``[NB, Bs, KVH, 1]`` views; slot ``s`` is page
+    ``s // Bs`` row ``s % Bs`` and negative slots are skipped
+    (pkg/ops/triton/per_token_head_store.py:163-218)."""
+    bs = k_data.shape[1]
+    s = slots.to(torch.int64)
+    live = s >= 0
+    for x, data, scale in ((key, k_data, k_scale), (value, v_data, v_scale)):
+        codes, sc = fp8_pth_quantize(x)
+        data[s[live] // bs, s[live] % bs] = codes[live]
+        scale[s[live] // bs, s[live] % bs] = sc[live]
+
+
+def fp8_pth_gather(
+    k_data: torch.Tensor,
+    k_scale: torch.Tensor,
+    v_data: torch.Tensor,
+    v_scale: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: list[int],
+    target_dtype: torch.dtype,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Paged codes -> dense TND ``[sum L, KVH, D]``: ``dequantize`` then
+    ``.to(target_dtype)``, as ``fake_quant`` reads a code back
+    (semantics.py:63-70), for positions ``p < L`` of each request at slot
+    ``table[b, p // Bs] * Bs + p % Bs``; negative ids read page 0 as the
+    KIVI gather does (pkg/ops/kivi_gather.py:109)."""
+    bs = k_data.shape[1]
+    outs = []
+    for data, scale in ((k_data, k_scale), (v_data, v_scale)):
+        rows = []
+        for b, n in enumerate(seq_lens):
+            p = torch.arange(int(n))
+            blk = block_table[b, p // bs].to(torch.int64).clamp(min=0)
+            rows.append(fp8_pth_dequantize(data[blk, p % bs], scale[blk, p % bs]))
+        dense = torch.cat(rows) if rows else data.new_zeros((0,) + data.shape[2:])
+        outs.append(dense.to(target_dtype))
+    return outs[0], outs[1]
+
+
+# ---------------------------------------------------------------------------
 # a6: residual window state (incremental rule) -- a reference-free model
 # ---------------------------------------------------------------------------
 

@@ -22,12 +22,15 @@ from vllm_ascend_quantized_kv_cache.adapters.vllm_ascend_hust.register import (
 )
 
 PKG = Path(__file__).resolve().parents[1] / "vllm-ascend-quantized-kv-cache-hust_amd"
+#: every method the registry knows, including the scheme with no host adapter
+KNOWN = ["fp8_per_token_head", "int8_dynamic", "kivi_int4"]
+#: the methods bootstrap routes (adapter wired, literal selectable)
 ROUTABLE = ["int8_dynamic", "kivi_int4"]
 
 
 def test_published_methods_and_dtypes():
-    assert kv_methods.list() == ROUTABLE
-    assert kv_methods.list(host="vllm_ascend_hust") == ROUTABLE
+    assert kv_methods.list() == KNOWN
+    assert kv_methods.list(host="vllm_ascend_hust") == KNOWN
     assert kv_methods.describe("int8_dynamic")["dtype"] == "int8"
     assert kv_methods.describe("kivi_int4")["dtype"] == "kivi_int4"
     with pytest.raises(ValueError, match="unknown quantized KV method"):

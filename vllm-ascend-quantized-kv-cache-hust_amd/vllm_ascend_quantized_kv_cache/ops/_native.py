@@ -86,6 +86,14 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_P, _I, _I64, _I, _I, _I, _F, _P, _P, _I64, _I, _P, _P, _P, _I64, _P, _P, _I64,
          _P, _P, _P],
     ),
+    "kvq_fp8_pth_store": (
+        _I,
+        [_P, _P, _I, _P, _I, _I64, _I, _I, _P, _P, _P, _P, _I64, _I, _P],
+    ),
+    "kvq_fp8_pth_gather": (
+        _I,
+        [_P, _P, _P, _P, _I64, _I, _I, _I, _P, _I, _I64, _P, _I64, _P, _P, _I, _P],
+    ),
 }
 
 KVQ_ERR_INVALID = -1
