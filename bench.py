@@ -750,10 +750,63 @@ def bench_int8_ops(torch, dev, *, reps=10, seed=0):
                 "frac": round(byt / ms / 1e6 / HBM_PEAK_GBS, 4)} for k, (ms, byt) in res.items()}
 
 
+def bench_fp8_ops(torch, dev, *, reps=10, seed=0):
+    """fp8_per_token_head store and gather at config 2's shape (64 x 4096
+    tokens, 8 KV heads, D 128, bf16): 1.1 GB of K/V in and 0.55 GB of codes
+    out per store, so no call finds its inputs in the MALL."""
+    from vllm_ascend_quantized_kv_cache.methods.fp8_per_token_head.byte_cache import (
+        Fp8PerTokenHeadLayout,
+        fp8_caches_from_byte_tensors,
+    )
+    from vllm_ascend_quantized_kv_cache.ops.fp8_ops import (
+        fp8_per_token_head_dequant_gather,
+        fp8_per_token_head_store,
+    )
+
+    b, kvh, d, bs, n = 64, 8, 128, 128, 4096
+    nb = b * n // bs
+    gen = torch.Generator().manual_seed(seed)
+    table_cpu = torch.randperm(nb, generator=gen).view(b, n // bs)
+    table = table_cpu.to(torch.int32).to(dev)
+    gdev = torch.Generator(device=dev).manual_seed(seed + 9)
+    t = b * n
+    key = torch.randn((t, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
+    value = torch.randn((t, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
+    pos = torch.arange(n, device=dev)
+    slots = torch.cat([table[i].to(torch.int64)[pos // bs] * bs + pos % bs for i in range(b)])
+    layout = Fp8PerTokenHeadLayout(nb, bs, kvh, d)
+    kb = torch.zeros((nb, bs, kvh, layout.bytes_per_token_head), dtype=torch.uint8, device=dev)
+    vb = torch.zeros_like(kb)
+    views = fp8_caches_from_byte_tensors(kb, vb, layout)
+    host_table = table_cpu.numpy()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn):
+        sustain(torch, fn)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    rows = t * kvh  # per side
+    res = {}
+    ms = timed(lambda: fp8_per_token_head_store(key, value, slots, *views))
+    res["store"] = (ms, 2 * rows * (2 * d + d + 4))  # bf16 in, codes + scale out
+    ms = timed(lambda: fp8_per_token_head_dequant_gather(
+        *views, table, [n] * b, torch.bfloat16, block_table_host=host_table))
+    res["gather"] = (ms, 2 * rows * (d + 4 + 2 * d))  # codes + scale in, bf16 out
+    del key, value, kb, vb, views
+    torch.cuda.empty_cache()
+    return {k: {"ms": round(ms, 4), "gbs": round(byt / ms / 1e6, 1),
+                "frac": round(byt / ms / 1e6 / HBM_PEAK_GBS, 4)} for k, (ms, byt) in res.items()}
+
+
 # ---------------------------------------------------------------------------
 
 
-EXTRA_LEGS = ("forward", "config4", "config4attn", "config2", "config2ops", "config5")
+EXTRA_LEGS = ("forward", "config4", "config4attn", "config2", "config2ops", "config5", "fp8ops")
 
 
 def main() -> int:
@@ -905,6 +958,11 @@ def run_leg(torch, dev, leg: str, lens: list[int], args) -> dict:
         for k, v in i8ops.items():
             out[f"config2_int8_{k}"] = v
         log("config2: " + ", ".join(f"{k} {v['gbs']:.0f} GB/s" for k, v in i8ops.items()))
+    elif leg == "fp8ops":
+        f8 = bench_fp8_ops(torch, dev)
+        for k, v in f8.items():
+            out[f"fp8_per_token_head_{k}"] = v
+        log("fp8_per_token_head: " + ", ".join(f"{k} {v['gbs']:.0f} GB/s" for k, v in f8.items()))
     elif leg == "config5":
         # one layer: 10.8 GB of pages, far past any cache
         c5 = bench_kivi_decode(

@@ -8,7 +8,8 @@
   codes follow the division, as the reference semantics does;
 * the paged store is bit-exact against the oracle (codes and scales, the
   whole page image, padding slots untouched) for bf16 / fp16 / fp32 inputs,
-  int32 / int64 slots and head sizes that exercise every lane-group shape;
+  int32 / int64 slots and head sizes that exercise every lane width (16, 8
+  and 4 codes a lane) and group shape, including partly idle groups;
 * the gather is bit-exact against the oracle's dequantize-then-cast, with
   unallocated tail ids;
 * attention over the paged codes is within 1e-2 of fp32 attention over the
@@ -107,6 +108,8 @@ def _inputs(t, kvh, d, dtype, seed):
         (torch.bfloat16, 256, 2, torch.int64),
         (torch.bfloat16, 512, 1, torch.int32),  # one wave per row
         (torch.float16, 8, 8, torch.int64),     # one lane per row
+        (torch.bfloat16, 40, 3, torch.int64),   # 8 codes a lane, 5 lanes of 8
+        (torch.float32, 24, 2, torch.int32),    # 8 codes a lane, 3 lanes of 4
     ],
 )
 def test_store_matches_oracle_bit_exact(gpu_device, dtype, d, kvh, index):
@@ -132,7 +135,7 @@ def test_store_matches_oracle_bit_exact(gpu_device, dtype, d, kvh, index):
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("d,kvh", [(128, 8), (100, 2), (64, 4)])
+@pytest.mark.parametrize("d,kvh", [(128, 8), (100, 2), (64, 4), (40, 3)])
 def test_gather_matches_oracle_bit_exact(gpu_device, out_dtype, d, kvh):
     nb, bs = 12, 16
     lens = [37, 16, 0, 70]

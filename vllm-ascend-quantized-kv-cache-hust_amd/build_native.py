@@ -48,8 +48,11 @@ COMMON_FLAGS = [
 # could change a result the reference defines (a NaN input has no defined
 # KIVI code), and without NaN semantics the compiler drops the canonicalizing
 # v_max_f32 it otherwise puts in front of every min/max.
+# The fp8 store's amax and clamps likewise see only finite activations (a NaN
+# has no E4M3 code the reference's clamp could produce).
 EXTRA_FLAGS = {
     "kivi_pack.hip": ["-fno-honor-nans"],
+    "fp8_kv.hip": ["-fno-honor-nans"],
 }
 
 
