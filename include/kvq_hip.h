@@ -256,7 +256,7 @@ int kvq_kivi_store_planned(const void* key_input, const void* value_input, void*
  * Request b's query row i sits at kv position lk_b - lq_b + i; with `causal`
  * keys past it are masked.  GQA maps query head h to kv head
  * h / (num_heads / num_kv_heads).  cu_* are int32 [batch + 1]; max_q_len
- * bounds lq_b.  head_size in {32, 64, 128, 256}.
+ * bounds lq_b.  head_size in {32, 64, 128, 256}; scale > 0.
  * Replaces npu_fused_infer_attention_score with input_layout "TND"
  * (pkg/methods/kivi_int4/attention_backend.py:1248-1262, 1320-1334 and the
  * dense fallback 1341-1392; pkg/methods/int8_dynamic/attention_backend.py:

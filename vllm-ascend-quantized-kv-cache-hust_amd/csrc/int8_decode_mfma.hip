@@ -127,6 +127,18 @@ struct SoftmaxState {
   f4 o[8];    // o[t][r]: head 4g + r, dim 8n + t
 };
 
+// x + (x of lane n ^ 8 in the same 16-lane row): v_add_f32 with a DPP
+// row_ror:8 operand.
+__device__ __forceinline__ float add_ror8(float x) {
+  const int y = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false);
+  return x + __int_as_float(y);
+}
+
+// FOLD (GQA groups of at most 8 heads): qh carries the hi part of head n in
+// columns n < 8 and the lo part of head n - 8 in columns n >= 8, so one MFMA
+// per k-step gives both partial scores and a rotate-by-8 add sums them (both
+// lanes then hold head n % 8's score; ql unused).
+template <bool FOLD>
 __device__ __forceinline__ void compute_tile(const TileRegs& t, int p, int pb, int pe,
                                              const h8 (&qh)[4], const h8 (&ql)[4], float sc,
                                              int g, SoftmaxState& st) {
@@ -143,8 +155,14 @@ __device__ __forceinline__ void compute_tile(const TileRegs& t, int p, int pb, i
       const h8 a = as_h8(key_pair<0>(w[2 * ks]), key_pair<1>(w[2 * ks]),
                          key_pair<0>(w[2 * ks + 1]), key_pair<1>(w[2 * ks + 1]));
       s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[ks], s[j], 0, 0, 0);
-      s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ks], s[j], 0, 0, 0);
+      if (!FOLD) s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ks], s[j], 0, 0, 0);
     }
+  }
+  if (FOLD) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[j][r] = add_ror8(s[j][r]);
   }
   // ---- online softmax for head n over tokens 16j + 4g + r ----
   float mx = -INFINITY;
@@ -216,7 +234,7 @@ __device__ __forceinline__ void compute_tile(const TileRegs& t, int p, int pb, i
   }
 }
 
-template <typename TQ>
+template <typename TQ, bool FOLD>
 __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 int8_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qscale,
                         const int8_t* __restrict__ kc, const int8_t* __restrict__ vc, int bs,
@@ -249,8 +267,9 @@ int8_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   float qf[32];
   float amax = 0.0f;
   {
-    const bool live = n < rep;
-    const TQ* qrow = query + (static_cast<int64_t>(b) * hq + h * rep + (live ? n : 0)) * kD;
+    const int hn = FOLD ? (n & 7) : n;  // folded: columns n and n + 8 carry head n % 8
+    const bool live = hn < rep;
+    const TQ* qrow = query + (static_cast<int64_t>(b) * hq + h * rep + (live ? hn : 0)) * kD;
     const TQ* arow = k_aq + static_cast<int64_t>(h) * kD;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
@@ -281,8 +300,14 @@ int8_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
       hw[u] = h2_bits(hh[0], hh[1]);
       lw[u] = h2_bits(ll[0], ll[1]);
     }
-    qh[ks] = as_h8(hw[0], hw[1], hw[2], hw[3]);
-    ql[ks] = as_h8(lw[0], lw[1], lw[2], lw[3]);
+    if (FOLD) {
+      const bool lo_col = n >= 8;
+      qh[ks] = as_h8(lo_col ? lw[0] : hw[0], lo_col ? lw[1] : hw[1], lo_col ? lw[2] : hw[2],
+                     lo_col ? lw[3] : hw[3]);
+    } else {
+      qh[ks] = as_h8(hw[0], hw[1], hw[2], hw[3]);
+      ql[ks] = as_h8(lw[0], lw[1], lw[2], lw[3]);
+    }
   }
   const float sc = ldexpf(qscale, -e);
 
@@ -311,13 +336,13 @@ int8_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   if (p0 + kTile < pe) load_tile(tb, c, p0 + kTile);
   for (int p = p0; p < pe; p += 3 * kTile) {
     if (p + 2 * kTile < pe) load_tile(tc, c, p + 2 * kTile);
-    compute_tile(ta, p, pb, pe, qh, ql, sc, g, st);
+    compute_tile<FOLD>(ta, p, pb, pe, qh, ql, sc, g, st);
     if (p + kTile >= pe) break;
     if (p + 3 * kTile < pe) load_tile(ta, c, p + 3 * kTile);
-    compute_tile(tb, p + kTile, pb, pe, qh, ql, sc, g, st);
+    compute_tile<FOLD>(tb, p + kTile, pb, pe, qh, ql, sc, g, st);
     if (p + 2 * kTile >= pe) break;
     if (p + 4 * kTile < pe) load_tile(tb, c, p + 4 * kTile);
-    compute_tile(tc, p + 2 * kTile, pb, pe, qh, ql, sc, g, st);
+    compute_tile<FOLD>(tc, p + 2 * kTile, pb, pe, qh, ql, sc, g, st);
   }
 
   // ---- epilogue ----
@@ -365,11 +390,16 @@ int launch_int8_decode_mfma(const void* query, int dtype, int hq, int kvh, int d
   if (d != kD || hq / kvh > 16 || bs % 16) return KVQ_OK;
   if (num_work * kvh > 0x7fffffff) return KVQ_ERR_INVALID;
   const dim3 grid(static_cast<unsigned>(num_work * kvh));
+  // GQA groups of at most 8 heads fold the hi/lo score parts into one MFMA
+  const bool fold = hq / kvh <= 8;
+#define KVQ_LAUNCH_I8(TQ, F)                                                                  \
+  hipLaunchKernelGGL((int8_decode_mfma_kernel<TQ, F>), grid, dim3(64), 0, s,                 \
+                     static_cast<const TQ*>(query), hq, kvh, qscale, kc, vc, bs, nb,         \
+                     static_cast<const TQ*>(k_aq), static_cast<const TQ*>(v_aq), block_table,\
+                     maxb, work, ws_o, ws_ml)
   KVQ_DISPATCH_FLOAT(dtype, TQ,
-    hipLaunchKernelGGL((int8_decode_mfma_kernel<TQ>), grid, dim3(64), 0, s,
-                       static_cast<const TQ*>(query), hq, kvh, qscale, kc, vc, bs, nb,
-                       static_cast<const TQ*>(k_aq), static_cast<const TQ*>(v_aq), block_table,
-                       maxb, work, ws_o, ws_ml));
+    if (fold) KVQ_LAUNCH_I8(TQ, true); else KVQ_LAUNCH_I8(TQ, false));
+#undef KVQ_LAUNCH_I8
   KVQ_LAUNCH_CHECK();
   *launched = true;
   return KVQ_OK;

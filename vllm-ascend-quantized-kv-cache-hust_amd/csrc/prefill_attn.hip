@@ -278,8 +278,7 @@ __device__ __forceinline__ void wait_vmcnt0() {
   asm volatile("" ::: "memory");
 }
 
-constexpr int kFaRows = 32;   // query rows per wave
-constexpr int kFaWaves = 4;
+constexpr int kFaGroupRows = 128;  // query rows per workgroup
 constexpr int kFaBlock = 64;  // keys per block
 constexpr int kFaVPitch = kFaBlock + 4;
 
@@ -291,22 +290,33 @@ struct FaLds {
   static constexpr int BYTES = 2 * BUF;
 };
 
-template <typename T, int D>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// NG 16-row query column groups per wave; the workgroup's 8 / NG waves cover
+// 128 rows and share the LDS blocks.  The launcher uses NG = 2 (4 waves of 32
+// rows, 2 waves per SIMD): each LDS operand feeds two MFMAs.  NG = 1 (8 waves
+// of 16 rows, 4 per SIMD) measured 26% slower on config 4 (twice the LDS reads
+// per MFMA, and spills at the 128-VGPR limit of 4 waves per SIMD).
+template <typename T, int D, int NG>
+__global__ void __launch_bounds__(64 * (8 / NG))
+__attribute__((amdgpu_waves_per_eu(4 / NG, 4 / NG)))
 prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
                        const T* __restrict__ v, const int32_t* __restrict__ cu_q,
                        const int32_t* __restrict__ cu_k, int hq, int kvh, float qscale,
                        int causal, int qblocks, T* __restrict__ out) {
   using O = typename Op<T>::type;
   using L = FaLds<D>;
+  constexpr int kFaWaves = 8 / NG;
+  constexpr int kFaRows = 16 * NG;  // query rows per wave
   constexpr int KS = D / 32;      // score k-steps
   constexpr int DB = D / 16;      // output dim blocks
   constexpr int PPR = D / 8;      // 16-byte pieces per row
   constexpr int RPI = 64 / PPR;   // K rows per DMA instruction
   constexpr int KINST = kFaBlock / RPI / kFaWaves;  // DMA instructions per wave per block
-  constexpr int VTASKS = (kFaBlock / 4) * PPR;      // (key quad, piece) tasks per block
+  // V^T staging: task = (KPT consecutive keys, 16-byte piece of the row); two
+  // keys a task when the workgroup has a thread for each, else four
+  constexpr int KPT = (kFaBlock / 2) * PPR <= 64 * kFaWaves ? 2 : 4;
+  constexpr int VTASKS = (kFaBlock / KPT) * PPR;   // tasks per block
   static_assert(KINST >= 1 && kFaBlock % (RPI * kFaWaves) == 0, "K DMA split");
-  static_assert(VTASKS <= 256, "one V task per thread");
+  static_assert(VTASKS <= 64 * kFaWaves, "one V task per thread");
   extern __shared__ __align__(16) char lds[];
 
   // heavy query blocks first: block x = qblocks - 1 - blockIdx.x
@@ -333,11 +343,11 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   const int wave_last_pos = lk - lq + wave_last;
 
   // Q^T operands: group g2, k-step s: query row wrow0 + 16*g2 + n, dims 32s + 8kg + i
-  u8v qop[2][KS];
-  int my_pos[2];
-  bool live[2];
+  u8v qop[NG][KS];
+  int my_pos[NG];
+  bool live[NG];
 #pragma unroll
-  for (int g2 = 0; g2 < 2; ++g2) {
+  for (int g2 = 0; g2 < NG; ++g2) {
     const int row = wrow0 + 16 * g2 + n;
     live[g2] = row < lq;
     my_pos[g2] = lk - lq + row;
@@ -377,24 +387,25 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
       dma16(src, buf + 1024 * inst);
     }
   };
-  // V task of this thread: key quad j, piece c (dims 8c .. 8c + 7).  Lanes
-  // next to each other take consecutive key quads, so a quarter-wave's
-  // transposed stores (row 8c + i, keys 4j .. 4j + 3) are 128 contiguous bytes.
-  const int vj = tid % 16;
-  const int vc = tid / 16;
+  // V task of this thread: keys KPT*j .. KPT*j + KPT - 1, piece c (dims 8c ..
+  // 8c + 7).  Lanes next to each other take consecutive key groups, so a
+  // quarter-wave's transposed stores (row 8c + i, keys KPT*j ..) are contiguous.
+  constexpr int NJ = kFaBlock / KPT;
+  const int vj = tid % NJ;
+  const int vc = tid / NJ;
   const bool vtask = tid < VTASKS;
-  uint4 vr[4];
-  const T* vlane = vbase + (4 * vj) * row_stride + 8 * vc;
+  uint4 vr[KPT];
+  const T* vlane = vbase + (KPT * vj) * row_stride + 8 * vc;
   auto load_v = [&](int kb) {
     if (!vtask) return;
     if (kb + kFaBlock <= lk) {  // uniform: only the last block clamps
       const T* src = vlane + kb * row_stride;
 #pragma unroll
-      for (int l = 0; l < 4; ++l) vr[l] = *reinterpret_cast<const uint4*>(src + l * row_stride);
+      for (int l = 0; l < KPT; ++l) vr[l] = *reinterpret_cast<const uint4*>(src + l * row_stride);
     } else {
 #pragma unroll
-      for (int l = 0; l < 4; ++l) {
-        int pos = kb + 4 * vj + l;
+      for (int l = 0; l < KPT; ++l) {
+        int pos = kb + KPT * vj + l;
         pos = pos < lk ? pos : lk - 1;
         vr[l] = *reinterpret_cast<const uint4*>(vbase + pos * row_stride + 8 * vc);
       }
@@ -405,29 +416,42 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
     uint16_t* vt = reinterpret_cast<uint16_t*>(buf + L::K_BYTES);
     const uint32_t w0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
     const uint32_t w1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
-    const uint32_t w2[4] = {vr[2].x, vr[2].y, vr[2].z, vr[2].w};
-    const uint32_t w3[4] = {vr[3].x, vr[3].y, vr[3].z, vr[3].w};
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      // dim 8c + 2w: low halves of keys 0..3; dim 8c + 2w + 1: high halves
-      uint2 lo, hi;
-      lo.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x05040100u);
-      lo.y = __builtin_amdgcn_perm(w3[w], w2[w], 0x05040100u);
-      hi.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u);
-      hi.y = __builtin_amdgcn_perm(w3[w], w2[w], 0x07060302u);
-      *reinterpret_cast<uint2*>(vt + (8 * vc + 2 * w) * kFaVPitch + 4 * vj) = lo;
-      *reinterpret_cast<uint2*>(vt + (8 * vc + 2 * w + 1) * kFaVPitch + 4 * vj) = hi;
+      // dim 8c + 2w: the low halves of the keys; dim 8c + 2w + 1: the high halves
+      uint16_t* lo_row = vt + (8 * vc + 2 * w) * kFaVPitch + KPT * vj;
+      uint16_t* hi_row = vt + (8 * vc + 2 * w + 1) * kFaVPitch + KPT * vj;
+      if constexpr (KPT == 2) {
+        *reinterpret_cast<uint32_t*>(lo_row) = __builtin_amdgcn_perm(w1[w], w0[w], 0x05040100u);
+        *reinterpret_cast<uint32_t*>(hi_row) = __builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u);
+      } else {
+        const uint32_t w2 = (&vr[2].x)[w], w3 = (&vr[KPT - 1].x)[w];
+        uint2 lo, hi;
+        lo.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x05040100u);
+        lo.y = __builtin_amdgcn_perm(w3, w2, 0x05040100u);
+        hi.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u);
+        hi.y = __builtin_amdgcn_perm(w3, w2, 0x07060302u);
+        *reinterpret_cast<uint2*>(lo_row) = lo;
+        *reinterpret_cast<uint2*>(hi_row) = hi;
+      }
     }
   };
 
-  float m_run[2] = {-INFINITY, -INFINITY};
+  float m_run[NG];
+#pragma unroll
+  for (int g2 = 0; g2 < NG; ++g2) m_run[g2] = -INFINITY;
+  const float lazy_thr = 8.0f / qscale;  // qscale > 0
   // l_acc[g2]: every row holds the running sum of the (rounded) P of query
   // column n, accumulated by an MFMA with an all-ones A, so it is the exact sum
   // of what the PV MFMAs saw and rescales together with o
-  f4 l_acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
-  f4 o[DB][2];
+  f4 l_acc[NG];
+  f4 o[DB][NG];
 #pragma unroll
-  for (int j = 0; j < DB; ++j) o[j][0] = o[j][1] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int g2 = 0; g2 < NG; ++g2) {
+    l_acc[g2] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < DB; ++j) o[j][g2] = f4{0.f, 0.f, 0.f, 0.f};
+  }
   const uint16_t one = op_bits(1.0f, O{});
   const u8v ones = u8v{one, one, one, one, one, one, one, one};
 
@@ -455,9 +479,11 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
       const uint16_t* sk = reinterpret_cast<const uint16_t*>(cur);
       const uint16_t* svt = reinterpret_cast<const uint16_t*>(cur + L::K_BYTES);
       // ---- S^T = K * Q^T ----
-      f4 sacc[4][2];
+      f4 sacc[4][NG];
 #pragma unroll
-      for (int kb2 = 0; kb2 < 4; ++kb2) sacc[kb2][0] = sacc[kb2][1] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int kb2 = 0; kb2 < 4; ++kb2)
+#pragma unroll
+        for (int g2 = 0; g2 < NG; ++g2) sacc[kb2][g2] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb2 = 0; kb2 < 4; ++kb2) {
         // all k-steps' K operands of this 16-key block first, then the MFMAs:
@@ -471,18 +497,18 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          sacc[kb2][0] = mfma16(a[s], qop[0][s], sacc[kb2][0], O{});
-          sacc[kb2][1] = mfma16(a[s], qop[1][s], sacc[kb2][1], O{});
-        }
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+          for (int g2 = 0; g2 < NG; ++g2)
+            sacc[kb2][g2] = mfma16(a[s], qop[g2][s], sacc[kb2][g2], O{});
       }
       // ---- online softmax per query column ----
       // the max runs over raw scores (qscale > 0), the exponent is one fma:
       // p = 2^(qscale * s - qscale * m)
       const bool full = kb + kFaBlock <= lk && (!causal || kb + kFaBlock - 1 <= lk - lq + wrow0);
-      u8v pop[2][2];  // [g2][ks]
+      u8v pop[NG][2];  // [g2][ks]
 #pragma unroll
-      for (int g2 = 0; g2 < 2; ++g2) {
+      for (int g2 = 0; g2 < NG; ++g2) {
         float sv[16];
         float tmax = -INFINITY;
 #pragma unroll
@@ -499,11 +525,18 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
           }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run[g2], tmax);  // raw-score units
+        // lazy offset: the row's exponent offset moves only when its max grows
+        // past it by more than 8 (log2 units), so p <= 2^8 and most blocks
+        // leave o and l unscaled; the normalisation by l makes the result the
+        // same softmax whatever offset the row settled on
+        const bool grow = tmax > m_run[g2] + lazy_thr;  // raw-score units
+        const float m_new = grow ? tmax : m_run[g2];
         const float m_off = m_new == -INFINITY ? 0.0f : -qscale * m_new;
-        const float alpha = m_run[g2] == -INFINITY
-                                ? 0.0f
-                                : __builtin_amdgcn_exp2f(__builtin_fmaf(qscale, m_run[g2], m_off));
+        const float alpha =
+            !grow ? 1.0f
+                  : (m_run[g2] == -INFINITY
+                         ? 0.0f
+                         : __builtin_amdgcn_exp2f(__builtin_fmaf(qscale, m_run[g2], m_off)));
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           uint32_t w[4];
@@ -538,12 +571,11 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
-        for (int j = 0; j < DB; ++j) {
-          o[j][0] = mfma16(a[j], pop[0][ks], o[j][0], O{});
-          o[j][1] = mfma16(a[j], pop[1][ks], o[j][1], O{});
-        }
-        l_acc[0] = mfma16(ones, pop[0][ks], l_acc[0], O{});
-        l_acc[1] = mfma16(ones, pop[1][ks], l_acc[1], O{});
+        for (int j = 0; j < DB; ++j)
+#pragma unroll
+          for (int g2 = 0; g2 < NG; ++g2) o[j][g2] = mfma16(a[j], pop[g2][ks], o[j][g2], O{});
+#pragma unroll
+        for (int g2 = 0; g2 < NG; ++g2) l_acc[g2] = mfma16(ones, pop[g2][ks], l_acc[g2], O{});
       }
     }
     if (more) {
@@ -558,7 +590,7 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
 
   // o[j][g2][r] = O^T[dim 16j + 4kg + r][query 16*g2 + n]
 #pragma unroll
-  for (int g2 = 0; g2 < 2; ++g2) {
+  for (int g2 = 0; g2 < NG; ++g2) {
     if (!live[g2]) continue;
     const float l = l_acc[g2][0];
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
@@ -584,19 +616,21 @@ extern "C" int kvq_prefill_attn(const void* query, const void* key, const void* 
   if (num_kv_heads <= 0 || num_heads % num_kv_heads) return KVQ_ERR_GEOMETRY;
   if (head_size != 64 && head_size != 128 && head_size != 256 && head_size != 32)
     return KVQ_ERR_GEOMETRY;
+  if (!(scale > 0.0f)) return KVQ_ERR_INVALID;  // the softmax max runs over raw scores
   hipStream_t s = static_cast<hipStream_t>(stream);
   const float qscale = scale * 1.4426950408889634f;
   int64_t lds_max = 0;  // LDS one workgroup may use on this device
   const int lrc = device_lds_max(&lds_max);
   if (lrc != KVQ_OK) return lrc;
   const int64_t fa_lds = head_size == 64 ? FaLds<64>::BYTES : FaLds<128>::BYTES;
+  constexpr int kFaNG = 2;
   if ((dtype == KVQ_DTYPE_BF16 || dtype == KVQ_DTYPE_F16) &&
       (head_size == 64 || head_size == 128) && fa_lds <= lds_max) {
-    const int64_t fab = (max_q_len + kFaRows * kFaWaves - 1) / (kFaRows * kFaWaves);
+    const int64_t fab = (max_q_len + kFaGroupRows - 1) / kFaGroupRows;
     if (fab > 0x7fffffff) return KVQ_ERR_INVALID;
     const dim3 fgrid(static_cast<unsigned>(fab), num_heads, static_cast<unsigned>(batch));
 #define KVQ_PREFILL_FA(TT, DD)                                                              \
-    hipLaunchKernelGGL((prefill_attn_fa_kernel<TT, DD>), fgrid, dim3(256),                  \
+    hipLaunchKernelGGL((prefill_attn_fa_kernel<TT, DD, kFaNG>), fgrid, dim3(64 * (8 / kFaNG)), \
                        FaLds<DD>::BYTES, s, static_cast<const TT*>(query),                 \
                        static_cast<const TT*>(key), static_cast<const TT*>(value),         \
                        cu_seqlens_q, cu_seqlens_k, num_heads, num_kv_heads, qscale, causal, \
