@@ -121,27 +121,6 @@ __device__ __forceinline__ float max_kg(float v) {
   return v;
 }
 
-// ---- LDS DMA -------------------------------------------------------------
-// global_load_lds: every lane reads `size` bytes at its own global address and
-// the wave writes them to LDS at base + size * lane (base must be uniform).
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-__device__ __forceinline__ void dma16(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)(lds), 16, 0, 0);
-}
-__device__ __forceinline__ void dma4(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)(lds), 4, 0, 0);
-}
-
-// s_waitcnt vmcnt(N) with lgkmcnt/expcnt left alone (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-  asm volatile("" ::: "memory");
-}
-
 // ---- tile layout -------------------------------------------------------------
 // One wave's tile buffer.  Key and value words arrive with 16-byte DMA lanes in
 // their page order; the small scale/min regions are gathered with 4-byte lanes

@@ -312,6 +312,27 @@ struct Raw8<f16> {
   }
 };
 
+// ---- LDS DMA -------------------------------------------------------------
+// global_load_lds: every lane reads `size` bytes at its own global address and
+// the wave writes them to LDS at base + size * lane (base must be uniform).
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)(lds), 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)(lds), 4, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) with lgkmcnt/expcnt left alone (gfx9 encoding: vmcnt
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+
 // LDS one workgroup may use on the current device, cached per device (the
 // attribute query is host work that a decode step should not repeat).
 inline int device_lds_max(int64_t* out) {

@@ -265,19 +265,6 @@ prefill_attn_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
 // The rescale needs no shuffles: S^T and O^T both put the lane's query in
 // its column.
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-__device__ __forceinline__ void dma16(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)(lds), 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(0) with expcnt/lgkmcnt left at their maxima (gfx9 encoding:
-// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-__device__ __forceinline__ void wait_vmcnt0() {
-  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
-  asm volatile("" ::: "memory");
-}
-
 constexpr int kFaGroupRows = 128;  // query rows per workgroup
 constexpr int kFaBlock = 64;  // keys per block
 constexpr int kFaVPitch = kFaBlock + 4;
@@ -458,7 +445,7 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   // prologue: block 0
   issue_k(lds, 0);
   load_v(0);
-  wait_vmcnt0();  // K landed in LDS, V in registers
+  wait_vmcnt<0>();  // K landed in LDS, V in registers
   store_vt(lds);
   __syncthreads();
 
@@ -579,7 +566,7 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
       }
     }
     if (more) {
-      wait_vmcnt0();  // next K landed in LDS, next V in registers
+      wait_vmcnt<0>();  // next K landed in LDS, next V in registers
       store_vt(nxt);
     }
   };
