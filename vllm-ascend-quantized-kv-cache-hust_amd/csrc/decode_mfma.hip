@@ -684,17 +684,13 @@ struct WaveAcc {
       bias_v[v] = 0.0f;
     }
   }
-  // Epilogue: remove the PV offset, undo the 16x columns, add the minima, and
-  // write the item's (o, m, l) for heads 0..rep-1 of the group.
-  __device__ __forceinline__ void store(const LaneNib<CPG>& ln, int wi, int hq, int h, int rep,
-                                        int n, int kg, float* __restrict__ ws_o,
-                                        float* __restrict__ ws_ml) {
-    constexpr int D = 128;
+  // Epilogue: remove the PV offset, undo the 16x columns and add the minima;
+  // o[v*NJJ + jj][r] of the result is O[head 4*kg + r][dim_of(v, jj)].
+  __device__ __forceinline__ tail::Partial finish(const LaneNib<CPG>& ln, int kg) {
     constexpr int NJJ = CPG / 2;
-    constexpr int SUB = 16 / CPG;
 #pragma unroll
     for (int v = 0; v < NVS; ++v) bias_v[v] = sum_kg(bias_v[v]);
-    const int64_t head0 = static_cast<int64_t>(wi) * hq + h * rep;
+    tail::Partial p;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int hh = 4 * kg + r;
@@ -703,32 +699,74 @@ struct WaveAcc {
         const int vs_ = VG1 ? 0 : v;
         const float bv = __shfl(bias_v[vs_], hh, 64);
 #pragma unroll
-        for (int jj = 0; jj < NJJ; ++jj) {
-          const int dim = 8 * (n % CPG + CPG * v) + jj * SUB + n / CPG;
-          if (hh < rep)
-            ws_o[(head0 + hh) * D + dim] =
-                (o_acc[v * NJJ + jj][r] - c_acc[vs_][r]) * ln.col_scale + bv;
-        }
+        for (int jj = 0; jj < NJJ; ++jj)
+          p.o[v * NJJ + jj][r] = (o_acc[v * NJJ + jj][r] - c_acc[vs_][r]) * ln.col_scale + bv;
       }
     }
-    if (kg == 0 && n < rep) {
-      ws_ml[2 * (head0 + n)] = m_run;
-      ws_ml[2 * (head0 + n) + 1] = l_run;
-    }
+    p.m = m_run;
+    p.l = l_run;
+    return p;
   }
 };
 
+// Writes an int4-path partial for heads 0..rep-1 of kv head h's group.
+template <int CPG>
+__device__ __forceinline__ void store_partial(const tail::Partial& p, int wi, int hq, int h,
+                                              int rep, int n, int kg, float* __restrict__ ws_o,
+                                              float* __restrict__ ws_ml) {
+  constexpr int D = 128;
+  constexpr int NJJ = CPG / 2;
+  constexpr int SUB = 16 / CPG;
+  const int64_t head0 = static_cast<int64_t>(wi) * hq + h * rep;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int hh = 4 * kg + r;
+#pragma unroll
+    for (int v = 0; v < 16 / CPG; ++v)
+#pragma unroll
+      for (int jj = 0; jj < NJJ; ++jj) {
+        const int dim = 8 * (n % CPG + CPG * v) + jj * SUB + n / CPG;
+        if (hh < rep) ws_o[(head0 + hh) * D + dim] = p.o[v * NJJ + jj][r];
+      }
+  }
+  if (kg == 0 && n < rep) {
+    ws_ml[2 * (head0 + n)] = p.m;
+    ws_ml[2 * (head0 + n) + 1] = p.l;
+  }
+}
+
+// LDS of one wave: its two tile buffers, or the tail path's staging.
+template <int CPG, bool VG1, bool KSV, bool TAIL>
+__host__ __device__ constexpr int wave_lds_bytes() {
+  return TAIL && tail::kLdsBytes > 2 * Tile<CPG, VG1, KSV>::BYTES
+             ? tail::kLdsBytes
+             : 2 * Tile<CPG, VG1, KSV>::BYTES;
+}
+
+// A workgroup holds npair * hpw waves: kv heads q*hpw .. q*hpw + hpw - 1 of
+// its items, npair (1 or 2) waves per head.  With two, wave `half` 0 / 1 takes
+// the first / second 64-position chunk of every 128-position window of an
+// int4 item (the two halves of a 128-token page, whose key rows it thereby
+// fetches whole and at the same moment), and every other 32-position sub-tile
+// of a tail item; the halves' partials merge through LDS at the item's end.
+// A barrier per window keeps the workgroup's waves in step, so that the heads
+// sharing a value line (and a scale line) request it together as well.
+// (Measured on config-3 and config-5 decode, in-step groups cut the HBM
+// fetch by up to 17% but wait at the barriers for longer than that saves
+// while the kernel is bound by instruction issue: the launcher runs one wave
+// per (kv head, item) in a workgroup of its own.)
 // Without pieces (TAIL): the grid covers the work items twice; the first pass
 // takes the int4 (kind-0) items, the second the tail (kind-1) items, so every
 // tail wave is dispatched after every int4 wave and runs in the slots the
 // shorter int4 items free, with no second stream or event between the two.
-// With pieces (TAIL only): one wave per (piece, kv head) walks the piece's
-// items [pieces[k], pieces[k+1]) in order, int4 and tail alike; the host cuts
-// the pieces to about equal cost, so every wave of the single pass ends at
-// about the same time.
+// With pieces (TAIL only): one workgroup per (piece, head group) walks the
+// piece's items [pieces[k], pieces[k+1]) in order, int4 and tail alike; the
+// host cuts the pieces to about equal cost, so every workgroup of the single
+// pass ends at about the same time.
 template <typename TQ, int CPG, bool VG1, bool KSV, bool FOLD, bool TAIL>
-__global__ void __launch_bounds__(64, 2)
-kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qscale,
+__global__ void __launch_bounds__(512, 2)
+kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, int hpw, int npair,
+                        float qscale,
                         const uint32_t* __restrict__ kq, const float* __restrict__ ks,
                         const float* __restrict__ km, const uint32_t* __restrict__ vq,
                         const float* __restrict__ vs, const float* __restrict__ vm, int bs,
@@ -741,45 +779,55 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   using T = Tile<CPG, VG1, KSV>;
   constexpr int D = T::D;
   constexpr int GT = T::GT;
+  constexpr int WAVE_LDS = wave_lds_bytes<CPG, VG1, KSV, TAIL>();
 
   extern __shared__ __align__(16) char lds_raw[];
   const int32_t* pieces = TAIL ? pieces_arg : nullptr;
-  const int lane = threadIdx.x;
-  int it0, it1, h, pass = 0;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int hw = wave % hpw;    // head within the workgroup's group
+  const int half = wave / hpw;  // < npair
+  char* const my_lds = lds_raw + wave * WAVE_LDS;
+  // the half-1 partner of this wave's head hands its partial over here
+  float* const xfer = reinterpret_cast<float*>(lds_raw + (hw + hpw) * WAVE_LDS);
+  const int nq = kvh / hpw;
+  int it0, it1, qh, pass = 0;
   if (pieces) {
     int k;
-    if (!xcd_item_head(blockIdx.x, kvh, num_pieces, k, h)) return;
+    if (!xcd_item_head(blockIdx.x, nq, num_pieces, k, qh)) return;  // workgroup-uniform
     it0 = pieces[k];
     it1 = pieces[k + 1];
   } else {
-    const int64_t pass_len = xcd_grid_size(num_work, kvh);
+    const int64_t pass_len = xcd_grid_size(num_work, nq);
     pass = TAIL && blockIdx.x >= pass_len ? 1 : 0;
-    if (!xcd_item_head(blockIdx.x - pass * pass_len, kvh, num_work, it0, h)) return;
+    if (!xcd_item_head(blockIdx.x - pass * pass_len, nq, num_work, it0, qh)) return;
     it1 = it0 + 1;
   }
+  const int h = qh * hpw + hw;
+  const int rep = hq / kvh;
+  const int n = lane & 15;
+  const int kg = lane >> 4;
+  // every branch below depends on the work item only: workgroup-uniform, so
+  // every wave meets the same barriers
   for (int wi = it0; wi < it1; ++wi) {
   const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
   const int kind = wk[3];
-  // without pieces the other pass (or the tail kernel) owns it (uniform);
+  // without pieces the other pass (or the tail kernel) owns it;
   // kinds 0, 2 and 3 are int4 ranges, kind 1 the tail
   if (!pieces && (kind == 1 ? 1 : 0) != pass) continue;
   if constexpr (TAIL) {
     if (kind == 1) {
-      tail::tail_item<TQ>(lds_raw, query, hq, kvh, qscale, kq, ks, km, vq, vs, vm, bs, g, nb,
-                          block_table, maxb, seq_meta, wk, wi, h, ring_k, ring_v, ring_len,
-                          ws_o, ws_ml);
+      tail::Partial tp = tail::tail_item<TQ>(my_lds, query, hq, kvh, qscale, kq, ks, km, vq, vs,
+                                             vm, bs, g, nb, block_table, maxb, seq_meta, wk, wi,
+                                             h, ring_k, ring_v, ring_len, half, npair);
+      if (npair == 2) tail::merge_halves(tp, xfer, half, lane);
+      if (half == 0) tail::tail_store(tp, wi, hq, h, rep, lane, ws_o, ws_ml);
       continue;
     }
   }
   const int b = wk[0];
   const int pb = wk[1];
   const int pe = wk[2];
-  // kind 2 / 3: only the even / odd 64-position chunks of [pb, pe) (the
-  // other half is the paired item's, on the same XCD)
-  const int half = kind >= 2 ? kind - 2 : -1;
-  const int rep = hq / kvh;
-  const int n = lane & 15;
-  const int kg = lane >> 4;
   const int gpb = bs / g;
   const int ng = D / g;
   const int wpd = bs / 8;
@@ -804,19 +852,22 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
                          ks + krow * gpb + (off0 >> gsh), km + krow * gpb + (off0 >> gsh), gpb,
                          vs + vtok * ng, vm + vtok * ng, ng, g, with_ks);
   };
-  // the wave's tiles: every GT-aligned tile of [pb, pe), or with a half only
-  // those in its 64-position chunks
+  // 64-position chunks: window k holds chunk cb + cs*k + (cs/npair)*half of
+  // each half.  Kind 0: the (64*npair)-aligned windows over [pb, pe); kind 2 /
+  // 3 (only the even / odd chunks of [pb, pe)): npair of its chunks.  Items
+  // start on multiples of 64, so chunks are 64-aligned and hold whole tiles.
+  const int hs = kind >= 2 ? kind - 2 : -1;
+  const int cb = hs < 0 ? (pb & ~(64 * npair - 1)) : pb + 64 * hs;
+  const int cs = 64 * npair * (hs < 0 ? 1 : 2);
+  const int nwin = (pe - cb + cs - 1) / cs;
+  int p_first = cb + (cs / npair) * half;
+  if (p_first < pb) p_first += cs;  // kind 0 from an odd chunk: half 0 starts a window later
+  // the wave's tile after p: the next tile of its chunk, else its next chunk
   auto next_tile = [&](int p) {
     p += GT;
-    if (half >= 0 && ((p - pb) >> 6 & 1) != half) p += 64;
+    if ((p & 63) == 0) p += cs - 64;
     return p;
   };
-  auto prev_tile = [&](int p) {
-    p -= GT;
-    if (half >= 0 && ((p - pb) >> 6 & 1) != half) p -= 64;
-    return p;
-  };
-  const int p_first = half == 1 ? pb + 64 : pb;
   // One tile step: DMA of the wave's next tile into `nxt`, then compute tile
   // p0 from `cur`.  Both buffers are __restrict__ within the step, which tells the
   // compiler's wait-count pass that the reads of `cur` cannot alias the DMA
@@ -824,7 +875,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
   // next tile -- in front of the first LDS read and the double buffer never
   // overlaps.  The wait for tile p0 itself is explicit.
   QGroup qg;
-  auto step = [&](const char* __restrict__ cur, char* __restrict__ nxt, int p0) {
+  auto step = [&](const char* __restrict__ cur, char* __restrict__ nxt, int p0, bool new_group) {
     const int p1 = next_tile(p0);
     if (p1 < pe) {
       // a tile needs the key scales exactly when its key group differs from
@@ -842,8 +893,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
     const uint32_t* W = reinterpret_cast<const uint32_t*>(cur);
     // tiles are GT-aligned and GT divides g: the wave's first tile, or one in
     // another key group than its previous tile, prepares the group's Q'
-    if (p0 == p_first || (p0 >> gsh) != (prev_tile(p0) >> gsh))
-      prepare_group<TQ, CPG, FOLD, KSV>(W, n, kg, qv, qscale, qg);
+    if (new_group) prepare_group<TQ, CPG, FOLD, KSV>(W, n, kg, qv, qscale, qg);
     const WaveValues<CPG, VG1> vals(W, kg, n % CPG);
     if (p0 + GT <= pe)
       compute_tile<TQ, CPG, VG1, true, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run,
@@ -852,16 +902,26 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, float qsc
       compute_tile<TQ, CPG, VG1, false, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run,
                                               acc.l_run, acc.o_acc, acc.c_acc, acc.bias_v);
   };
-  if (p_first < pe) issue(lds_raw, p_first, true);  // prologue: tile 0 into buffer 0
+  if (p_first < pe) issue(my_lds, p_first, true);  // prologue: tile 0 into buffer 0
   int cur = 0;
-  for (int p0 = p_first; p0 < pe; p0 = next_tile(p0)) {
-    step(lds_raw + cur * T::BYTES, lds_raw + (cur ^ 1) * T::BYTES, p0);
-    // every LDS read of this buffer has been consumed before the next
-    // iteration's DMA may overwrite it
-    asm volatile("" ::: "memory");
-    cur ^= 1;
+  int p = p_first;
+  int g_prev = -1;  // key group of the wave's previous tile
+  for (int k = 0; k < nwin; ++k) {
+    __builtin_amdgcn_s_barrier();  // the workgroup's waves enter window k together
+    const int wend = cb + cs * (k + 1);
+    while (p < pe && p < wend) {
+      step(my_lds + cur * T::BYTES, my_lds + (cur ^ 1) * T::BYTES, p, (p >> gsh) != g_prev);
+      // every LDS read of this buffer has been consumed before the next
+      // iteration's DMA may overwrite it
+      asm volatile("" ::: "memory");
+      cur ^= 1;
+      g_prev = p >> gsh;
+      p = next_tile(p);
+    }
   }
-  acc.store(ln, wi, hq, h, rep, n, kg, ws_o, ws_ml);
+  tail::Partial part = acc.finish(ln, kg);
+  if (npair == 2) tail::merge_halves(part, xfer, half, lane);
+  if (half == 0) store_partial<CPG>(part, wi, hq, h, rep, n, kg, ws_o, ws_ml);
   }  // items
 }
 
@@ -901,6 +961,19 @@ __global__ void mfma_layout_probe_kernel(const _Float16* __restrict__ a,
 
 namespace kvq {
 
+// Waves per (kv head, item) and kv heads per workgroup of the INT4 decode.
+// (kivi_plan.cpp counts 8 / kDecodeWavesPerHead (kv head, piece) slots per CU.)
+constexpr int kDecodeWavesPerHead = 1;
+constexpr int kDecodeHeadsPerWg = 1;
+
+// LDS per wave of the kernel instance these parameters select.
+template <bool TAIL>
+int64_t wave_lds_of(int cpg, bool vg1, bool ksv) {
+  if (cpg != 8) return wave_lds_bytes<4, false, false, TAIL>();
+  if (ksv) return wave_lds_bytes<8, true, true, TAIL>();
+  return vg1 ? wave_lds_bytes<8, true, false, TAIL>() : wave_lds_bytes<8, false, false, TAIL>();
+}
+
 int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int d, float qscale,
                             const int32_t* kq, const float* ks, const float* km,
                             const int32_t* vq, const float* vs, const float* vm, int bs, int g,
@@ -919,30 +992,38 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
   if (bs % (8 * cpg)) return KVQ_OK;
   const uint32_t* kqu = reinterpret_cast<const uint32_t*>(kq);
   const uint32_t* vqu = reinterpret_cast<const uint32_t*>(vq);
-  const int64_t pass_len = xcd_grid_size(num_work, kvh);
   const bool tail = tail_path_applies(q_dtype, hq, kvh, d, ring_dtype, bs);
   // pieces need the tail path (a piece mixes int4 and tail items)
   const bool use_pieces = tail && pieces && num_pieces > 0;
-  const int64_t blocks =
-      use_pieces ? xcd_grid_size(num_pieces, kvh) : (tail ? 2 : 1) * pass_len;
-  if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
-  const int32_t* pieces_k = use_pieces ? pieces : nullptr;
-  const dim3 grid(static_cast<unsigned>(blocks));
-  const dim3 block(64);
   // GQA groups of at most 8 heads fold the hi/lo score parts into one MFMA
   const bool fold = hq / kvh <= 8;
   // one value group per head row: value scales gathered once per PV k-step
   const bool vg1 = cpg == 8 && g >= 128;
   // a key group per page: its scales are contiguous per head
   const bool ksv = vg1 && bs == g;
-  const size_t lds_int4 =
-      2 * static_cast<size_t>(cpg == 8 ? (vg1 ? Tile<8, true>::BYTES : Tile<8>::BYTES)
-                                       : Tile<4>::BYTES);
-  const size_t lds_tail = static_cast<size_t>(tail::kLdsBytes);
-  const size_t lds = tail && lds_tail > lds_int4 ? lds_tail : lds_int4;
+  const int64_t wave_lds = tail ? wave_lds_of<true>(cpg, vg1, ksv) : wave_lds_of<false>(cpg, vg1, ksv);
+  int64_t lds_max = 0;  // LDS one workgroup may use on this device
+  const int lrc = device_lds_max(&lds_max);
+  if (lrc != KVQ_OK) return lrc;
+  // waves per kv head, and kv heads per workgroup: as many as the heads and
+  // the LDS allow, up to kDecodeHeadsPerWg
+  const int npair = kDecodeWavesPerHead;
+  int hpw = kDecodeHeadsPerWg;
+  while (hpw > 1 && (kvh % hpw || npair * hpw * wave_lds > lds_max)) hpw /= 2;
+  if (npair * wave_lds > lds_max) return KVQ_OK;  // not this device: the portable kernels run
+  const int nq = kvh / hpw;
+  const int64_t pass_len = xcd_grid_size(num_work, nq);
+  const int64_t blocks =
+      use_pieces ? xcd_grid_size(num_pieces, nq) : (tail ? 2 : 1) * pass_len;
+  if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
+  const int32_t* pieces_k = use_pieces ? pieces : nullptr;
+  const dim3 grid(static_cast<unsigned>(blocks));
+  const dim3 block(64 * npair * hpw);
+  const size_t lds = static_cast<size_t>(npair * hpw * wave_lds);
 #define KVQ_LAUNCH_MFMA(TQ, C, V, KV, F, TL)                                                  \
   hipLaunchKernelGGL((kivi_decode_mfma_kernel<TQ, C, V, KV, F, TL>), grid, block, lds, s,    \
-                     static_cast<const TQ*>(query), hq, kvh, qscale, kqu, ks, km, vqu, vs, vm,\
+                     static_cast<const TQ*>(query), hq, kvh, hpw, npair, qscale, kqu, ks, km, \
+                     vqu, vs, vm,                                                             \
                      bs, g, nb, block_table, maxb, seq_meta, work, num_work, pieces_k,       \
                      num_pieces, static_cast<const TQ*>(ring_k), static_cast<const TQ*>(ring_v),\
                      ring_len, ws_o, ws_ml)

@@ -19,7 +19,9 @@
 //     consumed by then) and computes O = P * V with P split into two T parts
 //     (hi + lo), so p keeps ~16 bits;
 //   * leaves (m, l, o) per head in the split-K workspace for the combine.
-// LDS: 2 * kTT * kKP * 2 bytes = 17 KiB, inside the int4 path's 20 KiB per wave.
+// LDS: 2 * kTT * kKP * 2 bytes = 17 KiB, inside the int4 path's 19-20 KiB per wave.
+// Two waves may share an item: wave `half` of `nhalf` takes every nhalf-th
+// sub-tile, and the halves' partial results merge through LDS (merge_halves).
 #pragma once
 
 #include "kvq_common.h"
@@ -98,6 +100,51 @@ __device__ __forceinline__ int ring_lane(int x, int ring_len) {
   return x < ring_len ? (x < 0 ? 0 : x) : ring_len - 1;
 }
 
+// One wave's partial attention result for one work item and kv head, in the
+// lane layout of the path that produced it: o[q][r] belongs to query head
+// 4*kg + r of the GQA group and one head dim fixed by (q, lane); m and l are
+// the log2-domain running max and sum of head n = lane % 16.
+struct Partial {
+  f4 o[8];
+  float m, l;
+};
+
+// Two waves of a workgroup (half 0 and half 1) split an item's positions; the
+// half-1 wave hands its partial to its half-0 partner through `xfer` (LDS of
+// at least 34 * 64 floats that only the half-1 wave writes), and the half-0
+// wave folds it into its own, as the split-K combine would.  Every wave of the
+// workgroup calls this, under workgroup-uniform control flow: two barriers.
+__device__ __forceinline__ void merge_halves(Partial& p, float* __restrict__ xfer, int half,
+                                             int lane) {
+  f4* xo = reinterpret_cast<f4*>(xfer);
+  if (half == 1) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) xo[q * 64 + lane] = p.o[q];
+    xfer[32 * 64 + lane] = p.m;
+    xfer[33 * 64 + lane] = p.l;
+  }
+  __syncthreads();
+  if (half == 0) {
+    const float mb = xfer[32 * 64 + lane];
+    const float lb = xfer[33 * 64 + lane];
+    const float mx = fmaxf(p.m, mb);
+    // an empty half has m = -inf, l = 0, o = 0: weight 0 (and no inf - inf)
+    const float sa = p.m == -INFINITY ? 0.0f : exp2f(p.m - mx);
+    const float sb = mb == -INFINITY ? 0.0f : exp2f(mb - mx);
+    const int kg = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float ar = __shfl(sa, 4 * kg + r, 64);
+      const float br = __shfl(sb, 4 * kg + r, 64);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) p.o[q][r] = p.o[q][r] * ar + xo[q * 64 + lane][r] * br;
+    }
+    p.l = p.l * sa + lb * sb;
+    p.m = mx;
+  }
+  __syncthreads();  // the partner's region is free again
+}
+
 constexpr int kD = 128;
 constexpr int kTT = 32;          // positions per sub-tile
 constexpr int kKP = kD + 8;      // K row pitch (elements): rows stay 16-byte aligned
@@ -106,9 +153,10 @@ constexpr int kKW = kTT / 8 + 1;  // key words of one dim covering a sub-tile (8
 constexpr int kLdsBytes = 2 * kTT * kKP * 2;
 static_assert(kD * kVP <= 2 * kTT * kKP, "V^T fits the key region it reuses");
 
-// Work item wi (kind 1) for kv head h.  lds_raw: at least kLdsBytes.
+// Work item wi (kind 1) for kv head h: the partial over sub-tiles half,
+// half + nhalf, ... of the item.  lds_raw: at least kLdsBytes, the wave's own.
 template <typename T>
-__device__ __forceinline__ void tail_item(char* __restrict__ lds_raw, const T* __restrict__ query,
+__device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T* __restrict__ query,
                                           int hq, int kvh, float qscale,
                                           const uint32_t* __restrict__ kq,
                                           const float* __restrict__ ks,
@@ -121,7 +169,7 @@ __device__ __forceinline__ void tail_item(char* __restrict__ lds_raw, const T* _
                                           const int32_t* __restrict__ wk, int wi, int h,
                                           const T* __restrict__ ring_k,
                                           const T* __restrict__ ring_v, int ring_len,
-                                          float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+                                          int half, int nhalf) {
   constexpr int D = kD;
   uint16_t* sk = reinterpret_cast<uint16_t*>(lds_raw);  // [kTT][kKP] key hi parts
   uint16_t* skl = sk + kTT * kKP;                        // [kTT][kKP] key lo parts
@@ -162,7 +210,7 @@ __device__ __forceinline__ void tail_item(char* __restrict__ lds_raw, const T* _
 #pragma unroll
   for (int q = 0; q < 8; ++q) o_acc[q] = f4{0.f, 0.f, 0.f, 0.f};
 
-  for (int p0 = pb; p0 < pe; p0 += kTT) {
+  for (int p0 = pb + kTT * half; p0 < pe; p0 += kTT * nhalf) {
     const int nt = (pe - p0) < kTT ? (pe - p0) : kTT;
     // one wave: its LDS accesses take effect in program order, so the previous
     // sub-tile's reads are done before these writes
@@ -368,19 +416,33 @@ __device__ __forceinline__ void tail_item(char* __restrict__ lds_raw, const T* _
     }
   }
 
-  // ---- epilogue: o_acc[q][r] = O[head 4*kg + r][dim 16*q + n] ------------------
+  Partial res;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) res.o[q] = o_acc[q];
+  res.m = m_run;
+  res.l = l_run;
+  return res;
+}
+
+// Writes a tail partial for heads 0..rep-1 of kv head h's group: o[q][r] is
+// O[head 4*kg + r][dim 16*q + n].
+__device__ __forceinline__ void tail_store(const Partial& p, int wi, int hq, int h, int rep,
+                                           int lane, float* __restrict__ ws_o,
+                                           float* __restrict__ ws_ml) {
+  const int n = lane & 15;
+  const int kg = lane >> 4;
   const int64_t head0 = static_cast<int64_t>(wi) * hq + h * rep;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int hh = 4 * kg + r;
     if (hh < rep) {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) ws_o[(head0 + hh) * D + 16 * q + n] = o_acc[q][r];
+      for (int q = 0; q < 8; ++q) ws_o[(head0 + hh) * kD + 16 * q + n] = p.o[q][r];
     }
   }
   if (kg == 0 && n < rep) {
-    ws_ml[2 * (head0 + n)] = m_run;
-    ws_ml[2 * (head0 + n) + 1] = l_run;
+    ws_ml[2 * (head0 + n)] = p.m;
+    ws_ml[2 * (head0 + n) + 1] = p.l;
   }
 }
 

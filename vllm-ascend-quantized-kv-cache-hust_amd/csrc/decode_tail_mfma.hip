@@ -25,9 +25,10 @@ kivi_decode_tail_mfma_kernel(const T* __restrict__ query, int hq, int kvh, float
   if (!xcd_item_head(blockIdx.x, kvh, num_work, wi, h)) return;
   const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
   if (wk[3] != 1) return;  // kind-0 items belong to the int4 kernels (uniform)
-  tail::tail_item<T>(lds_raw, query, hq, kvh, qscale, kq, ks, km, vq, vs, vm, bs, g, nb,
-                     block_table, maxb, seq_meta, wk, wi, h, ring_k, ring_v, ring_len, ws_o,
-                     ws_ml);
+  const tail::Partial p =
+      tail::tail_item<T>(lds_raw, query, hq, kvh, qscale, kq, ks, km, vq, vs, vm, bs, g, nb,
+                         block_table, maxb, seq_meta, wk, wi, h, ring_k, ring_v, ring_len, 0, 1);
+  tail::tail_store(p, wi, hq, h, hq / kvh, threadIdx.x & 63, ws_o, ws_ml);
 }
 
 }  // namespace

@@ -25,7 +25,9 @@
 
 namespace {
 
-constexpr int kWavesPerCu = 8;          // decode waves resident per CU
+// (piece, kv head) slots per CU: the decode kernel keeps 8 waves resident per
+// CU, one per (piece, kv head) (8 / kDecodeWavesPerHead of decode_mfma.hip)
+constexpr int kHeadSlotsPerCu = 8;
 constexpr double kPieceMaxCost = 4096;  // int4 positions per piece before a second round
 constexpr int kTailItemTokens = 64;     // positions per tail item in split plans
 
@@ -65,7 +67,7 @@ struct Planner {
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 int64_t slots_for(int kvh, int cu_count) {
-  return std::max<int64_t>(1, static_cast<int64_t>(cu_count) * kWavesPerCu / std::max(1, kvh));
+  return std::max<int64_t>(1, static_cast<int64_t>(cu_count) * kHeadSlotsPerCu / std::max(1, kvh));
 }
 
 // Cost of the whole batch in int4-position units: int4 ranges in 64-position
@@ -184,12 +186,12 @@ extern "C" int64_t kvq_plan_kivi_decode(const int32_t* seqs, int64_t batch, int 
     if (total_cost(pl, tail_cost) <= static_cast<double>(slots) * kPieceMaxCost) {
       mode = KVQ_PLAN_PIECES;
     } else {
-      // paired items: each wave still takes split_tokens int4 positions
+      // items of up to 8192 positions
       int64_t positions = 0;
       for (int64_t b = 0; b < batch; ++b) positions += seqs[6 * b];
       const int64_t per_item = ceil_div(ceil_div(positions, slots), 128) * 128;
-      split_tokens = std::min<int64_t>(4096, std::max<int64_t>(256, per_item));
-      mode = KVQ_PLAN_SPLIT_PAIRED;
+      split_tokens = std::min<int64_t>(8192, std::max<int64_t>(256, per_item));
+      mode = KVQ_PLAN_SPLIT;
     }
   }
   switch (mode) {
