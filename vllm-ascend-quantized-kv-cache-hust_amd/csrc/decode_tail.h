@@ -212,11 +212,11 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
 
   for (int p0 = pb + kTT * half; p0 < pe; p0 += kTT * nhalf) {
     const int nt = (pe - p0) < kTT ? (pe - p0) : kTT;
+    const int mk = khist - p0 < 0 ? 0 : (khist - p0 < nt ? khist - p0 : nt);  // int4 keys
     // one wave: its LDS accesses take effect in program order, so the previous
     // sub-tile's reads are done before these writes
     // ---- K rows -------------------------------------------------------------
     {
-      const int mk = khist - p0 < 0 ? 0 : (khist - p0 < nt ? khist - p0 : nt);  // int4 keys
       if (mk > 0) {
         // lane: dims 2*lane and 2*lane + 1, the <= kKW words of each covering
         // positions [p0, p0+mk); the two dims of a token go out as one pair
@@ -254,7 +254,8 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
           }
         }
       }
-      // ring keys: task = (position, 16-byte chunk), copied as is
+      // ring keys: task = (position, 16-byte chunk), copied as is; their lo
+      // parts are zero and only read when the sub-tile also holds int4 keys
       const int tasks = (nt - mk) * (D / 8);
       for (int t0 = 0; t0 < tasks; t0 += 64 * 4) {
         uint4 x[4];
@@ -273,7 +274,8 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
           if (t < tasks) {
             const int pi = mk + t / (D / 8);
             *reinterpret_cast<uint4*>(sk + pi * kKP + 8 * (t % (D / 8))) = x[k];
-            *reinterpret_cast<uint4*>(skl + pi * kKP + 8 * (t % (D / 8))) = make_uint4(0, 0, 0, 0);
+            if (mk > 0)
+              *reinterpret_cast<uint4*>(skl + pi * kKP + 8 * (t % (D / 8))) = make_uint4(0, 0, 0, 0);
           }
         }
       }
@@ -287,9 +289,11 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
       for (int s4 = 0; s4 < 4; ++s4) {
         const int o = (16 * jm + n) * kKP + 32 * s4 + 8 * kg;
         const u8v a = *reinterpret_cast<const u8v*>(sk + o);
-        const u8v al = *reinterpret_cast<const u8v*>(skl + o);
         sacc[jm] = mfma16(a, qb[s4], sacc[jm], T{});
-        sacc[jm] = mfma16(al, qb[s4], sacc[jm], T{});
+        if (mk > 0) {  // uniform: key lo parts exist only for int4 keys
+          const u8v al = *reinterpret_cast<const u8v*>(skl + o);
+          sacc[jm] = mfma16(al, qb[s4], sacc[jm], T{});
+        }
       }
     }
     float tmax = -INFINITY;
