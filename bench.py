@@ -651,9 +651,9 @@ def bench_int8_decode(torch, dev, *, reps=20, seed=0, layers=2):
         int8_calc_scales,
         int8_decode_attention,
         int8_quant_scatter,
+        int8_split_tokens,
         plan_int8_work,
     )
-    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import choose_split_tokens
 
     b, hq, kvh, d, bs, n = 64, 32, 8, 128, 128, 4096
     nb = b * n // bs
@@ -678,7 +678,7 @@ def bench_int8_decode(torch, dev, *, reps=20, seed=0, layers=2):
         caches.append((kc, vc, k_aq, v_aq))
     q = torch.randn((b, hq, d), generator=gdev, device=dev).to(torch.bfloat16)
     lens = [n] * b
-    meta, work = plan_int8_work(lens, choose_split_tokens(sum(lens), kvh))
+    meta, work = plan_int8_work(lens, int8_split_tokens(sum(lens), kvh))
     plan = (torch.from_numpy(meta).to(dev), torch.from_numpy(work).to(dev))
     out = torch.empty_like(q)
 

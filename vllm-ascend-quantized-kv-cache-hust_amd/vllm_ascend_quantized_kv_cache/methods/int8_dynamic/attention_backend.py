@@ -183,7 +183,7 @@ class AscendInt8AttentionBackendMixin:
     def _forward_int8_decode_step(self, query: Any, key: Any, value: Any, attn_metadata: Any,
                                   output: Any, layer: Any) -> Any:
         """Quantize + scatter, fused decode and combine over one staged plan."""
-        from ...ops.kivi_decode import choose_split_tokens
+        from ...ops.int8_ops import int8_split_tokens
         from .decode_step import Int8StepBuffers, launch_int8_step
 
         lens = [int(x) for x in attn_metadata.seq_lens_list]
@@ -197,7 +197,7 @@ class AscendInt8AttentionBackendMixin:
                 f"int8_decode_attention: a sequence length exceeds its block table "
                 f"({max(lens)} > {table.shape[1]} x {bs})"
             )
-        split = choose_split_tokens(sum(lens), self.num_kv_heads)
+        split = int8_split_tokens(sum(lens), self.num_kv_heads)
         need = b + sum(-(-n // split) for n in lens)
         bufs = getattr(self, "_int8_step_bufs", None)
         if bufs is None or bufs.batch < b or bufs.work_cap < need:

@@ -18,8 +18,7 @@ import numpy as np
 import torch
 
 from ...ops import _native
-from ...ops.int8_ops import plan_int8_work
-from ...ops.kivi_decode import choose_split_tokens
+from ...ops.int8_ops import int8_split_tokens, plan_int8_work
 
 
 class Int8StepBuffers:
@@ -124,7 +123,7 @@ class Int8DecodeGraph:
         bs = kc.shape[1]
         self.impl, self.layer, self.batch = impl, layer, batch
         self.max_len = max_blocks * bs
-        # each step splits as an eager step does (choose_split_tokens, at
+        # each step splits as an eager step does (int8_split_tokens, at
         # least 256 positions per item), so the capacity is the item count at
         # the smallest split
         work_cap = batch * (-(-self.max_len // 256)) + batch
@@ -139,7 +138,7 @@ class Int8DecodeGraph:
         if len(lens) != self.batch or max(lens) > self.max_len:
             raise RuntimeError("INT8 decode graph: the step does not fit the captured shape.")
         slots = impl._int8_host_slots(attn_metadata, len(lens))
-        split = choose_split_tokens(sum(lens), impl.num_kv_heads)
+        split = int8_split_tokens(sum(lens), impl.num_kv_heads)
         self.num_work = self.bufs.stage(slots, lens, split, fixed=True)
         table = attn_metadata.block_tables[: self.batch]
         self.table[:, : table.shape[1]].copy_(table, non_blocking=True)

@@ -11,7 +11,22 @@ import numpy as np
 import torch
 
 from . import _native
-from .kivi_decode import choose_split_tokens
+
+#: INT8 decode waves per CU the default plan aims at.  Its waves are long
+#: streams of 128-byte rows whose setup (Q' split, epilogue, one partial per
+#: item for the combine) costs as much as a few tiles: on config 2 (64 x 4096
+#: tokens, 8 KV heads) items of 2048 positions (4 waves per CU) decode in 112
+#: us against 119 us for 1024 (8 per CU), 130 us for 1536 and 169 us for 4096.
+INT8_DECODE_WAVES_PER_CU = 4
+
+
+def int8_split_tokens(total_positions: int, num_kv_heads: int, cu_count: int = 256) -> int:
+    """Positions per INT8 decode item: about INT8_DECODE_WAVES_PER_CU waves
+    per CU, in [256, 4096], a multiple of 128."""
+    target_items = max(1, (cu_count * INT8_DECODE_WAVES_PER_CU) // max(1, num_kv_heads))
+    per_item = -(-total_positions // target_items)
+    per_item = -(-per_item // 128) * 128
+    return int(min(4096, max(256, per_item)))
 
 
 def int8_calc_scales(key: torch.Tensor, value: torch.Tensor):
@@ -151,7 +166,7 @@ def int8_decode_attention(
         )
     if plan is None:
         if split_tokens is None:
-            split_tokens = choose_split_tokens(int(sum(seq_lens)), kvh)
+            split_tokens = int8_split_tokens(int(sum(seq_lens)), kvh)
         meta_np, work_np = plan_int8_work(seq_lens, split_tokens)
         meta = torch.from_numpy(meta_np).to(query.device)
         work = torch.from_numpy(work_np).to(query.device)
@@ -203,10 +218,12 @@ def int8_dequantize(x: torch.Tensor, inv: torch.Tensor, target_dtype) -> torch.T
 
 
 __all__ = [
+    "INT8_DECODE_WAVES_PER_CU",
     "int8_calc_scales",
     "int8_decode_attention",
     "int8_dequant_gather",
     "int8_dequantize",
+    "int8_split_tokens",
     "int8_quant_scatter",
     "int8_quantize",
     "plan_int8_work",
