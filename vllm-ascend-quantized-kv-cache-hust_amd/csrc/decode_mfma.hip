@@ -752,9 +752,11 @@ __host__ __device__ constexpr int wave_lds_bytes() {
 // A barrier per window keeps the workgroup's waves in step, so that the heads
 // sharing a value line (and a scale line) request it together as well.
 // (Measured on config-3 and config-5 decode, in-step groups cut the HBM
-// fetch by up to 17% but wait at the barriers for longer than that saves
-// while the kernel is bound by instruction issue: the launcher runs one wave
-// per (kv head, item) in a workgroup of its own.)
+// fetch by up to 17% but wait at the barriers for longer than that saves:
+// the launcher runs one wave per (kv head, item) in a workgroup of its own.
+// The general form stays: with npair and hpw as run-time values the kernel
+// allocates 233 VGPRs and spills nothing, while a one-wave-only copy of the
+// same loop spills.)
 // Without pieces (TAIL): the grid covers the work items twice; the first pass
 // takes the int4 (kind-0) items, the second the tail (kind-1) items, so every
 // tail wave is dispatched after every int4 wave and runs in the slots the

@@ -250,29 +250,31 @@ prefill_attn_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
 //   K  [64][D]    written by global_load_lds (16-byte lanes); the 16-byte
 //                 column of each row is XOR-swizzled by the row so that the
 //                 16 rows one score MFMA reads sit in different banks;
-//   V^T [D][64+4] written from registers: a thread loads 4 keys x 8 dims and
-//                 stores each dim's 4 keys as one 8-byte word (neighbouring
-//                 lanes hold neighbouring key quads: conflict-free stores), so
-//                 the PV operand (4 consecutive keys of one dim) is an 8-byte
-//                 read.
-// While block i is computed, block i+1's K is in flight (DMA) and its V sits in
-// registers until the compute is done.
+//   V  [64][D]    written by global_load_lds too, row-major; 16-byte column
+//                 c of row r stored at c ^ 2*(r % 4), so that the four rows
+//                 one transposing read covers sit in different banks.
+// While block i is computed, block i+1's K and V are in flight (DMA).
 //   S^T = K * Q^T: A = 16 keys x 32 dims (one 16-byte read per lane), B = the
 //                  wave's Q^T (registers), each A feeding both column groups.
 //   O^T += V^T * P^T: B = P^T straight from the S^T registers (the lane's
 //                  keys 16*(2ks + i/4) + 4*kg + i%4 of its query column),
-//                  A = the same 8 keys of one dim from V^T (two 8-byte reads).
+//                  A = the same 8 keys of one dim, gathered out of the
+//                  row-major V by two transposing LDS reads
+//                  (ds_read_b64_tr_b16: within each 16-lane group, lane l gets
+//                  element l % 4 of the 8-byte runs that lanes l / 4 + 4k
+//                  address, k = 0..3).
 // The rescale needs no shuffles: S^T and O^T both put the lane's query in
 // its column.
 
 constexpr int kFaGroupRows = 128;  // query rows per workgroup
 constexpr int kFaBlock = 64;  // keys per block
-constexpr int kFaVPitch = kFaBlock + 4;
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s* lds_v4s_ptr;
 
 template <int D>
 struct FaLds {
   static constexpr int K_BYTES = kFaBlock * D * 2;
-  static constexpr int V_BYTES = D * kFaVPitch * 2;
+  static constexpr int V_BYTES = kFaBlock * D * 2;
   static constexpr int BUF = K_BYTES + V_BYTES;
   static constexpr int BYTES = 2 * BUF;
 };
@@ -298,12 +300,8 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   constexpr int PPR = D / 8;      // 16-byte pieces per row
   constexpr int RPI = 64 / PPR;   // K rows per DMA instruction
   constexpr int KINST = kFaBlock / RPI / kFaWaves;  // DMA instructions per wave per block
-  // V^T staging: task = (KPT consecutive keys, 16-byte piece of the row); two
-  // keys a task when the workgroup has a thread for each, else four
-  constexpr int KPT = (kFaBlock / 2) * PPR <= 64 * kFaWaves ? 2 : 4;
-  constexpr int VTASKS = (kFaBlock / KPT) * PPR;   // tasks per block
-  static_assert(KINST >= 1 && kFaBlock % (RPI * kFaWaves) == 0, "K DMA split");
-  static_assert(VTASKS <= 64 * kFaWaves, "one V task per thread");
+  static_assert(KINST >= 1 && kFaBlock % (RPI * kFaWaves) == 0, "K / V DMA split");
+  static_assert(PPR >= 8, "V swizzle 2 * (r % 4) stays inside the row");
   extern __shared__ __align__(16) char lds[];
 
   // heavy query blocks first: block x = qblocks - 1 - blockIdx.x
@@ -351,78 +349,41 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   const T* kbase = k + (static_cast<int64_t>(k_start) * kvh + kvhead) * D;
   const T* vbase = v + (static_cast<int64_t>(k_start) * kvh + kvhead) * D;
   const int64_t row_stride = static_cast<int64_t>(kvh) * D;
-  // per-lane element offsets of the K rows this lane moves (row r of the
-  // block, swizzled piece), relative to the block's first row
-  int64_t koff[KINST];
+  // per-lane element offsets of the K and V rows this lane moves (row r of
+  // the block, swizzled piece), relative to the block's first row
+  int64_t koff[KINST], voff[KINST];
   int krow[KINST];
 #pragma unroll
   for (int i = 0; i < KINST; ++i) {
     const int inst = wave * KINST + i;
     const int r = inst * RPI + lane / PPR;  // block row of this lane
-    const int piece = (lane % PPR) ^ (r % PPR);  // swizzled column
     krow[i] = r;
-    koff[i] = r * row_stride + 8 * piece;
+    koff[i] = r * row_stride + 8 * ((lane % PPR) ^ (r % PPR));
+    voff[i] = r * row_stride + 8 * ((lane % PPR) ^ (2 * (r % 4)));
   }
-  auto issue_k = [&](char* buf, int kb) {
+  // DMA of block rows kb .. kb + 63 of `base` into `dst` with the lane
+  // offsets `off`; rows past the end read the last row (masked later)
+  auto issue_rows = [&](const T* base, const int64_t (&off)[KINST], char* dst, int kb) {
     const bool whole = kb + kFaBlock <= lk;  // uniform: only the last block clamps
 #pragma unroll
     for (int i = 0; i < KINST; ++i) {
       const int inst = wave * KINST + i;
-      const T* src = kbase + kb * row_stride + koff[i];
-      if (!whole && kb + krow[i] >= lk)  // rows past the end: a valid row, masked later
-        src = kbase + static_cast<int64_t>(lk - 1) * row_stride + (koff[i] - krow[i] * row_stride);
-      dma16(src, buf + 1024 * inst);
+      const T* src = base + kb * row_stride + off[i];
+      if (!whole && kb + krow[i] >= lk)
+        src = base + static_cast<int64_t>(lk - 1) * row_stride + (off[i] - krow[i] * row_stride);
+      dma16(src, dst + 1024 * inst);
     }
   };
-  // V task of this thread: keys KPT*j .. KPT*j + KPT - 1, piece c (dims 8c ..
-  // 8c + 7).  Lanes next to each other take consecutive key groups, so a
-  // quarter-wave's transposed stores (row 8c + i, keys KPT*j ..) are contiguous.
-  constexpr int NJ = kFaBlock / KPT;
-  const int vj = tid % NJ;
-  const int vc = tid / NJ;
-  const bool vtask = tid < VTASKS;
-  uint4 vr[KPT];
-  const T* vlane = vbase + (KPT * vj) * row_stride + 8 * vc;
-  auto load_v = [&](int kb) {
-    if (!vtask) return;
-    if (kb + kFaBlock <= lk) {  // uniform: only the last block clamps
-      const T* src = vlane + kb * row_stride;
-#pragma unroll
-      for (int l = 0; l < KPT; ++l) vr[l] = *reinterpret_cast<const uint4*>(src + l * row_stride);
-    } else {
-#pragma unroll
-      for (int l = 0; l < KPT; ++l) {
-        int pos = kb + KPT * vj + l;
-        pos = pos < lk ? pos : lk - 1;
-        vr[l] = *reinterpret_cast<const uint4*>(vbase + pos * row_stride + 8 * vc);
-      }
-    }
+  auto issue_kv = [&](char* buf, int kb) {
+    issue_rows(kbase, koff, buf, kb);
+    issue_rows(vbase, voff, buf + L::K_BYTES, kb);
   };
-  auto store_vt = [&](char* buf) {
-    if (!vtask) return;
-    uint16_t* vt = reinterpret_cast<uint16_t*>(buf + L::K_BYTES);
-    const uint32_t w0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
-    const uint32_t w1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      // dim 8c + 2w: the low halves of the keys; dim 8c + 2w + 1: the high halves
-      uint16_t* lo_row = vt + (8 * vc + 2 * w) * kFaVPitch + KPT * vj;
-      uint16_t* hi_row = vt + (8 * vc + 2 * w + 1) * kFaVPitch + KPT * vj;
-      if constexpr (KPT == 2) {
-        *reinterpret_cast<uint32_t*>(lo_row) = __builtin_amdgcn_perm(w1[w], w0[w], 0x05040100u);
-        *reinterpret_cast<uint32_t*>(hi_row) = __builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u);
-      } else {
-        const uint32_t w2 = (&vr[2].x)[w], w3 = (&vr[KPT - 1].x)[w];
-        uint2 lo, hi;
-        lo.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x05040100u);
-        lo.y = __builtin_amdgcn_perm(w3, w2, 0x05040100u);
-        hi.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u);
-        hi.y = __builtin_amdgcn_perm(w3, w2, 0x07060302u);
-        *reinterpret_cast<uint2*>(lo_row) = lo;
-        *reinterpret_cast<uint2*>(hi_row) = hi;
-      }
-    }
-  };
+  // PV operand reads: lane s of a 16-lane group addresses V row keybase + s / 4,
+  // dims 16j + 4 (s % 4) .. + 3 (swizzled 16-byte column), so that lane n of
+  // the group receives V[keybase + k][16j + n], k = 0..3
+  const int tr_row = lane % 16 / 4;
+  const int tr_chunk = (lane % 4) / 2;  // + 2j
+  const int tr_half = 8 * (lane % 2);   // byte offset inside the 16-byte column
 
   float m_run[NG];
 #pragma unroll
@@ -443,10 +404,8 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   const u8v ones = u8v{one, one, one, one, one, one, one, one};
 
   // prologue: block 0
-  issue_k(lds, 0);
-  load_v(0);
-  wait_vmcnt<0>();  // K landed in LDS, V in registers
-  store_vt(lds);
+  issue_kv(lds, 0);
+  wait_vmcnt<0>();  // K and V landed in LDS
   __syncthreads();
 
   // One block step: staging of block i + 1 into `nxt` and compute of block i
@@ -457,14 +416,11 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   auto step = [&](const char* __restrict__ cur, char* __restrict__ nxt, int i) {
     const int kb = i * kFaBlock;
     const bool more = i + 1 < nblk;
-    if (more) {
-      issue_k(nxt, kb + kFaBlock);
-      load_v(kb + kFaBlock);
-    }
+    if (more) issue_kv(nxt, kb + kFaBlock);
     // waves whose rows all precede this block under the causal mask skip it
     if (wrow0 <= wave_last && !(causal && kb > wave_last_pos)) {
       const uint16_t* sk = reinterpret_cast<const uint16_t*>(cur);
-      const uint16_t* svt = reinterpret_cast<const uint16_t*>(cur + L::K_BYTES);
+      const char* sv_base = cur + L::K_BYTES;
       // ---- S^T = K * Q^T ----
       f4 sacc[4][NG];
 #pragma unroll
@@ -551,10 +507,19 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
         u8v a[DB];  // every dim block's V^T operand of this k-step, then the MFMAs
 #pragma unroll
         for (int j = 0; j < DB; ++j) {
-          const uint16_t* row = svt + (16 * j + n) * kFaVPitch + 32 * ks + 4 * kg;
-          const uint2 lo = *reinterpret_cast<const uint2*>(row);
-          const uint2 hi = *reinterpret_cast<const uint2*>(row + 16);
-          a[j] = __builtin_bit_cast(u8v, make_uint4(lo.x, lo.y, hi.x, hi.y));
+          v4s part[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            // keys 32 ks + 16 hh + 4 kg + k, k = 0..3
+            const int r = 32 * ks + 16 * hh + 4 * kg + tr_row;
+            const int pos = (2 * j + tr_chunk) ^ (2 * (r % 4));
+            part[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_v4s_ptr)(sv_base + r * (2 * D) + 16 * pos + tr_half));
+          }
+          a[j] = u8v{static_cast<uint16_t>(part[0][0]), static_cast<uint16_t>(part[0][1]),
+                     static_cast<uint16_t>(part[0][2]), static_cast<uint16_t>(part[0][3]),
+                     static_cast<uint16_t>(part[1][0]), static_cast<uint16_t>(part[1][1]),
+                     static_cast<uint16_t>(part[1][2]), static_cast<uint16_t>(part[1][3])};
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
@@ -565,10 +530,7 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
         for (int g2 = 0; g2 < NG; ++g2) l_acc[g2] = mfma16(ones, pop[g2][ks], l_acc[g2], O{});
       }
     }
-    if (more) {
-      wait_vmcnt<0>();  // next K landed in LDS, next V in registers
-      store_vt(nxt);
-    }
+    if (more) wait_vmcnt<0>();  // next K and V landed in LDS
   };
   for (int i = 0; i < nblk; ++i) {
     step(lds + (i & 1) * L::BUF, lds + ((i + 1) & 1) * L::BUF, i);
