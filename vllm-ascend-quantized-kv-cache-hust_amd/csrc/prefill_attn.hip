@@ -316,7 +316,8 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   const int row0 = qb * (kFaRows * kFaWaves);
   if (row0 >= lq || lk <= 0) return;  // uniform over the workgroup
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  // wave-uniform; saying so keeps the DMA destinations in scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int n = lane & 15;
   const int kg = lane >> 4;
@@ -349,29 +350,34 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   const T* kbase = k + (static_cast<int64_t>(k_start) * kvh + kvhead) * D;
   const T* vbase = v + (static_cast<int64_t>(k_start) * kvh + kvhead) * D;
   const int64_t row_stride = static_cast<int64_t>(kvh) * D;
-  // per-lane element offsets of the K and V rows this lane moves (row r of
-  // the block, swizzled piece), relative to the block's first row
-  int64_t koff[KINST], voff[KINST];
+  // per-lane byte offsets of the K and V rows this lane moves (row r of the
+  // block, swizzled piece), relative to the block's first row: 32-bit, so
+  // that every DMA is a uniform base plus a lane offset
+  uint32_t koff[KINST], voff[KINST];
   int krow[KINST];
 #pragma unroll
   for (int i = 0; i < KINST; ++i) {
     const int inst = wave * KINST + i;
     const int r = inst * RPI + lane / PPR;  // block row of this lane
     krow[i] = r;
-    koff[i] = r * row_stride + 8 * ((lane % PPR) ^ (r % PPR));
-    voff[i] = r * row_stride + 8 * ((lane % PPR) ^ (2 * (r % 4)));
+    koff[i] = static_cast<uint32_t>((r * row_stride + 8 * ((lane % PPR) ^ (r % PPR))) * 2);
+    voff[i] = static_cast<uint32_t>((r * row_stride + 8 * ((lane % PPR) ^ (2 * (r % 4)))) * 2);
   }
   // DMA of block rows kb .. kb + 63 of `base` into `dst` with the lane
-  // offsets `off`; rows past the end read the last row (masked later)
-  auto issue_rows = [&](const T* base, const int64_t (&off)[KINST], char* dst, int kb) {
-    const bool whole = kb + kFaBlock <= lk;  // uniform: only the last block clamps
+  // offsets `off`; in the last block rows past the end read the last row
+  // (masked later)
+  auto issue_rows = [&](const T* base, const uint32_t (&off)[KINST], char* dst, int kb) {
+    const char* gb = reinterpret_cast<const char*>(base + static_cast<int64_t>(kb) * row_stride);
+    if (kb + kFaBlock <= lk) {  // uniform: only the last block clamps
 #pragma unroll
-    for (int i = 0; i < KINST; ++i) {
-      const int inst = wave * KINST + i;
-      const T* src = base + kb * row_stride + off[i];
-      if (!whole && kb + krow[i] >= lk)
-        src = base + static_cast<int64_t>(lk - 1) * row_stride + (off[i] - krow[i] * row_stride);
-      dma16(src, dst + 1024 * inst);
+      for (int i = 0; i < KINST; ++i) dma16(gb + off[i], dst + 1024 * (wave * KINST + i));
+    } else {
+#pragma unroll
+      for (int i = 0; i < KINST; ++i) {
+        const int back = kb + krow[i] >= lk ? kb + krow[i] - (lk - 1) : 0;  // rows to step back
+        dma16(gb + off[i] - static_cast<int64_t>(back) * row_stride * 2,
+              dst + 1024 * (wave * KINST + i));
+      }
     }
   };
   auto issue_kv = [&](char* buf, int kb) {
