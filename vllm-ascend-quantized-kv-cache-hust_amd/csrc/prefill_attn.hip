@@ -267,6 +267,7 @@ prefill_attn_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
 // its column.
 
 constexpr int kFaGroupRows = 128;  // query rows per workgroup
+constexpr int kFaXcds = 8;         // XCDs workgroup ids are dealt over
 constexpr int kFaBlock = 64;  // keys per block
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s* lds_v4s_ptr;
@@ -290,7 +291,7 @@ __attribute__((amdgpu_waves_per_eu(4 / NG, 4 / NG)))
 prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
                        const T* __restrict__ v, const int32_t* __restrict__ cu_q,
                        const int32_t* __restrict__ cu_k, int hq, int kvh, float qscale,
-                       int causal, int qblocks, T* __restrict__ out) {
+                       int causal, int qblocks, int batch, T* __restrict__ out) {
   using O = typename Op<T>::type;
   using L = FaLds<D>;
   constexpr int kFaWaves = 8 / NG;
@@ -304,11 +305,22 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   static_assert(PPR >= 8, "V swizzle 2 * (r % 4) stays inside the row");
   extern __shared__ __align__(16) char lds[];
 
-  // heavy query blocks first: block x = qblocks - 1 - blockIdx.x
-  const int qb = qblocks - 1 - static_cast<int>(blockIdx.x);
-  const int head = blockIdx.y;
-  const int b = blockIdx.z;
-  const int kvhead = head / (hq / kvh);
+  // Workgroup ids go to the XCDs round-robin.  The rep * qblocks workgroups
+  // that stream one (request, kv head)'s K/V run on one XCD, one such pair
+  // after another, so that XCD's L2 keeps the pair's blocks between them;
+  // inside a pair the heavy query blocks (more keys under the causal mask)
+  // come first, the pair's query heads interleaved.
+  const int rep = hq / kvh;
+  const int per_pair = rep * qblocks;
+  const int xcd = static_cast<int>(blockIdx.x) % kFaXcds;
+  const int xj = static_cast<int>(blockIdx.x) / kFaXcds;
+  const int pair = xcd + kFaXcds * (xj / per_pair);
+  if (pair >= batch * kvh) return;  // padding of the last round
+  const int w = xj % per_pair;
+  const int b = pair / kvh;
+  const int kvhead = pair - b * kvh;
+  const int head = kvhead * rep + w % rep;
+  const int qb = qblocks - 1 - w / rep;
   const int q_start = cu_q[b];
   const int lq = cu_q[b + 1] - q_start;
   const int k_start = cu_k[b];
@@ -582,14 +594,16 @@ extern "C" int kvq_prefill_attn(const void* query, const void* key, const void* 
   if ((dtype == KVQ_DTYPE_BF16 || dtype == KVQ_DTYPE_F16) &&
       (head_size == 64 || head_size == 128) && fa_lds <= lds_max) {
     const int64_t fab = (max_q_len + kFaGroupRows - 1) / kFaGroupRows;
-    if (fab > 0x7fffffff) return KVQ_ERR_INVALID;
-    const dim3 fgrid(static_cast<unsigned>(fab), num_heads, static_cast<unsigned>(batch));
+    const int64_t pairs = batch * num_kv_heads;
+    const int64_t wgs = (pairs + kFaXcds - 1) / kFaXcds * kFaXcds * (num_heads / num_kv_heads) * fab;
+    if (wgs > 0x7fffffff) return KVQ_ERR_INVALID;
+    const dim3 fgrid(static_cast<unsigned>(wgs));
 #define KVQ_PREFILL_FA(TT, DD)                                                              \
     hipLaunchKernelGGL((prefill_attn_fa_kernel<TT, DD, kFaNG>), fgrid, dim3(64 * (8 / kFaNG)), \
                        FaLds<DD>::BYTES, s, static_cast<const TT*>(query),                 \
                        static_cast<const TT*>(key), static_cast<const TT*>(value),         \
                        cu_seqlens_q, cu_seqlens_k, num_heads, num_kv_heads, qscale, causal, \
-                       static_cast<int>(fab), static_cast<TT*>(out))
+                       static_cast<int>(fab), static_cast<int>(batch), static_cast<TT*>(out))
     if (dtype == KVQ_DTYPE_BF16) {
       if (head_size == 64) KVQ_PREFILL_FA(kvq::bf16, 64);
       else KVQ_PREFILL_FA(kvq::bf16, 128);
