@@ -3,8 +3,10 @@
 
 The device quantizes with d = x - mn, k = floor(d * rcp(scale)) and code
 k + [y >= 0], y = fma(scale * 2^-24, 2^e(t), fma(-scale, t, d)), where
-t = k + pred(0.5) and 2^e(t) is t with its mantissa cleared
-(kivi_pack_word in csrc/kvq_common.h).  This test replays that rule in fp32
+t = k + pred(0.5) and 2^e(t) is t with its mantissa cleared; it takes the
+code as t + 0.25 (y >= 0) or t - 0.25 rounded to nearest even, with the sign
+moved from y (kivi_pack_word in csrc/kvq_common.h).  This test replays that
+rule in fp32
 with both fmas emulated exactly (one rounding each) and the reciprocal off by
 up to one ulp either way (v_rcp_f32's bound), and requires codes identical to
 the exact rule of the reference (pkg/ops/triton/kivi_pack.py:98-104, 195-204)
@@ -54,8 +56,12 @@ def _rule(x, mn, sc, rcp, t_of=None, half_ulp=True):
     e = (t.view(np.uint32) & np.uint32(0x7F800000)).view(F)
     s24 = (sc * F(2.0**-24)).astype(F)
     inner = _fma32(-sc, t, d)
-    y = (s24.astype(np.float64) * e + inner) if half_ulp else inner.astype(np.float64)
-    r = np.where(y >= 0, k + 1, k).astype(F)
+    y = _fma32(s24, e, inner) if half_ulp else inner
+    # the sign of y picks +-0.25; a -0 would pick the wrong side, and cannot occur
+    assert not (np.signbit(y) & (y == 0)).any()
+    step = np.where(np.signbit(y), F(-0.25), F(0.25)).astype(F)
+    r = np.rint((t + step).astype(F)).astype(F)  # v_cvt_pk_u8_f32: nearest even
+    assert (r == np.where(y >= 0, k + 1, k)).all()
     assert (r >= 0).all() and (r <= 15).all()  # codes with no clamp
     return r
 

@@ -19,7 +19,14 @@
 //   group's G/8 adjacent lanes (DPP quad permutes and ds_swizzle).  Head sizes
 //   whose rows do not tile a wave keep the one-thread-per-word kernel.
 //
-// Both quantize with kivi_pack_word: a reciprocal per group, a floor per
+// One-launch store (kvq_kivi_store, the mixin's store batches: both packs and
+// the ring-row writes of a step or a chunk)
+//   kivi_pack_lds_kernel: 8 KB units staged by LDS DMA, each lane holding one
+//   quantization group's 64 values after the read-back, two units in flight
+//   per wave (layout notes at the kernel).  Packing a prefill chunk's keys and
+//   values this way takes one launch.
+//
+// All quantize with kivi_pack_word: a reciprocal per group, a floor per
 // element, and two fmas that decide exactly, with no division and no branch,
 // whether the reference's rounded quotient reaches the next code.
 #include <mutex>
@@ -479,88 +486,428 @@ kivi_pack_value_wave_kernel(const T* __restrict__ src_a, int64_t n_a, const T* _
   }
 }
 
-// ---- one-launch store -------------------------------------------------------
-// A store batch (key pack groups, value pack rows, ring-row writes of both
-// sides) whose ring writes overwrite no row that the same batch packs has no
-// order inside it, so it runs as one grid of 4-wave workgroups split into
-// [key pack | value pack | ring rows].  Pack sources index [ring rows ; input
-// rows]; ring writes copy input rows to ring rows (same dtype, 16 bytes per
-// thread).  jobs (int64): key pack src | key pack slot | value pack src |
-// value pack slot | key ring src | key ring dst | value ring src | value ring
-// dst.  The ring is read (pack sources) and written (ring rows) by the same
-// grid, so its pointers are not restrict-qualified.
-//
-// PLANNED: the grid and the job sections are sized by capacities (c0..c3) and
-// the actual counts are read from the device (jobs[0..3], sections from
-// jobs + 4 at capacity offsets), so one captured launch serves every step;
-// waves past a count exit at once.
-template <typename T, int G, bool PLANNED>
-__global__ void __launch_bounds__(256)
-kivi_store_kernel(T* ring_k, T* ring_v, int64_t n_ring, const T* __restrict__ in_k,
-                  const T* __restrict__ in_v, const int64_t* __restrict__ jobs, int64_t c0,
-                  int64_t c1, int64_t c2, int64_t c3, int64_t kblocks, int64_t vblocks,
-                  FastDiv kvh_div, int bs, int32_t* __restrict__ kq, float* __restrict__ ks,
-                  float* __restrict__ km, int32_t* __restrict__ vq, float* __restrict__ vs,
-                  float* __restrict__ vm) {
-  constexpr int D = 128;
-  constexpr int WPR = D / 8;
-  const int kvh = static_cast<int>(kvh_div.d);
-  const int64_t row_elems = static_cast<int64_t>(kvh) * D;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  // counts and the eight job sections
-  int64_t nkp = c0, nvp = c1, nkr = c2, nvr = c3;
-  const int64_t* kp_src = jobs;
-  if constexpr (PLANNED) {
-    nkp = min(jobs[0], c0);
-    nvp = min(jobs[1], c1);
-    nkr = min(jobs[2], c2);
-    nvr = min(jobs[3], c3);
-    kp_src = jobs + 4;
+// ---- LDS-staged pack (head size 128, G in {64, 128}, 16-bit input) ---------
+// The work is cut into units of 8 KB of source rows.  A key unit is one token
+// group of one head and part of its dims: G = 128 -> 128 tokens x 32 dims (a
+// quarter of the head), G = 64 -> 64 tokens x 64 dims (a half).  A value unit
+// is 32 (token, head) rows.  Each wave takes up to four units and walks them
+// with two wave-private LDS stages: a unit's rows arrive by LDS DMA (16 bytes
+// a lane, the 16-byte chunks of a row XOR-swizzled), are copied to registers,
+// and the stage is refilled with the unit after next while the copy is
+// quantized and stored, so two units stay in flight.  Read back, every lane
+// holds 64 values of one quantization group:
+//   key unit: 64 tokens of one dim, gathered with ds_read_b64_tr_b16.  Lane
+//     l of each 16-lane group receives element l % 4 of the 8-byte runs that
+//     lanes l / 4 + 4k address (k = 0..3, in that order): lane a pointing at
+//     token T + a / 4, dims 4m..4m+3 hands lane 4q + r tokens T..T+3 of dim
+//     4m + r;
+//   value unit: half a row (64 dims), by 16-byte LDS reads.
+// The group min/max is a lane-local scan plus at most one exchange with the
+// lane holding the group's other half (G = 128), and every lane writes its 8
+// packed words as one 32-byte run; scales and minima go out as consecutive
+// 4-byte lanes.  The swizzles keep the transposing reads and the row reads
+// free of bank conflicts within each half wave.  Each unit's source rows and
+// page slots are read once, up front, into a small LDS table, so the loop
+// itself issues no vector loads but the DMAs.  The loop is not unrolled and
+// keys and values share one quantize body: the kernel stays well inside the
+// instruction cache.
+namespace lp {
+
+constexpr int kUnit = 8192;  // source bytes per unit
+constexpr int kWaves = 4;    // waves per workgroup
+constexpr int kUnitsPerWave = 4;
+constexpr int kStages = 2;   // LDS stages per wave (units in flight)
+constexpr int kMeta = 512;   // per unit: 128 int32 source rows (keys) or 32 (values)
+constexpr int kLds = kStages * kUnit * kWaves + kMeta * kUnitsPerWave * kWaves;
+constexpr int kD = 128;
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s* lds_v4s_ptr;
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
+// LDS DMA of 16 bytes a lane into stage + 16 * lane, written as inline asm so
+// that the compiler's wait-count pass does not track it: with stores in
+// flight that pass can only wait for every outstanding access (vmcnt(0)),
+// where the loop below waits for exactly the DMA it needs.  The stage
+// address goes to M0 through an operand constraint; the nop keeps the M0
+// write and the DMA apart.
+__device__ __forceinline__ void dma16_counted(const void* g, const char* stage) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(stage))));
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(m0) : "memory");
+}
+
+// s_waitcnt lgkmcnt(0), vmcnt and expcnt left alone.
+__device__ __forceinline__ void wait_lgkm0() {
+  __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (3 << 14));
+  asm volatile("" ::: "memory");
+}
+
+// One side of a pack: token t reads row index[t] (or t) of a, rows past n_a
+// continuing into b, and goes to page slot slots[t] (negative: not stored).
+// Source row numbers stay below 2^31.
+template <typename T, typename I>
+struct Side {
+  const T* a;
+  int64_t n_a;
+  const T* b;
+  const int64_t* index;
+  const I* slots;
+  int64_t count;  // tokens
+};
+
+template <typename T, typename I>
+struct Ctx {
+  Side<T, I> k, v;
+  int kvh, bs;
+  FastDiv kdiv;  // division by kvh
+  int32_t* kq;
+  float* ks;
+  float* km;
+  int32_t* vq;
+  float* vs;
+  float* vm;
+};
+
+template <typename T>
+__device__ __forceinline__ void unpack2(uint32_t w, float& lo, float& hi);
+template <>
+__device__ __forceinline__ void unpack2<bf16>(uint32_t w, float& lo, float& hi) {
+  lo = __uint_as_float(w << 16);
+  hi = __uint_as_float(w & 0xffff0000u);
+}
+template <>
+__device__ __forceinline__ void unpack2<f16>(uint32_t w, float& lo, float& hi) {
+  lo = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w)));
+  hi = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+}
+
+// 64 values (32 words of two) -> group min, scale and 8 packed words of 8
+// consecutive values each.  The min/max is exchanged first with the lane
+// holding the group's other half: XOR 1 with the next lane (a value row at
+// G = 128), XOR 8 within the 16-lane row (a key dim at G = 128), or none.
+template <typename T>
+__device__ __forceinline__ void quantize64(const uint32_t (&e)[32], int partner,
+                                           uint32_t (&word)[8], float& mn_out, float& sc_out) {
+  float mn, mx;
+  {
+    float a, b;
+    unpack2<T>(e[0], a, b);
+    mn = fmin_ordered(a, b);
+    mx = fmax_ordered(a, b);
   }
-  const int64_t* kp_slot = kp_src + c0;
-  const int64_t* vp_src = kp_slot + c0;
-  const int64_t* vp_slot = vp_src + c1;
-  const int64_t* kr_src = vp_slot + c1;
-  const int64_t* kr_dst = kr_src + c2;
-  const int64_t* vr_src = kr_dst + c2;
-  const int64_t* vr_dst = vr_src + c3;
-  int64_t b = blockIdx.x;
-  if (b < kblocks) {
-    const int64_t u = b * 4 + wave;
-    if (u < nkp / G * kvh * 2)
-      key_pack_wave<T, int64_t, G>(ring_k, n_ring, in_k, kp_src, kp_slot, u, lane, kvh, bs, kq,
-                                   ks, km);
-    return;
+#pragma unroll
+  for (int i = 1; i < 32; ++i) {
+    float a, b;
+    unpack2<T>(e[i], a, b);
+    mn = fmin_ordered(fmin_ordered(mn, a), b);
+    mx = fmax_ordered(fmax_ordered(mx, a), b);
   }
-  b -= kblocks;
-  if (b < vblocks) {
-    const int64_t* vsrc = vp_src;
-    const int64_t* vslot = vp_slot;
-    const int64_t rows = nvp * kvh;  // the host keeps this below 2^31
-    // a wave whose first row is past the end has nothing to store (uniform)
-    if ((b * 4 + wave) * (64 / WPR) >= rows) return;
-    const int64_t r = (b * 4 + wave) * (64 / WPR) + lane / WPR;
-    const int64_t rc = r < rows ? r : rows - 1;  // past the end: read the last row, store nothing
-    const uint32_t t = kvh_div.div(static_cast<uint32_t>(rc));
-    const int h = static_cast<int>(rc) - static_cast<int>(t) * kvh;
-    const int w = lane % WPR;
+  if (partner == 1) {
+    mn = fmin_ordered(mn, lane_xor<1>(mn));
+    mx = fmax_ordered(mx, lane_xor<1>(mx));
+  } else if (partner == 8) {
+    // rotating a 16-lane row by 8 swaps its halves: lane ^ 8
+    mn = fmin_ordered(mn, __int_as_float(__builtin_amdgcn_update_dpp(
+                              0, __float_as_int(mn), 0x128, 0xF, 0xF, false)));
+    mx = fmax_ordered(mx, __int_as_float(__builtin_amdgcn_update_dpp(
+                              0, __float_as_int(mx), 0x128, 0xF, 0xF, false)));
+  }
+  const float sc = kivi_group_scale(mn, mx);
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
     float x[8];
-    load8(src_row<T>(ring_v, n_ring, in_v, vsrc[t], row_elems) + h * D + w * 8, x);
-    value_pack_word<WPR>(x, w, r < rows, vslot[t], h, kvh, G / 8, D / G, vq, vs, vm);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) unpack2<T>(e[4 * w + i], x[2 * i], x[2 * i + 1]);
+    word[w] = kivi_pack_word(x, mn, sc);
+  }
+  mn_out = mn;
+  sc_out = sc;
+}
+
+// Unit u's source-row table, for a side read through an index.  Key: the
+// rows of its G tokens (int32).  Value: for each of its 32 (token, head) rows
+// the source head row row * kvh + h (int32; the last row for rows past the
+// end).  A side without an index needs no table.
+template <typename T, typename I, int G>
+__device__ __forceinline__ void load_table(const Ctx<T, I>& c, int64_t nk, int64_t u, char* meta,
+                                           int lane) {
+  int32_t* rows = reinterpret_cast<int32_t*>(meta);
+  if (u < nk) {
+    if (!c.k.index) return;
+    constexpr int P = G == 128 ? 4 : 2;
+    const int64_t t0 = u / P / c.kvh * G;
+#pragma unroll
+    for (int i = 0; i < G / 64; ++i) rows[64 * i + lane] = static_cast<int32_t>(c.k.index[t0 + 64 * i + lane]);
+  } else if (c.v.index && lane < 32) {
+    const int64_t nrows = c.v.count * c.kvh;
+    const int64_t r = (u - nk) * 32 + lane;
+    const int64_t rc = r < nrows ? r : nrows - 1;
+    const uint32_t t = c.kdiv.div(static_cast<uint32_t>(rc));
+    const int h = static_cast<int>(rc) - static_cast<int>(t) * c.kvh;
+    rows[lane] = static_cast<int32_t>(c.v.index[t] * c.kvh + h);
+  }
+}
+
+// Page slot of token t, read through the scalar cache (t is uniform), so the
+// load is counted apart from the DMAs.
+template <typename I>
+__device__ __forceinline__ int64_t slot_of(const I* slots, int64_t t) {
+  typedef const __attribute__((address_space(4))) I* const_ptr;
+  return static_cast<int64_t>(((const_ptr)(reinterpret_cast<uintptr_t>(slots)))[t]);
+}
+
+// Unit u's 8 DMAs into stage.  Every unit issues exactly 8 (a key group with
+// no slot is loaded too, then not stored): the loop's counted waits rely on it.
+// A source address is base + row * row_bytes, the base chosen by whether the
+// row lies in a or in b and holding the lane's column.
+template <typename T, typename I, int G>
+__device__ __forceinline__ void issue(const Ctx<T, I>& c, int64_t nk, int64_t u, const char* meta,
+                                      const char* stage, int lane) {
+  const int32_t* rows = reinterpret_cast<const int32_t*>(meta);
+  uint64_t addr[8];
+  if (u < nk) {
+    constexpr int P = G == 128 ? 4 : 2;
+    const int part = static_cast<int>(u % P);
+    const int h = static_cast<int>((u / P) % c.kvh);
+    const uint32_t rb = static_cast<uint32_t>(c.kvh * kD * sizeof(T));
+    const uint64_t a0 = reinterpret_cast<uintptr_t>(c.k.a);
+    const uint64_t b0 = reinterpret_cast<uintptr_t>(c.k.b) - static_cast<uint64_t>(c.k.n_a) * rb;
+    // the lane's column: G = 128 -> 16-byte chunk (lane % 4) ^ 2 (d >= 4)
+    // of the quarter; G = 64 -> chunk (lane % 8) ^ (4 ((lane / 8) >> 1 & 1))
+    int col0, col1;
+    if constexpr (G == 128) {
+      col0 = part * 32 + 8 * (lane % 4);
+      col1 = part * 32 + 8 * ((lane % 4) ^ 2);
+    } else {
+      col0 = col1 = part * 64 + 8 * ((lane % 8) ^ (4 * (((lane / 8) >> 1) & 1)));
+    }
+    const uint32_t off0 = static_cast<uint32_t>((h * kD + col0) * sizeof(T));
+    const uint32_t off1 = static_cast<uint32_t>((h * kD + col1) * sizeof(T));
+    const int64_t t0 = u / P / c.kvh * G;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const int tok = G == 128 ? 16 * d + lane / 4 : 8 * d + lane / 8;
+      const int32_t row = c.k.index ? rows[tok] : static_cast<int32_t>(t0 + tok);
+      const uint64_t base = (row < c.k.n_a ? a0 : b0) + (G == 128 && d >= 4 ? off1 : off0);
+      addr[d] = base + static_cast<uint64_t>(static_cast<uint32_t>(row)) * rb;
+    }
+  } else {
+    // DMA d: row 4d + lane / 16 of the unit, 16-byte chunk
+    // (lane % 16) ^ (row % 8) = (lane % 16) ^ (lane / 16 + 4 (d % 2))
+    const uint32_t hb = static_cast<uint32_t>(kD * sizeof(T));
+    const int64_t split = c.v.n_a * c.kvh;
+    const uint64_t a0 = reinterpret_cast<uintptr_t>(c.v.a);
+    const uint64_t b0 = reinterpret_cast<uintptr_t>(c.v.b) - static_cast<uint64_t>(split) * hb;
+    const uint32_t off0 = 16u * static_cast<uint32_t>((lane % 16) ^ (lane / 16));
+    const uint32_t off1 = 16u * static_cast<uint32_t>((lane % 16) ^ (lane / 16 + 4));
+    const int64_t nrows = c.v.count * c.kvh;
+    const int64_t r0 = (u - nk) * 32;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const int64_t r = r0 + 4 * d + lane / 16;
+      const int32_t f = c.v.index ? rows[4 * d + lane / 16]
+                                  : static_cast<int32_t>(r < nrows ? r : nrows - 1);
+      const uint64_t base = (f < split ? a0 : b0) + (d % 2 ? off1 : off0);
+      addr[d] = base + static_cast<uint64_t>(static_cast<uint32_t>(f)) * hb;
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < 8; ++d)
+    dma16_counted(reinterpret_cast<const void*>(addr[d]), stage + d * 1024);
+}
+
+// Read a landed stage into registers: 64 values of one group per lane, in
+// order (see the layout notes above).
+template <int G>
+__device__ __forceinline__ void read_stage(bool key, const char* stage, int lane,
+                                           uint32_t (&e)[32]) {
+  if (key) {
+    const int a = lane % 16;
+    const int g = lane / 16;
+    int base, step;
+    if constexpr (G == 128) {
+      base = 64 * (64 * ((a % 4) >> 1) + a / 4) + 16 * (g ^ (2 * ((a % 4) >> 1))) +
+             8 * ((a % 4) & 1);
+      step = 256;
+    } else {
+      base = 128 * (a / 4) + 16 * ((2 * g + ((a % 4) >> 1)) ^ (4 * (((a / 4) >> 1) & 1))) +
+             8 * ((a % 4) & 1);
+      step = 512;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const u2v r = __builtin_bit_cast(
+          u2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_ptr)(stage + base + step * i)));
+      e[2 * i] = r.x;
+      e[2 * i + 1] = r.y;
+    }
+  } else {
+    const int rho = lane / 2;
+    const int hh = lane % 2;
+    const int s = rho % 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const u4v q = *reinterpret_cast<const u4v*>(stage + rho * 256 + 16 * (8 * hh + (j ^ s)));
+      e[4 * j] = q.x;
+      e[4 * j + 1] = q.y;
+      e[4 * j + 2] = q.z;
+      e[4 * j + 3] = q.w;
+    }
+  }
+}
+
+// Quantize unit u (held in registers) and store its words, scales and minima.
+template <typename T, typename I, int G>
+__device__ __forceinline__ void finish(const Ctx<T, I>& c, int64_t nk, int64_t u, const char* meta,
+                                       const uint32_t (&e)[32], int lane) {
+  const bool key = u < nk;
+  const int a = lane % 16;
+  int64_t slot;
+  int64_t orow = 0;
+  if (key) {
+    constexpr int P = G == 128 ? 4 : 2;
+    slot = slot_of(c.k.slots, u / P / c.kvh * G);
+    if (slot < 0) return;  // uniform: the group is not stored
+  } else {
+    // the unit's rows span tokens tf..tl: their slots come through the
+    // scalar cache and each lane picks its own
+    const int64_t nrows = c.v.count * c.kvh;
+    const int64_t r0 = (u - nk) * 32;
+    const int64_t r = r0 + lane / 2;
+    const int64_t rl = r0 + 31 < nrows ? r0 + 31 : nrows - 1;
+    const int64_t tf = c.kdiv.div(static_cast<uint32_t>(r0));
+    const int64_t tl = c.kdiv.div(static_cast<uint32_t>(rl));
+    const int64_t t = c.kdiv.div(static_cast<uint32_t>(r < nrows ? r : nrows - 1));
+    slot = -1;
+    for (int64_t tt = tf; tt <= tl; ++tt) {
+      const int64_t st = slot_of(c.v.slots, tt);
+      slot = t == tt ? st : slot;
+    }
+    if (r >= nrows) slot = -1;
+    orow = slot * c.kvh + (static_cast<int>(r < nrows ? r : nrows - 1) - static_cast<int>(t) * c.kvh);
+  }
+  uint32_t word[8];
+  float mn, sc;
+  quantize64<T>(e, G == 128 ? (key ? 8 : 1) : 0, word, mn, sc);
+  if (slot < 0) return;  // a value row past the end, or a token with no slot
+  const u4v lo{word[0], word[1], word[2], word[3]};
+  const u4v hi{word[4], word[5], word[6], word[7]};
+  if (key) {
+    constexpr int P = G == 128 ? 4 : 2;
+    const int part = static_cast<int>(u % P);
+    const int h = static_cast<int>((u / P) % c.kvh);
+    const int g = lane / 16;
+    const int dim = G == 128 ? part * 32 + 4 * (2 * g + ((a / 4) & 1)) + a % 4 : part * 64 + lane;
+    const int hh = G == 128 ? (a / 4) >> 1 : 0;  // token half of a G = 128 group
+    const int64_t blk = slot / c.bs;
+    const int off = static_cast<int>(slot - blk * c.bs);
+    const int64_t drow = (blk * c.kvh + h) * kD + dim;
+    if (hh == 0) {
+      const int64_t sidx = drow * (c.bs / G) + off / G;
+      c.ks[sidx] = sc;
+      c.km[sidx] = mn;
+    }
+    u4v* dst = reinterpret_cast<u4v*>(c.kq + drow * (c.bs / 8) + off / 8 + 8 * hh);
+    __builtin_nontemporal_store(lo, dst);
+    __builtin_nontemporal_store(hi, dst + 1);
+  } else {
+    const int hh = lane % 2;
+    if (G == 64 || hh == 0) {
+      const int64_t sidx = orow * (kD / G) + (G == 64 ? hh : 0);
+      c.vs[sidx] = sc;
+      c.vm[sidx] = mn;
+    }
+    u4v* dst = reinterpret_cast<u4v*>(c.vq + orow * (kD / 8) + 8 * hh);
+    __builtin_nontemporal_store(lo, dst);
+    __builtin_nontemporal_store(hi, dst + 1);
+  }
+}
+
+}  // namespace lp
+
+// One-launch store.  A store batch (key pack groups, value pack rows,
+// ring-row writes of both sides) whose ring writes overwrite no row that the
+// same batch packs has no order inside it, so it runs as one grid:
+// workgroups [0, pack_blocks) take the key units then the value units (unit
+// w + k * (pack_blocks * 4) for wave w, k < 4), the blocks after them copy
+// ring rows (16 bytes a thread, same dtype).  Pack sources index [ring rows ;
+// input rows].  The ring is read (pack sources) and written (ring rows) by
+// the same grid, so its pointers are not restrict-qualified.  PLANNED reads
+// the pack and ring counts from counts[0..3] (capped by the side counts given,
+// which are then capacities), so one captured launch serves every step;
+// waves past a count exit at once.
+template <typename T, typename I, int G, bool PLANNED>
+__global__ void __launch_bounds__(256)
+kivi_pack_lds_kernel(lp::Ctx<T, I> c, int64_t pack_blocks, const int64_t* __restrict__ counts,
+                     T* ring_k, T* ring_v, const T* __restrict__ in_k,
+                     const T* __restrict__ in_v, const int64_t* __restrict__ kr_src,
+                     const int64_t* __restrict__ kr_dst, const int64_t* __restrict__ vr_src,
+                     const int64_t* __restrict__ vr_dst, int64_t nkr, int64_t nvr) {
+  __shared__ __attribute__((aligned(16))) char lds[lp::kLds];
+  if constexpr (PLANNED) {
+    c.k.count = min(counts[0], c.k.count);
+    c.v.count = min(counts[1], c.v.count);
+    nkr = min(counts[2], nkr);
+    nvr = min(counts[3], nvr);
+  }
+  if (blockIdx.x >= pack_blocks) {
+    // ring rows: 16 bytes a thread, same dtype
+    const int per_row = c.kvh * (lp::kD / 8);
+    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) - pack_blocks) * 256 + threadIdx.x;
+    const int64_t i = i0 / per_row;
+    if (i >= nkr + nvr) return;
+    const int64_t e = (i0 - i * per_row) * 8;
+    const int64_t row_elems = static_cast<int64_t>(c.kvh) * lp::kD;
+    const bool key = i < nkr;
+    const int64_t j = key ? i : i - nkr;
+    const T* src = (key ? in_k : in_v) + (key ? kr_src : vr_src)[j] * row_elems + e;
+    T* dst = (key ? ring_k : ring_v) + (key ? kr_dst : vr_dst)[j] * row_elems + e;
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
     return;
   }
-  b -= vblocks;
-  const int per_row = kvh * (D / 8);
-  const int64_t c = b * 256 + threadIdx.x;
-  const int64_t i = c / per_row;
-  if (i >= nkr + nvr) return;
-  const int64_t e = (c - i * per_row) * 8;
-  const bool key = i < nkr;
-  const int64_t j = key ? i : i - nkr;
-  const T* src = (key ? in_k : in_v) + (key ? kr_src : vr_src)[j] * row_elems + e;
-  T* dst = (key ? ring_k : ring_v) + (key ? kr_dst : vr_dst)[j] * row_elems + e;
-  *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+  constexpr int P = G == 128 ? 4 : 2;
+  const int64_t nk = c.k.count / G * c.kvh * P;
+  const int64_t nu = nk + (c.v.count * c.kvh + 31) / 32;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t nw = pack_blocks * lp::kWaves;
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * lp::kWaves + wave;
+  int n = 0;
+#pragma unroll
+  for (int k = 0; k < lp::kUnitsPerWave; ++k) n += w + k * nw < nu ? 1 : 0;
+  if (n == 0) return;
+  constexpr int S = lp::kStages;
+  char* stage = lds + wave * S * lp::kUnit;
+  char* meta = lds + lp::kWaves * S * lp::kUnit + wave * lp::kUnitsPerWave * lp::kMeta;
+  if (c.k.index || c.v.index) {
+    for (int k = 0; k < n; ++k)
+      lp::load_table<T, I, G>(c, nk, w + k * nw, meta + k * lp::kMeta, lane);
+    wait_vmcnt<0>();  // the tables are written before any DMA goes out
+    lp::wait_lgkm0();
+  }
+#pragma unroll
+  for (int k = 0; k < S; ++k)
+    if (k < n) lp::issue<T, I, G>(c, nk, w + k * nw, meta + k * lp::kMeta, stage + k * lp::kUnit, lane);
+  // Step k: unit k's rows were DMA'd into stage k % S S steps ago, unit
+  // k + 1's (two stages) one step ago.  Loads complete in issue order, so with
+  // at most 8 vector-memory operations outstanding -- the 8 DMAs of unit
+  // k + 1 -- unit k has landed, whatever the stores in between do.
+#pragma clang loop unroll(disable)
+  for (int k = 0; k < n; ++k) {
+    const int64_t u = w + k * nw;
+    char* cur = stage + (k % S) * lp::kUnit;
+    if (S == 2 && k + 1 < n)
+      wait_vmcnt<8>();
+    else
+      wait_vmcnt<0>();
+    uint32_t e[32];
+    lp::read_stage<G>(u < nk, cur, lane, e);
+    lp::wait_lgkm0();  // the stage is read before the next DMA overwrites it
+    if (k + S < n) lp::issue<T, I, G>(c, nk, u + S * nw, meta + (k + S) * lp::kMeta, cur, lane);
+    lp::finish<T, I, G>(c, nk, u, meta + k * lp::kMeta, e, lane);
+  }
 }
 
 // Workgroups of `kernel` that fit the device at once (CUs x occupancy),
@@ -581,6 +928,78 @@ int64_t resident_blocks(K* kernel, int threads) {
     cache[dev] = static_cast<int64_t>(cus) * (per > 0 ? per : 1);
   }
   return cache[dev];
+}
+
+// Launch kivi_pack_lds_kernel: pack workgroups of 4 waves taking 1 to 4
+// units each (as few as lets the resident waves hold all the work at once),
+// then the ring-row blocks.  Side counts are token counts (capacities when
+// counts != null).
+template <typename T, typename I, int G>
+int launch_pack_lds(const lp::Ctx<T, I>& c, const int64_t* counts, T* ring_k, T* ring_v,
+                    const T* in_k, const T* in_v, const int64_t* kr_src, const int64_t* kr_dst,
+                    const int64_t* vr_src, const int64_t* vr_dst, int64_t nkr, int64_t nvr,
+                    hipStream_t s) {
+  constexpr int P = G == 128 ? 4 : 2;
+  if (c.v.count * c.kvh >= 0x7fffffff) return KVQ_ERR_INVALID;
+  const int64_t units = c.k.count / G * c.kvh * P + (c.v.count * c.kvh + 31) / 32;
+  const bool planned = counts != nullptr;
+  auto* kern = planned ? kivi_pack_lds_kernel<T, I, G, true> : kivi_pack_lds_kernel<T, I, G, false>;
+  // units per wave: enough that the resident waves cover the work at once,
+  // at most kUnitsPerWave (the kernel takes u, u + nw, ... while below units)
+  const int64_t fit = resident_blocks(kern, 256);
+  if (fit <= 0) return KVQ_ERR_INVALID;
+  const int64_t resident_waves = fit * lp::kWaves;
+  int64_t upw = (units + resident_waves - 1) / resident_waves;
+  upw = upw < 1 ? 1 : (upw > lp::kUnitsPerWave ? lp::kUnitsPerWave : upw);
+  const int64_t per_block = lp::kWaves * upw;
+  const int64_t pack_blocks = (units + per_block - 1) / per_block;
+  const int64_t rchunks = (nkr + nvr) * c.kvh * (lp::kD / 8);
+  const int64_t blocks = pack_blocks + (rchunks + 255) / 256;
+  if (blocks == 0) return KVQ_OK;
+  if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, c, pack_blocks,
+                     counts, ring_k, ring_v, in_k, in_v, kr_src, kr_dst, vr_src, vr_dst, nkr, nvr);
+  KVQ_LAUNCH_CHECK();
+  return KVQ_OK;
+}
+
+// The store's job sections on the LDS-staged pack: c0..c3 are the section
+// sizes (capacities when counts != null).
+template <typename T>
+int launch_store_lds(const void* key_input, const void* value_input, void* ring_k, void* ring_v,
+                     int64_t ring_rows, int kvh, int g, int bs, const int64_t* sections,
+                     const int64_t* counts, int64_t c0, int64_t c1, int64_t c2, int64_t c3,
+                     int32_t* kq, float* ks, float* km, int32_t* vq, float* vs, float* vm,
+                     hipStream_t s) {
+  const int64_t* kp_src = sections;
+  const int64_t* kp_slot = kp_src + c0;
+  const int64_t* vp_src = kp_slot + c0;
+  const int64_t* vp_slot = vp_src + c1;
+  const int64_t* kr_src = vp_slot + c1;
+  const int64_t* kr_dst = kr_src + c2;
+  const int64_t* vr_src = kr_dst + c2;
+  const int64_t* vr_dst = vr_src + c3;
+  T* rk = static_cast<T*>(ring_k);
+  T* rv = static_cast<T*>(ring_v);
+  const T* ik = static_cast<const T*>(key_input);
+  const T* iv = static_cast<const T*>(value_input);
+  lp::Ctx<T, int64_t> c{};
+  c.k = lp::Side<T, int64_t>{rk, ring_rows, ik, kp_src, kp_slot, c0};
+  c.v = lp::Side<T, int64_t>{rv, ring_rows, iv, vp_src, vp_slot, c1};
+  c.kvh = kvh;
+  c.bs = bs;
+  c.kdiv = FastDiv::make(static_cast<uint32_t>(kvh));
+  c.kq = kq;
+  c.ks = ks;
+  c.km = km;
+  c.vq = vq;
+  c.vs = vs;
+  c.vm = vm;
+  if (g == 128)
+    return launch_pack_lds<T, int64_t, 128>(c, counts, rk, rv, ik, iv, kr_src, kr_dst, vr_src,
+                                            vr_dst, c2, c3, s);
+  return launch_pack_lds<T, int64_t, 64>(c, counts, rk, rv, ik, iv, kr_src, kr_dst, vr_src,
+                                         vr_dst, c2, c3, s);
 }
 
 bool kivi_geometry_ok(int kvh, int d, int g, int bs) {
@@ -752,31 +1171,16 @@ extern "C" int kvq_kivi_store(const void* key_input, const void* value_input, vo
     return KVQ_ERR_GEOMETRY;
   if (n_key_pack % group_size) return KVQ_ERR_INVALID;
   if (n_value_pack * num_kv_heads >= 0x7fffffff) return KVQ_ERR_INVALID;
-  const int64_t kunits = n_key_pack / group_size * num_kv_heads * 2;
-  const int64_t kblocks = (kunits + 3) / 4;
-  const int64_t vunits = (n_value_pack * num_kv_heads + 3) / 4;  // 4 rows per wave
-  const int64_t vblocks = (vunits + 3) / 4;
-  const int64_t rchunks = (n_key_ring + n_value_ring) * num_kv_heads * (head_size / 8);
-  const int64_t rblocks = (rchunks + 255) / 256;
-  const int64_t blocks = kblocks + vblocks + rblocks;
-  if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const FastDiv kdiv = FastDiv::make(static_cast<uint32_t>(num_kv_heads));
-#define KVQ_LAUNCH_STORE(T, GG)                                                               \
-  hipLaunchKernelGGL((kivi_store_kernel<T, GG, false>), dim3(static_cast<unsigned>(blocks)),  \
-                     dim3(256), 0, s, static_cast<T*>(ring_k), static_cast<T*>(ring_v),        \
-                     ring_rows, static_cast<const T*>(key_input),                              \
-                     static_cast<const T*>(value_input), jobs, n_key_pack, n_value_pack,       \
-                     n_key_ring, n_value_ring, kblocks, vblocks, kdiv, block_size, k_quant,    \
-                     k_scale, k_mn, v_quant, v_scale, v_mn)
-  if (dtype == KVQ_DTYPE_BF16) {
-    if (group_size == 128) { KVQ_LAUNCH_STORE(bf16, 128); } else { KVQ_LAUNCH_STORE(bf16, 64); }
-  } else {
-    if (group_size == 128) { KVQ_LAUNCH_STORE(f16, 128); } else { KVQ_LAUNCH_STORE(f16, 64); }
-  }
-#undef KVQ_LAUNCH_STORE
-  KVQ_LAUNCH_CHECK();
-  return KVQ_OK;
+  if (dtype == KVQ_DTYPE_BF16)
+    return launch_store_lds<bf16>(key_input, value_input, ring_k, ring_v, ring_rows, num_kv_heads,
+                                  group_size, block_size, jobs, nullptr, n_key_pack, n_value_pack,
+                                  n_key_ring, n_value_ring, k_quant, k_scale, k_mn, v_quant,
+                                  v_scale, v_mn, s);
+  return launch_store_lds<f16>(key_input, value_input, ring_k, ring_v, ring_rows, num_kv_heads,
+                               group_size, block_size, jobs, nullptr, n_key_pack, n_value_pack,
+                               n_key_ring, n_value_ring, k_quant, k_scale, k_mn, v_quant, v_scale,
+                               v_mn, s);
 }
 
 extern "C" int kvq_kivi_store_planned(const void* key_input, const void* value_input,
@@ -799,30 +1203,15 @@ extern "C" int kvq_kivi_store_planned(const void* key_input, const void* value_i
     return KVQ_ERR_GEOMETRY;
   if (cap_key_pack % group_size) return KVQ_ERR_INVALID;
   if (cap_value_pack * num_kv_heads >= 0x7fffffff) return KVQ_ERR_INVALID;
-  const int64_t kunits = cap_key_pack / group_size * num_kv_heads * 2;
-  const int64_t kblocks = (kunits + 3) / 4;
-  const int64_t vunits = (cap_value_pack * num_kv_heads + 3) / 4;  // 4 rows per wave
-  const int64_t vblocks = (vunits + 3) / 4;
-  const int64_t rchunks = 2 * cap_ring * num_kv_heads * (head_size / 8);
-  const int64_t rblocks = (rchunks + 255) / 256;
-  const int64_t blocks = kblocks + vblocks + rblocks;
-  if (blocks == 0) return KVQ_OK;
-  if (blocks > 0x7fffffff) return KVQ_ERR_INVALID;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const FastDiv kdiv = FastDiv::make(static_cast<uint32_t>(num_kv_heads));
-#define KVQ_LAUNCH_STORE(T, GG)                                                               \
-  hipLaunchKernelGGL((kivi_store_kernel<T, GG, true>), dim3(static_cast<unsigned>(blocks)),   \
-                     dim3(256), 0, s, static_cast<T*>(ring_k), static_cast<T*>(ring_v),        \
-                     ring_rows, static_cast<const T*>(key_input),                              \
-                     static_cast<const T*>(value_input), plan, cap_key_pack, cap_value_pack,   \
-                     cap_ring, cap_ring, kblocks, vblocks, kdiv, block_size, k_quant, k_scale, \
-                     k_mn, v_quant, v_scale, v_mn)
-  if (dtype == KVQ_DTYPE_BF16) {
-    if (group_size == 128) { KVQ_LAUNCH_STORE(bf16, 128); } else { KVQ_LAUNCH_STORE(bf16, 64); }
-  } else {
-    if (group_size == 128) { KVQ_LAUNCH_STORE(f16, 128); } else { KVQ_LAUNCH_STORE(f16, 64); }
-  }
-#undef KVQ_LAUNCH_STORE
-  KVQ_LAUNCH_CHECK();
-  return KVQ_OK;
+  // plan: the four counts, then the job sections at capacity offsets
+  if (dtype == KVQ_DTYPE_BF16)
+    return launch_store_lds<bf16>(key_input, value_input, ring_k, ring_v, ring_rows, num_kv_heads,
+                                  group_size, block_size, plan + 4, plan, cap_key_pack,
+                                  cap_value_pack, cap_ring, cap_ring, k_quant, k_scale, k_mn,
+                                  v_quant, v_scale, v_mn, s);
+  return launch_store_lds<f16>(key_input, value_input, ring_k, ring_v, ring_rows, num_kv_heads,
+                               group_size, block_size, plan + 4, plan, cap_key_pack,
+                               cap_value_pack, cap_ring, cap_ring, k_quant, k_scale, k_mn, v_quant,
+                               v_scale, v_mn, s);
 }

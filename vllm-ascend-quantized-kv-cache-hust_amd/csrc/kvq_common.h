@@ -178,7 +178,11 @@ __device__ __forceinline__ uint32_t kivi_quantize(float x, float mn, float scale
 // add: k + pred(0.5) rounds to k + 0.5 for k >= 1.  v >= 0 and q < 15.5 keep
 // the codes in 0..15 with no clamp.  v_cvt_pk_u8_f32 drops each code into a
 // byte (even codes of the word in one register, odd codes in another) and a
-// single shift-or interleaves the nibbles.
+// single shift-or interleaves the nibbles.  The choice between k and k + 1
+// is folded into that conversion, which rounds to nearest even: it converts
+// t + 0.25 when y >= 0 and t - 0.25 otherwise (t = k + 0.5, or pred(0.5) at
+// k = 0, so the two round to k + 1 and k).  y is never -0: its outer product
+// is positive, so an exact cancellation rounds to +0.
 __device__ __forceinline__ uint32_t kivi_pack_word(const float (&x)[8], float mn, float scale) {
   const float rcp = __builtin_amdgcn_rcpf(scale);
   const float s24 = scale * 0x1p-24f;
@@ -190,7 +194,9 @@ __device__ __forceinline__ uint32_t kivi_pack_word(const float (&x)[8], float mn
     const float t = k + 0x1.fffffep-2f;
     const float e = __int_as_float(__float_as_int(t) & 0x7f800000);
     const float y = __builtin_fmaf(s24, e, __builtin_fmaf(-scale, t, d));
-    const float r = y >= 0.0f ? k + 1.0f : k;
+    // +-0.25 with y's sign: (y & sign) | bits(0.25)
+    const float step = __uint_as_float((__float_as_uint(y) & 0x80000000u) | 0x3e800000u);
+    const float r = t + step;
     if (i % 2 == 0)
       ev = __builtin_amdgcn_cvt_pk_u8_f32(r, i / 2, ev);
     else
