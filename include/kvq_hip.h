@@ -231,6 +231,27 @@ int64_t kvq_plan_kivi_decode(const int32_t* seqs, int64_t batch, int num_kv_head
                              int32_t* work, int64_t cap_work, int32_t* pieces,
                              int64_t cap_pieces, int64_t* num_pieces);
 
+/* Host checks of one decode step (host arrays, no device access), in one
+ * pass: the gather's metadata gate (pkg/ops/kivi_layout.py:205-238: the
+ * table covers the longest sequence, live block ids lie in [0, num_blocks))
+ * and the window-entry liveness of the residual rows
+ * (pkg/methods/kivi_int4/attention_backend.py:813-836: an entry written at
+ * position p with slot s is live while p < seq_len and the request's table
+ * still holds s's block at column p / block_size).
+ *   table int64 [batch, max_blocks]; seq_lens, rows int64 [batch] (ring row
+ *   of each request, -1 for none); k_slot, k_pos, v_slot, v_pos int64
+ *   [ring_rows, ring_len] (the host mirror of both windows)
+ * *kind: 0 (pass), 1 (a live block id < 0), 2 (a live block id >=
+ * num_blocks; the return value is the first such request), 3 (the table does
+ * not cover the longest sequence).  suspect[i] = 1 when request i's window
+ * holds an entry that may no longer be live.  Returns >= 0, or
+ * KVQ_ERR_INVALID. */
+int64_t kvq_kivi_step_check(const int64_t* table, int64_t batch, int64_t max_blocks,
+                            const int64_t* seq_lens, int64_t num_blocks, int64_t block_size,
+                            const int64_t* rows, const int64_t* k_slot, const int64_t* k_pos,
+                            const int64_t* v_slot, const int64_t* v_pos, int64_t ring_rows,
+                            int64_t ring_len, int32_t* suspect, int32_t* kind);
+
 /* kvq_kivi_store with its counts and jobs in one device buffer, sized for
  * capacities: plan (int64, device) = [n_key_pack, n_value_pack, n_key_ring,
  * n_value_ring, key pack src[cap_key_pack], key pack slot[cap_key_pack],

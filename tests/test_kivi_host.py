@@ -1068,3 +1068,62 @@ def test_int4_pipeline_across_geometries(head, kvh, group, block, residual):
     assert torch.isfinite(out).all() and out.abs().sum() > 0
     assert kivi_byte_cache_layout(kb, vb, num_kv_heads=kvh, head_size=head,
                                   group_size=group) == layout
+
+
+def test_native_step_check_matches_the_python_checks():
+    """kvq_kivi_step_check (the decode step's one-pass host check) raises as
+    check_gather_metadata_host does and flags the rows suspect_rows flags."""
+    from vllm_ascend_quantized_kv_cache.methods.kivi_int4.residual import KiviResidualRing
+    from vllm_ascend_quantized_kv_cache.ops.kivi_layout import check_gather_metadata_host
+
+    rng = np.random.default_rng(0)
+    bs, nb, rows_n, window = 16, 24, 6, 8
+    seen = {"ok": 0, "err": 0, "suspect": 0}
+    for _ in range(400):
+        ring = KiviResidualRing(rows_n, window, 2, 8, device="cpu")
+        b = int(rng.integers(1, 6))
+        maxb = int(rng.integers(1, 5))
+        table = rng.integers(0, nb, size=(b, maxb))
+        if rng.random() < 0.15:
+            table[rng.integers(b), rng.integers(maxb)] = -1
+        if rng.random() < 0.15:
+            table[rng.integers(b), rng.integers(maxb)] = nb + int(rng.integers(0, 3))
+        lens = rng.integers(0, maxb * bs + (3 if rng.random() < 0.1 else 1), size=b)
+        rows = np.full(b, -1, dtype=np.int64)
+        for i, r in enumerate(rng.permutation(rows_n)[:b]):
+            if rng.random() < 0.8:
+                rows[i] = r
+        for side in (True, False):
+            for i in range(b):
+                if rows[i] < 0:
+                    continue
+                for lane in range(window + 1):
+                    if rng.random() < 0.5:
+                        continue
+                    p = int(rng.integers(-1, int(lens[i]) + 2))
+                    col = min(max(p, 0) // bs, maxb - 1)
+                    good = table[i, col] * bs + max(p, 0) % bs
+                    s = good if rng.random() < 0.9 else int(rng.integers(0, nb * bs))
+                    ring.lane_slot[side][rows[i], lane] = s
+                    ring.lane_pos[side][rows[i], lane] = p
+        want_err = got_err = None
+        want = got = None
+        try:
+            check_gather_metadata_host(table, lens.tolist(), max_blocks=maxb, num_blocks=nb,
+                                       block_size=bs)
+            have = rows >= 0
+            idx = ring.suspect_rows(rows[have], lens[have], table[have], bs)
+            want = np.flatnonzero(have)[idx]
+        except RuntimeError as e:
+            want_err = str(e)
+        try:
+            got = ring.step_check(rows, lens, table, num_blocks=nb, block_size=bs)
+        except RuntimeError as e:
+            got_err = str(e)
+        assert want_err == got_err
+        if want_err is None:
+            assert np.array_equal(want, got)
+            seen["suspect" if got.size else "ok"] += 1
+        else:
+            seen["err"] += 1
+    assert min(seen.values()) > 10, seen

@@ -210,3 +210,66 @@ extern "C" int64_t kvq_plan_kivi_decode(const int32_t* seqs, int64_t batch, int 
   if (pl.overflow) return KVQ_ERR_CAPACITY;
   return pl.n;
 }
+
+// Host checks of one decode step, in one pass over the step's metadata (the
+// Python forms are check_gather_metadata_host and
+// KiviResidualRing.suspect_rows; this one runs per step on the fast path).
+extern "C" int64_t kvq_kivi_step_check(const int64_t* table, int64_t batch, int64_t max_blocks,
+                                       const int64_t* seq_lens, int64_t num_blocks,
+                                       int64_t block_size, const int64_t* rows,
+                                       const int64_t* k_slot, const int64_t* k_pos,
+                                       const int64_t* v_slot, const int64_t* v_pos,
+                                       int64_t ring_rows, int64_t ring_len, int32_t* suspect,
+                                       int32_t* kind) {
+  if (batch < 0 || max_blocks < 0 || block_size <= 0 || ring_len < 0 || !kind) return KVQ_ERR_INVALID;
+  *kind = 0;
+  if (batch == 0) return 0;
+  if (!table || !seq_lens || !rows || !suspect) return KVQ_ERR_INVALID;
+  // coverage of the longest sequence
+  int64_t longest = 0;
+  for (int64_t i = 0; i < batch; ++i) longest = seq_lens[i] > longest ? seq_lens[i] : longest;
+  if (longest > max_blocks * block_size) {
+    *kind = 3;
+    return 0;
+  }
+  // live block ids: the first request with a bad one, negative before too large
+  for (int64_t i = 0; i < batch; ++i) {
+    const int64_t live = seq_lens[i] > 0 ? (seq_lens[i] + block_size - 1) / block_size : 0;
+    bool neg = false, out = false;
+    for (int64_t c = 0; c < live; ++c) {
+      const int64_t b = table[i * max_blocks + c];
+      neg |= b < 0;
+      out |= b >= num_blocks;
+    }
+    if (neg || out) {
+      *kind = neg ? 1 : 2;
+      return i;
+    }
+  }
+  // window entries that may no longer be live: an entry at position p with
+  // slot s is live when p < seq_len and the table still has s's block at
+  // column p / block_size
+  const int64_t* slots[2] = {k_slot, v_slot};
+  const int64_t* poss[2] = {k_pos, v_pos};
+  for (int64_t i = 0; i < batch; ++i) {
+    suspect[i] = 0;
+    const int64_t row = rows[i];
+    if (row < 0) continue;
+    if (row >= ring_rows || !k_slot || !k_pos || !v_slot || !v_pos) return KVQ_ERR_INVALID;
+    for (int side = 0; side < 2 && !suspect[i]; ++side) {
+      const int64_t* ls = slots[side] + row * ring_len;
+      const int64_t* lp = poss[side] + row * ring_len;
+      for (int64_t lane = 0; lane < ring_len; ++lane) {
+        if (ls[lane] < 0) continue;
+        const int64_t p = lp[lane];
+        bool ok = p >= 0 && p < seq_lens[i] && p / block_size < max_blocks;
+        if (ok) ok = table[i * max_blocks + p / block_size] == ls[lane] / block_size;
+        if (!ok) {
+          suspect[i] = 1;
+          break;
+        }
+      }
+    }
+  }
+  return 0;
+}

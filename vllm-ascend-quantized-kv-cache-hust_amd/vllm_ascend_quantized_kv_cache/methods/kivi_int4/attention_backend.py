@@ -88,6 +88,7 @@ class AscendKiviInt4AttentionBackendMixin:
         self.v_scale_cache = None
         self.v_mn_cache = None
         self._kivi_ring: KiviResidualRing | None = None
+        self._kivi_bound_buffers = None
         scheduler_config = getattr(vllm_config, "scheduler_config", None)
         max_num_seqs = getattr(scheduler_config, "max_num_seqs", 128)
         self.kivi_max_num_seqs = (
@@ -151,6 +152,15 @@ class AscendKiviInt4AttentionBackendMixin:
         if len(kv_cache) == 0:
             return
         if len(kv_cache) == 2:
+            # the same two buffers as the last call: the six views are still
+            # bound (they hold the buffers' storage, so no other allocation
+            # can have taken these addresses)
+            bound = (kv_cache[0].data_ptr(), kv_cache[1].data_ptr(), tuple(kv_cache[0].shape),
+                     tuple(kv_cache[1].shape), kv_cache[0].dtype, kv_cache[1].dtype,
+                     self.num_kv_heads, self.head_size, self.kivi_group_size)
+            if (bound == getattr(self, "_kivi_bound_buffers", None) and self._kivi_ring is not None
+                    and all(t is not None for t in self._kivi_caches())):
+                return
             layout = kivi_byte_cache_layout(
                 kv_cache[0],
                 kv_cache[1],
@@ -159,6 +169,9 @@ class AscendKiviInt4AttentionBackendMixin:
                 group_size=self.kivi_group_size,
             )
             kv_cache = kivi_caches_from_byte_tensors(kv_cache[0], kv_cache[1], layout)
+            self._kivi_bound_buffers = bound
+        else:
+            self._kivi_bound_buffers = None
         if len(kv_cache) != 6:
             raise RuntimeError(
                 "KIVI INT4 kv_cache must be a 2-tuple of byte buffers or a "
@@ -998,16 +1011,16 @@ class AscendKiviInt4AttentionBackendMixin:
         entry that may no longer be live (its check, and any compaction,
         belongs after the store, which the general path orders).
         """
-        from ...ops.kivi_layout import check_gather_metadata_host
-
         ring = self._ensure_kivi_residual_buffers()
         bs = self._get_kivi_block_size()
         lens = np.asarray([int(x) for x in attn_metadata.seq_lens_list], dtype=np.int64)
         b = lens.size
         keys = self._get_kivi_req_keys(getattr(attn_metadata, "req_ids", None), b)
         table = self._host_array(attn_metadata, "block_tables")[:b].astype(np.int64, copy=False)
-        check_gather_metadata_host(table, lens.tolist(), max_blocks=table.shape[1],
-                                   num_blocks=self.k_quant_cache.shape[0], block_size=bs)
+        # the gather's metadata gate and the window liveness, one native pass
+        rows = self._request_rows(keys)
+        suspect = ring.step_check(rows, lens, table, num_blocks=self.k_quant_cache.shape[0],
+                                  block_size=bs)
         n = 0
         if key is not None and value is not None:
             n = min(int(getattr(attn_metadata, "num_actual_tokens", key.shape[0])), key.shape[0])
@@ -1023,9 +1036,7 @@ class AscendKiviInt4AttentionBackendMixin:
             if ((table[np.arange(b), col] != slots // bs).any()
                     or (slots % bs != pos % bs).any()):
                 return None
-        rows = self._request_rows(keys)
-        have = rows >= 0
-        if have.any() and ring.suspect_rows(rows[have], lens[have], table[have], bs).size:
+        if suspect.size:
             if not allow_compaction:
                 raise RuntimeError(
                     "KIVI decode step: a window entry may no longer be live; run this "

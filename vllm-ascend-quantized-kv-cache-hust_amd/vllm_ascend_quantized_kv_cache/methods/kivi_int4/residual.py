@@ -282,6 +282,42 @@ class KiviResidualRing:
             suspect |= (occ & ~ok).any(axis=1)
         return np.flatnonzero(suspect)
 
+    def step_check(self, rows: np.ndarray, seq_lens: np.ndarray, table: np.ndarray, *,
+                   num_blocks: int, block_size: int) -> np.ndarray:
+        """A decode step's host checks in one native pass
+        (``kvq_kivi_step_check``): the gather's metadata gate, raising as
+        ``check_gather_metadata_host`` does, then ``suspect_rows`` for the
+        requests with a row (``rows[i] >= 0``).  Returns the indices into
+        ``rows`` of the suspect requests."""
+        from ...ops import _native
+
+        table = np.ascontiguousarray(table, dtype=np.int64)
+        lens = np.ascontiguousarray(seq_lens, dtype=np.int64)
+        rows = np.ascontiguousarray(rows, dtype=np.int64)
+        b, maxb = table.shape
+        if lens.size != b or rows.size != b:
+            raise ValueError("step_check: table, seq_lens and rows must have one entry per request")
+        k_slot, k_pos, v_slot, v_pos = (np.ascontiguousarray(a) for a in (
+            self.lane_slot[True], self.lane_pos[True], self.lane_slot[False],
+            self.lane_pos[False]))
+        suspect = np.zeros(b, dtype=np.int32)
+        kind = np.zeros(1, dtype=np.int32)
+        r = _native.lib().kvq_kivi_step_check(
+            table.ctypes.data, b, maxb, lens.ctypes.data, int(num_blocks), int(block_size),
+            rows.ctypes.data, k_slot.ctypes.data, k_pos.ctypes.data, v_slot.ctypes.data,
+            v_pos.ctypes.data, self.rows, self.ring_len, suspect.ctypes.data, kind.ctypes.data)
+        _native.check(int(r) if r < 0 else 0, "kvq_kivi_step_check")
+        if kind[0] == 3:
+            raise RuntimeError(
+                "block_table does not cover the longest KIVI sequence: "
+                f"max_seq_len={int(lens.max())}, max_blocks={maxb}, block_size={block_size}."
+            )
+        if kind[0] == 1:
+            raise RuntimeError("KIVI block_table has invalid block ids for live tokens.")
+        if kind[0] == 2:
+            raise RuntimeError("KIVI block_table references blocks outside the int4 cache.")
+        return np.flatnonzero(suspect)
+
     # -- mutation ----------------------------------------------------------
 
     def load_row(self, row: int, *, is_key: bool, slots: list[int],

@@ -61,6 +61,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "kvq_plan_kivi_decode": (
         _I64, [_P, _I64, _I, _I, _I, _I64, _D, _P, _P, _I64, _P, _I64, _P]
     ),
+    "kvq_kivi_step_check": (
+        _I64,
+        [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _I64, _P, _P],
+    ),
     "kvq_kivi_store_planned": (
         _I,
         [_P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _I64, _I64, _I64,
