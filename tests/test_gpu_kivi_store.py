@@ -1,5 +1,6 @@
 # SPDX-License-Identifier: Apache-2.0
-"""One-launch store (``kvq_kivi_store``) against the separate launches.
+"""One-launch store (``kvq_kivi_store``) against the separate launches and
+against the oracle.
 
 The key pack, value pack and ring-write entry points are each pinned to the
 oracle elsewhere; here one batch of all four kinds of work is applied once
@@ -16,6 +17,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+from oracle import kvq_oracle as ref
 from tests._util import empty_kivi_caches
 from vllm_ascend_quantized_kv_cache.ops.kivi_pack import (
     kivi_store,
@@ -112,3 +114,48 @@ def test_store_one_launch_matches_separate_launches(gpu_device, segments, g, dty
         assert (caches_b[0] != 7).any()
     if counts[1]:
         assert (caches_b[3] != 7).any()
+
+
+@pytest.mark.parametrize("g", [64, 128])
+def test_store_large_batch_matches_oracle(gpu_device, g):
+    """A store batch large enough that each wave of the one-launch kernel
+    takes several units (two and four per wave: the counted-wait pipeline),
+    its pack sources scattered over ring rows and input rows, checked bit for
+    bit against the oracle's packs of the same source rows."""
+    dev = gpu_device
+    dtype = torch.bfloat16
+    nb, rows, cap = 512, 8, 129
+    for n_groups, n_val in ((60, 1500), (200, 6000)):
+        gen = torch.Generator().manual_seed(5 * g + n_groups)
+        chan = torch.exp(torch.randn(KVH, D, generator=gen))
+        n_in = n_groups * g + 64
+        ring_k = (torch.randn(rows, cap, KVH, D, generator=gen) * chan).to(dtype)
+        ring_v = torch.randn(rows, cap, KVH, D, generator=gen).to(dtype)
+        in_k = (torch.randn(n_in, KVH, D, generator=gen) * chan).to(dtype)
+        in_v = torch.randn(n_in, KVH, D, generator=gen).to(dtype)
+        n_ring = rows * cap
+        src_k = torch.cat([ring_k.view(-1, KVH, D), in_k])
+        src_v = torch.cat([ring_v.view(-1, KVH, D), in_v])
+        # key groups: sources anywhere in [ring ; input], whole groups at
+        # group-aligned offsets of shuffled blocks
+        kp_src = torch.randint(0, n_ring + n_in, (n_groups * g,), generator=gen)
+        gpb = BS // g
+        blocks = torch.randperm(nb // 2, generator=gen)
+        kp_slot = torch.cat([blocks[i // gpb] * BS + (i % gpb) * g + torch.arange(g)
+                             for i in range(n_groups)])
+        # value rows: distinct slots in the other half of the pool, a few skipped
+        vp_src = torch.randint(0, n_ring + n_in, (n_val,), generator=gen)
+        vp_slot = nb // 2 * BS + torch.randperm(nb // 2 * BS, generator=gen)[:n_val]
+        vp_slot[::97] = -1
+        print(f"large store case: g={g} groups={n_groups} values={n_val}", flush=True)
+        want = empty_kivi_caches(nb, BS, KVH, D, g, fill=7)
+        ref.pack_key_cache(src_k[kp_src], kp_slot, want[0], want[1], want[2], g)
+        ref.pack_value_cache(src_v[vp_src], vp_slot, want[3], want[4], want[5], g)
+        got = tuple(t.to(dev) for t in empty_kivi_caches(nb, BS, KVH, D, g, fill=7))
+        jobs = torch.cat([kp_src, kp_slot, vp_src, vp_slot]).to(torch.int64).to(dev)
+        assert kivi_store(in_k.to(dev), in_v.to(dev), ring_k.to(dev), ring_v.to(dev), jobs,
+                          (n_groups * g, n_val, 0, 0), got, g)
+        torch.cuda.synchronize()
+        names = ("k_quant", "k_scale", "k_mn", "v_quant", "v_scale", "v_mn")
+        for name, a, b in zip(names, want, got):
+            assert torch.equal(a.view(torch.int32), b.cpu().view(torch.int32)), f"{name} differs"
