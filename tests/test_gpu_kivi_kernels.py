@@ -161,8 +161,11 @@ def test_gather_bit_exact(gpu_device, d, kvh, g, bs):
         assert torch.equal(want_v, got_v.cpu()), out_dtype
 
 
-def _ring_case(dev, d, kvh, g, bs, r_len, lens, seed, ring_dtype=torch.float32):
-    """Packed history for several requests plus residual rings (FIFO, wrapped)."""
+def _ring_case(dev, d, kvh, g, bs, r_len, lens, seed, ring_dtype=torch.float32, split=None):
+    """Packed history for several requests plus residual rings (FIFO, wrapped).
+
+    ``split(n) -> (hist_k, hist_v)``: the int4 history of each side (default:
+    the incremental rule, ``ref.incremental_split``)."""
     nb = sum(-(-n // bs) for n in lens) + 2
     maxb = max(-(-n // bs) for n in lens)
     table = torch.full((len(lens), maxb), -1, dtype=torch.int32)
@@ -181,7 +184,7 @@ def _ring_case(dev, d, kvh, g, bs, r_len, lens, seed, ring_dtype=torch.float32):
         key, value = make_kv(n, kvh, d, seed=seed * 31 + b)
         keys.append(key)
         values.append(value)
-        hk, hv = ref.incremental_split(n, r_len)
+        hk, hv = split(n) if split else ref.incremental_split(n, r_len)
         slots = slots_for(table[b], range(n), bs)
         if hk:
             ref.pack_key_cache(key[:hk], slots[:hk], *cpu[:3], g)
@@ -287,6 +290,54 @@ def test_decode_head_group_geometries(gpu_device, kvh, g, bs, rep):
             ring_k.to(gpu_device), ring_v.to(gpu_device), scale, g, split_tokens=split,
         )
         torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("kvh,g,bs,rep", [(8, 128, 128, 5), (8, 32, 64, 4), (4, 64, 256, 8)])
+def test_decode_tail_int4_values_match_oracle(gpu_device, kvh, g, bs, rep):
+    """Tails whose values are int4: the key window reaches further back than the
+    value window (hist_k < hist_v), so the tail's first positions pair ring keys
+    with int4 values; tails start off the 32-position grid and cross pages."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
+        DecodeSeq,
+        kivi_decode_attention,
+        plan_decode_pieces,
+    )
+
+    d = 128
+    r_len = 3 * g
+
+    def split(n):  # keys: whole groups, at least g + 1 in the ring; values: 0-9 in the ring
+        hk = max(0, (n - g - 1) // g * g)
+        return hk, max(hk, n - n % 10)
+
+    lens = [5 * g + 37, 2 * g + 1, 3 * g - 11, 7 * g + 64, 41]
+    cpu, table, ring_k, ring_v, seqs, wk, wv, _, _ = _ring_case(
+        gpu_device, d, kvh, g, bs, r_len, lens, seed=33, ring_dtype=torch.bfloat16, split=split
+    )
+    assert any(hv > hk for (_, hk, hv, *_r) in seqs)
+    hq = kvh * rep
+    q = torch.randn(len(lens), hq, d, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    scale = d ** -0.5
+    dk, dv = ref.dequant_gather(*cpu, table, torch.tensor(lens), torch.float32, g)
+    dk = ref.overlay_residual(dk, lens, wk)
+    dv = ref.overlay_residual(dv, lens, wv)
+    want = ref.attention(q, dk, dv, [1] * len(lens), lens, scale, causal=True)
+    dseqs = [DecodeSeq(n, hk, hv, row, ks_, vs_) for (n, hk, hv, row, ks_, vs_) in seqs]
+    plans = [None, 64]
+    for split_tokens in plans:
+        got = kivi_decode_attention(
+            q.to(gpu_device), to_dev(cpu, gpu_device), table.to(gpu_device), dseqs,
+            ring_k.to(gpu_device), ring_v.to(gpu_device), scale, g, split_tokens=split_tokens,
+        )
+        torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
+    # pieces cut on few CUs: a wave walks several tail items of several requests
+    meta, work, pieces = plan_decode_pieces(dseqs, kvh, cu_count=3)
+    plan = tuple(torch.from_numpy(x).to(gpu_device) for x in (meta, work, pieces))
+    got = kivi_decode_attention(
+        q.to(gpu_device), to_dev(cpu, gpu_device), table.to(gpu_device), dseqs,
+        ring_k.to(gpu_device), ring_v.to(gpu_device), scale, g, plan=plan,
+    )
+    torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
 
 
 @pytest.mark.parametrize("kvh,g,bs,rep", [(8, 128, 128, 5), (8, 64, 128, 8), (4, 32, 64, 4)])

@@ -785,7 +785,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, int hpw, 
 
   extern __shared__ __align__(16) char lds_raw[];
   const int32_t* pieces = TAIL ? pieces_arg : nullptr;
-  const int lane = threadIdx.x & 63;
+  const int lane0 = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int hw = wave % hpw;    // head within the workgroup's group
   const int half = wave / hpw;  // < npair
@@ -807,8 +807,6 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, int hpw, 
   }
   const int h = qh * hpw + hw;
   const int rep = hq / kvh;
-  const int n = lane & 15;
-  const int kg = lane >> 4;
   // every branch below depends on the work item only: workgroup-uniform, so
   // every wave meets the same barriers
   for (int wi = it0; wi < it1; ++wi) {
@@ -822,11 +820,16 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, int hpw, 
       tail::Partial tp = tail::tail_item<TQ>(my_lds, query, hq, kvh, qscale, kq, ks, km, vq, vs,
                                              vm, bs, g, nb, block_table, maxb, seq_meta, wk, wi,
                                              h, ring_k, ring_v, ring_len, half, npair);
-      if (npair == 2) tail::merge_halves(tp, xfer, half, lane);
-      if (half == 0) tail::tail_store(tp, wi, hq, h, rep, lane, ws_o, ws_ml);
+      if (npair == 2) tail::merge_halves(tp, xfer, half, lane0);
+      if (half == 0) tail::tail_store(tp, wi, hq, h, rep, lane0, ws_o, ws_ml);
       continue;
     }
   }
+  // lane-dependent set-up per item (not hoisted out of the item loop)
+  int lane = lane0;
+  asm volatile("" : "+v"(lane));
+  const int n = lane & 15;
+  const int kg = lane >> 4;
   const int b = wk[0];
   const int pb = wk[1];
   const int pe = wk[2];

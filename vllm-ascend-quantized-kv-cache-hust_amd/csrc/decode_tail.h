@@ -15,10 +15,12 @@
 //   * S^T = (K_hi + K_lo) * Q^T with v_mfma_f32_16x16x32_{bf16,f16} on the raw
 //     query (exact products, fp32 accumulation; the softmax scale and log2(e)
 //     are applied to the fp32 scores);
-//   * then stages V transposed as [dim][token] over the same LDS (the keys are
-//     consumed by then) and computes O = P * V with P split into two T parts
-//     (hi + lo), so p keeps ~16 bits;
+//   * then stages V as rows over the same LDS (the keys are consumed by then)
+//     and computes O = P * V with P split into two T parts (hi + lo), so p
+//     keeps ~16 bits, the V operand gathered by transposing LDS reads;
 //   * leaves (m, l, o) per head in the split-K workspace for the combine.
+// The int4 key words and the ring value rows of the next sub-tile are loaded
+// into registers while the current one computes.
 // LDS: 2 * kTT * kKP * 2 bytes = 17 KiB, inside the int4 path's 19-20 KiB per wave.
 // Two waves may share an item: wave `half` of `nhalf` takes every nhalf-th
 // sub-tile, and the halves' partial results merge through LDS (merge_halves).
@@ -146,15 +148,47 @@ __device__ __forceinline__ void merge_halves(Partial& p, float* __restrict__ xfe
 }
 
 constexpr int kD = 128;
-constexpr int kTT = 32;          // positions per sub-tile
-constexpr int kKP = kD + 8;      // K row pitch (elements): rows stay 16-byte aligned
-constexpr int kVP = kTT + 4;     // V^T row pitch (elements): 8-byte aligned token quads
+constexpr int kTT = 32;           // positions per sub-tile
+constexpr int kKP = kD + 8;       // K row pitch (elements): rows stay 16-byte aligned
 constexpr int kKW = kTT / 8 + 1;  // key words of one dim covering a sub-tile (8-aligned start)
 constexpr int kLdsBytes = 2 * kTT * kKP * 2;
-static_assert(kD * kVP <= 2 * kTT * kKP, "V^T fits the key region it reuses");
+static_assert(kTT * kD * 2 <= kLdsBytes, "the V rows fit the key region they reuse");
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s* lds_v4s_ptr;
+
+// One sub-tile's int4 key operands for the lane's dims 2*lane and 2*lane + 1:
+// the kKW words covering the sub-tile, and the scale and minimum of the (at
+// most two: g >= 32) key groups they fall in, [dim][group].
+struct KeyWords {
+  uint32_t w[2][kKW];
+  float sc[2][2], mn[2][2];
+};
+
+// Eight 16-byte pieces of ring rows, as loaded by one lane (vector types, so
+// the pieces stay in registers: uint4 copies become byte copies that keep
+// a loop-carried array in scratch memory).
+typedef uint32_t w4 __attribute__((ext_vector_type(4)));
+struct Rows8 {
+  w4 r[8];
+};
 
 // Work item wi (kind 1) for kv head h: the partial over sub-tiles half,
 // half + nhalf, ... of the item.  lds_raw: at least kLdsBytes, the wave's own.
+//
+// Most global loads of a sub-tile are issued into registers while the
+// previous sub-tile computes, so that the wave waits for memory less often:
+//   int4 key words    issued after the scores, staged at the next sub-tile's start;
+//   ring value rows   issued after the PV step, staged after the next scores;
+//   block-table rows  two sub-tiles ahead, so no load waits on another;
+//   ring key rows     issued at the sub-tile's start, in flight while its int4
+//                     keys are staged (a sub-tile ahead they would need 32 more
+//                     registers, which the int4 path sharing the kernel's
+//                     allocation cannot spare).
+// Values go to LDS as rows ([token][dim], 16-byte chunk c of row r at chunk
+// c ^ 2 (r % 4)) and reach the PV MFMAs through transposing reads.  Int4 values
+// inside a tail (a value side without a window) are loaded and dequantized
+// where they are staged.
 template <typename T>
 __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T* __restrict__ query,
                                           int hq, int kvh, float qscale,
@@ -171,10 +205,14 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
                                           const T* __restrict__ ring_v, int ring_len,
                                           int half, int nhalf) {
   constexpr int D = kD;
-  uint16_t* sk = reinterpret_cast<uint16_t*>(lds_raw);  // [kTT][kKP] key hi parts
-  uint16_t* skl = sk + kTT * kKP;                        // [kTT][kKP] key lo parts
-  uint16_t* svt = sk;                                    // [D][kVP], after the scores
-  const int lane = threadIdx.x & 63;
+  uint16_t* sk = reinterpret_cast<uint16_t*>(lds_raw);  // [kTT][kKP] int4 key hi parts
+  uint16_t* skl = sk + kTT * kKP;                        // [kTT][kKP] int4 key lo parts
+  char* sv = lds_raw;                                    // [kTT][D] value rows, after the scores
+  // opaque to the optimizer: the lane-dependent set-up below is recomputed per
+  // item instead of being hoisted out of the caller's item loop, where it
+  // would stay live (in registers) across the int4 path as well
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));
   const int b = wk[0];
   const int pb = wk[1];
   const int pe = wk[2];
@@ -191,6 +229,12 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
   const int wpd = bs >> 3;
   const int32_t* bt = block_table + static_cast<int64_t>(b) * maxb;
   const int64_t ring_row0 = static_cast<int64_t>(row) * ring_len;
+  const int c0 = 2 * lane;  // the int4 key dims this lane stages
+  // lane 0 of the request's ring row for head h; lanes lie 32-bit byte offsets
+  // past it (a ring row of all heads is under 4 GiB), a uniform base plus a
+  // lane offset per load
+  const char* rk_base = reinterpret_cast<const char*>(ring_k + (ring_row0 * kvh + h) * D);
+  const char* rv_base = reinterpret_cast<const char*>(ring_v + (ring_row0 * kvh + h) * D);
 
   // B operand of QK: q[head n][32*s4 + 8*kg + i], raw (the scale is applied in fp32)
   u8v qb[4];
@@ -204,80 +248,164 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
     }
   }
 
+  // positions of the sub-tile at p: nt in the item, the first mk with int4
+  // keys, the first mv with int4 values
+  auto count = [&](int p, int hist) {
+    const int nt = (pe - p) < kTT ? (pe - p) : kTT;
+    return hist - p < 0 ? 0 : (hist - p < nt ? hist - p : nt);
+  };
+  // lane j: the block-table entry of the sub-tile's page j (pages past its
+  // last repeat the last); only sub-tiles with int4 data look pages up
+  auto load_pages = [&](int p) -> int32_t {
+    if (p >= pe || (p >= khist && p >= vhist)) return 0;  // uniform
+    const int last = ((pe - p < kTT ? pe : p + kTT) - 1) >> bsh;
+    const int idx = (p >> bsh) + lane;
+    return bt[idx < last ? idx : last];
+  };
+  // the page of position q of the sub-tile at p (all lanes take part)
+  auto page_of = [&](int32_t pg, int p, int q) -> int64_t {
+    const int64_t blk = __shfl(pg, (q >> bsh) - (p >> bsh), 64);
+    return blk < 0 ? 0 : (blk >= nb ? nb - 1 : blk);  // never leave the cache
+  };
+  // the same for a position the whole wave shares: a scalar
+  auto page_uniform = [&](int32_t pg, int p, int q) -> int64_t {
+    const int64_t blk = __builtin_amdgcn_readlane(pg, (q >> bsh) - (p >> bsh));
+    return blk < 0 ? 0 : (blk >= nb ? nb - 1 : blk);
+  };
+  // int4 key words, scales and minima of positions [p, p + mk): the kKW words
+  // of each of the lane's two dims (clamped into the range: every load valid)
+  auto load_key_words = [&](int p, int32_t pg, KeyWords& kw) {
+    const int mk = count(p, khist);
+    if (mk == 0) return;  // uniform
+    const int first = p & ~7;
+    // every position here is the whole wave's: pages and offsets are scalars,
+    // and the lane's dims c0 and c0 + 1 add byte offsets to a scalar base
+    const uint32_t wo = static_cast<uint32_t>(c0 * wpd * 4);
+    const uint32_t so = static_cast<uint32_t>(c0 * gpb * 4);
+#pragma unroll
+    for (int k = 0; k < kKW; ++k) {
+      const int q = first + 8 * k;
+      const int qq = q < p ? p : (q < p + mk ? q : p + mk - 1);
+      const int64_t r = (page_uniform(pg, p, qq) * kvh + h) * D;
+      const char* wb = reinterpret_cast<const char*>(kq + r * wpd + ((qq & (bs - 1)) >> 3));
+      kw.w[0][k] = *reinterpret_cast<const uint32_t*>(wb + wo);
+      kw.w[1][k] = *reinterpret_cast<const uint32_t*>(wb + wo + 4 * wpd);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {  // the groups of positions p and p + mk - 1
+      const int qq = s ? p + mk - 1 : p;
+      const int64_t r = (page_uniform(pg, p, qq) * kvh + h) * D * gpb + ((qq & (bs - 1)) >> gsh);
+      const char* sb = reinterpret_cast<const char*>(ks + r);
+      const char* mb = reinterpret_cast<const char*>(km + r);
+      kw.sc[0][s] = *reinterpret_cast<const float*>(sb + so);
+      kw.sc[1][s] = *reinterpret_cast<const float*>(sb + so + 4 * gpb);
+      kw.mn[0][s] = *reinterpret_cast<const float*>(mb + so);
+      kw.mn[1][s] = *reinterpret_cast<const float*>(mb + so + 4 * gpb);
+    }
+  };
+  // ring key rows: slot 4*jm + s4 holds row 16*jm + n of the sub-tile, dims
+  // 32*s4 + 8*kg .. + 7; rows outside [mk, nt) read a row in the ring and are
+  // not staged
+  auto load_ring_keys = [&](int p) {
+    const int nt = (pe - p) < kTT ? (pe - p) : kTT;
+    const int mk = count(p, khist);
+    Rows8 kr;
+#pragma unroll
+    for (int jm = 0; jm < 2; ++jm) {
+      const int pi = 16 * jm + n;
+      const int pc = pi < mk ? mk : (pi < nt ? pi : nt - 1);
+      const int rl = ring_lane(kfirst + (p + pc - khist), ring_len);
+      const uint32_t off = static_cast<uint32_t>((rl * kvh * D + 8 * kg) * 2);
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        kr.r[4 * jm + s4] = *reinterpret_cast<const w4*>(rk_base + off + 64 * s4);
+    }
+    return kr;
+  };
+  // ring value rows: slot k holds row (lane / 16) + 4k, chunk lane % 16
+  auto load_ring_values = [&](int p) {
+    const int nt = (pe - p) < kTT ? (pe - p) : kTT;
+    const int mv = count(p, vhist);
+    Rows8 vr;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int pi = kg + 4 * k;
+      const int pc = pi < mv ? mv : (pi < nt ? pi : nt - 1);
+      const int rl = ring_lane(vfirst + (p + pc - vhist), ring_len);
+      vr.r[k] = *reinterpret_cast<const w4*>(rv_base + static_cast<uint32_t>((rl * kvh * D + 8 * n) * 2));
+    }
+    return vr;
+  };
+
   float m_run = -INFINITY;
   float l_run = 0.0f;
   f4 o_acc[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) o_acc[q] = f4{0.f, 0.f, 0.f, 0.f};
 
-  for (int p0 = pb + kTT * half; p0 < pe; p0 += kTT * nhalf) {
+  const int step = kTT * nhalf;
+  const int p_first = pb + kTT * half;
+  KeyWords kw;
+  Rows8 vr;
+  int32_t pg_cur = load_pages(p_first);
+  if (p_first < pe) {  // uniform
+    load_key_words(p_first, pg_cur, kw);
+    vr = load_ring_values(p_first);
+  }
+  int32_t pg_next = load_pages(p_first + step);
+
+  // PV operand reads: lane s of a 16-lane group addresses value row base + s / 4,
+  // dims 16q + 4 (s % 4) .. + 3, so that lane n receives V[base + k][16q + n]
+  const int tr_row = n >> 2;
+  const int tr_chunk = (n & 3) >> 1;
+  const int tr_half = 8 * (n & 1);
+
+  for (int p0 = p_first; p0 < pe; p0 += step) {
     const int nt = (pe - p0) < kTT ? (pe - p0) : kTT;
-    const int mk = khist - p0 < 0 ? 0 : (khist - p0 < nt ? khist - p0 : nt);  // int4 keys
+    const int mk = count(p0, khist);
+    const int mv = count(p0, vhist);
+    const int p1 = p0 + step;
+    // the ring key rows, in flight while the int4 keys are staged
+    const Rows8 kr = load_ring_keys(p0);
     // one wave: its LDS accesses take effect in program order, so the previous
     // sub-tile's reads are done before these writes
-    // ---- K rows -------------------------------------------------------------
-    {
-      if (mk > 0) {
-        // lane: dims 2*lane and 2*lane + 1, the <= kKW words of each covering
-        // positions [p0, p0+mk); the two dims of a token go out as one pair
-        const int first = p0 & ~7;
-        const int c0 = 2 * lane;
-        uint32_t w[2][kKW];
-        float sc[2][kKW], mn[2][kKW];
+    // ---- key rows: int4 rows [0, mk) as hi and lo parts, ring rows [mk, nt)
+    // as they are (their lo parts zero, read only when the sub-tile has int4 rows)
+    if (mk > 0) {
+      const int first = p0 & ~7;
+      const int ga = p0 >> gsh;
 #pragma unroll
-        for (int k = 0; k < kKW; ++k) {
-          // clamped into [p0, p0 + mk): every load is valid and unconditional
-          const int p = first + 8 * k;
-          const int pp = p < p0 ? p0 : (p < p0 + mk ? p : p0 + mk - 1);
-          const int64_t r = (clamp_page(bt, pp, bsh, nb) * kvh + h) * D + c0;
-          const int off = pp & (bs - 1);
+      for (int k = 0; k < kKW; ++k) {
+        const int q = first + 8 * k;
+        const bool gb = ((q < p0 ? p0 : q) >> gsh) != ga;  // selects, not an index: registers
+        const float sc0 = gb ? kw.sc[0][1] : kw.sc[0][0], mn0 = gb ? kw.mn[0][1] : kw.mn[0][0];
+        const float sc1 = gb ? kw.sc[1][1] : kw.sc[1][0], mn1 = gb ? kw.mn[1][1] : kw.mn[1][0];
 #pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            w[e][k] = kq[(r + e) * wpd + (off >> 3)];
-            sc[e][k] = ks[(r + e) * gpb + (off >> gsh)];
-            mn[e][k] = km[(r + e) * gpb + (off >> gsh)];
-          }
-        }
-#pragma unroll
-        for (int k = 0; k < kKW; ++k) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int t = first + 8 * k + j - p0;
-            if (t >= 0 && t < mk) {
-              const float x0 = kivi_dequant((w[0][k] >> (4 * j)) & 0xfu, sc[0][k], mn[0][k]);
-              const float x1 = kivi_dequant((w[1][k] >> (4 * j)) & 0xfu, sc[1][k], mn[1][k]);
-              const uint32_t hi = pack2<T>(x0, x1);
-              *reinterpret_cast<uint32_t*>(sk + t * kKP + c0) = hi;
-              *reinterpret_cast<uint32_t*>(skl + t * kKP + c0) =
-                  pack2<T>(x0 - half_f32<T>(hi, 0), x1 - half_f32<T>(hi, 1));
-            }
+        for (int j = 0; j < 8; ++j) {
+          const int t = q + j - p0;
+          if (t >= 0 && t < mk) {
+            const float x0 = kivi_dequant((kw.w[0][k] >> (4 * j)) & 0xfu, sc0, mn0);
+            const float x1 = kivi_dequant((kw.w[1][k] >> (4 * j)) & 0xfu, sc1, mn1);
+            const uint32_t hi = pack2<T>(x0, x1);
+            *reinterpret_cast<uint32_t*>(sk + t * kKP + c0) = hi;
+            *reinterpret_cast<uint32_t*>(skl + t * kKP + c0) =
+                pack2<T>(x0 - half_f32<T>(hi, 0), x1 - half_f32<T>(hi, 1));
           }
         }
       }
-      // ring keys: task = (position, 16-byte chunk), copied as is; their lo
-      // parts are zero and only read when the sub-tile also holds int4 keys
-      const int tasks = (nt - mk) * (D / 8);
-      for (int t0 = 0; t0 < tasks; t0 += 64 * 4) {
-        uint4 x[4];
+    }
+    const bool ring0 = n >= mk && n < nt;            // row n is a ring key
+    const bool ring1 = 16 + n >= mk && 16 + n < nt;  // row 16 + n
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int t0k = t0 + 64 * k + lane;
-          const int t = t0k < tasks ? t0k : tasks - 1;  // clamped: unconditional load
-          const int pi = mk + t / (D / 8);
-          const int rl = ring_lane(kfirst + (p0 + pi - khist), ring_len);
-          x[k] = *reinterpret_cast<const uint4*>(ring_k + ((ring_row0 + rl) * kvh + h) * D +
-                                                 8 * (t % (D / 8)));
-        }
+    for (int i = 0; i < 8; ++i) {
+      const int o = (16 * (i >> 2) + n) * kKP + 32 * (i & 3) + 8 * kg;
+      if (i < 4 ? ring0 : ring1) *reinterpret_cast<w4*>(sk + o) = kr.r[i];
+    }
+    if (mk > 0) {  // uniform
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int t = t0 + 64 * k + lane;
-          if (t < tasks) {
-            const int pi = mk + t / (D / 8);
-            *reinterpret_cast<uint4*>(sk + pi * kKP + 8 * (t % (D / 8))) = x[k];
-            if (mk > 0)
-              *reinterpret_cast<uint4*>(skl + pi * kKP + 8 * (t % (D / 8))) = make_uint4(0, 0, 0, 0);
-          }
-        }
+      for (int i = 0; i < 8; ++i) {
+        const int o = (16 * (i >> 2) + n) * kKP + 32 * (i & 3) + 8 * kg;
+        if (i < 4 ? ring0 : ring1) *reinterpret_cast<w4*>(skl + o) = w4{0, 0, 0, 0};
       }
     }
     // ---- scores: S^T[token][head] for kTT/16 x 16 tokens ------------------------
@@ -296,15 +424,16 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
         }
       }
     }
+    if (p1 < pe) load_key_words(p1, pg_next, kw);  // uniform: the next sub-tile's int4 keys
     float tmax = -INFINITY;
 #pragma unroll
     for (int jm = 0; jm < kTT / 16; ++jm) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int pos = p0 + 16 * jm + 4 * kg + r;
-        const float sv = pos < pe ? sacc[jm][r] * qscale : -INFINITY;
-        sacc[jm][r] = sv;
-        tmax = fmaxf(tmax, sv);
+        const float sv_ = pos < pe ? sacc[jm][r] * qscale : -INFINITY;
+        sacc[jm][r] = sv_;
+        tmax = fmaxf(tmax, sv_);
       }
     }
     tmax = max_kg(tmax);
@@ -329,71 +458,33 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
       for (int q = 0; q < 8; ++q) o_acc[q][r] *= ar;
     }
 
-    // ---- V rows, stored transposed ----------------------------------------------
-    // lane task = (token pair, 8-dim word): both tokens' 8 values as T pairs
-    // (int4 words dequantized, ring rows as they are), then for every dim one
-    // 32-bit store of the two tokens, which are adjacent in the [dim][token] rows
-    {
-      const int mv = vhist - p0 < 0 ? 0 : (vhist - p0 < nt ? vhist - p0 : nt);  // int4 values
-      const int nd = D / 8;
-      const int tasks = ((nt + 1) / 2) * nd;
-      for (int t0 = 0; t0 < tasks; t0 += 64 * 2) {
-        uint4 x[2][2];
+    // ---- value rows into LDS (over the consumed key rows) -----------------------
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          const int t0k = t0 + 64 * k + lane;
-          const int t = t0k < tasks ? t0k : tasks - 1;  // clamped: unconditional loads
-          const int dv = t % nd;
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            int pi = 2 * (t / nd) + e;
-            pi = pi < nt ? pi : nt - 1;  // an odd sub-tile's last pair: zeroed below
-            if (pi < mv) {
-              const int p = p0 + pi;
-              const int64_t vrow =
-                  ((clamp_page(bt, p, bsh, nb) << bsh) + (p & (bs - 1))) * kvh + h;
-              const uint32_t w = vq[vrow * nd + dv];
-              const float sc = vs[vrow * (D >> gsh) + ((8 * dv) >> gsh)];
-              const float mn = vm[vrow * (D >> gsh) + ((8 * dv) >> gsh)];
-              uint32_t q[4];
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                q[i] = pack2<T>(kivi_dequant((w >> (8 * i)) & 0xfu, sc, mn),
-                                kivi_dequant((w >> (8 * i + 4)) & 0xfu, sc, mn));
-              x[k][e] = make_uint4(q[0], q[1], q[2], q[3]);
-            } else {
-              const int rl = ring_lane(vfirst + (p0 + pi - vhist), ring_len);
-              x[k][e] = *reinterpret_cast<const uint4*>(
-                  ring_v + ((ring_row0 + rl) * kvh + h) * D + 8 * dv);
-            }
-          }
-        }
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          const int t = t0 + 64 * k + lane;
-          if (t < tasks) {
-            const int pi0 = 2 * (t / nd);
-            const int dv = t % nd;
-            const bool past = pi0 + 1 >= nt;
-            const uint32_t a[4] = {x[k][0].x, x[k][0].y, x[k][0].z, x[k][0].w};
-            const uint32_t b[4] = {x[k][1].x, x[k][1].y, x[k][1].z, x[k][1].w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const uint32_t bb = past ? 0u : b[i];
-              // dim 8 dv + 2 i: the low halves; dim 8 dv + 2 i + 1: the high halves
-              *reinterpret_cast<uint32_t*>(svt + (8 * dv + 2 * i) * kVP + pi0) =
-                  __builtin_amdgcn_perm(bb, a[i], 0x05040100u);
-              *reinterpret_cast<uint32_t*>(svt + (8 * dv + 2 * i + 1) * kVP + pi0) =
-                  __builtin_amdgcn_perm(bb, a[i], 0x07060302u);
-            }
-          }
-        }
-      }
+    for (int k = 0; k < 8; ++k) {
+      const int pi = kg + 4 * k;
       // positions past the item: p = 0 there, and zero V keeps 0 * V exact
-      for (int e = lane; e < (kTT - nt) * D; e += 64) {
-        const int d = e / (kTT - nt);
-        const int pi = nt + e % (kTT - nt);
-        svt[d * kVP + pi] = 0;
+      const w4 x = pi < nt ? vr.r[k] : w4{0, 0, 0, 0};
+      *reinterpret_cast<w4*>(sv + pi * (2 * D) + 16 * (n ^ (2 * (pi & 3)))) = x;
+    }
+    if (mv > 0) {  // uniform: int4 values (rare), loaded and dequantized over their rows
+#pragma unroll 1
+      for (int k = 0; k < 8; ++k) {
+        const int pi = kg + 4 * k;
+        const int64_t blk = page_of(pg_cur, p0, p0 + (pi < mv ? pi : 0));
+        if (pi < mv) {
+          const int p = p0 + pi;
+          const int64_t vrow = ((blk << bsh) + (p & (bs - 1))) * kvh + h;
+          const uint32_t w = vq[vrow * (D / 8) + n];
+          const float sc = vs[vrow * (D >> gsh) + ((8 * n) >> gsh)];
+          const float mn = vm[vrow * (D >> gsh) + ((8 * n) >> gsh)];
+          uint32_t q[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            q[i] = pack2<T>(kivi_dequant((w >> (8 * i)) & 0xfu, sc, mn),
+                            kivi_dequant((w >> (8 * i + 4)) & 0xfu, sc, mn));
+          *reinterpret_cast<w4*>(sv + pi * (2 * D) + 16 * (n ^ (2 * (pi & 3)))) =
+              w4{q[0], q[1], q[2], q[3]};
+        }
       }
     }
 
@@ -410,14 +501,26 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
       }
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const uint16_t* vrow = svt + (16 * q + n) * kVP + 32 * st + 4 * kg;
-        const u4s v0 = *reinterpret_cast<const u4s*>(vrow);
-        const u4s v1 = *reinterpret_cast<const u4s*>(vrow + 16);
-        const u8v bv = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        v4s part[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int r = 32 * st + 16 * hh + 4 * kg + tr_row;
+          const int pos = (2 * q + tr_chunk) ^ (2 * tr_row);
+          part[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_v4s_ptr)(sv + r * (2 * D) + 16 * pos + tr_half));
+        }
+        const u8v bv = {static_cast<uint16_t>(part[0][0]), static_cast<uint16_t>(part[0][1]),
+                        static_cast<uint16_t>(part[0][2]), static_cast<uint16_t>(part[0][3]),
+                        static_cast<uint16_t>(part[1][0]), static_cast<uint16_t>(part[1][1]),
+                        static_cast<uint16_t>(part[1][2]), static_cast<uint16_t>(part[1][3])};
         o_acc[q] = mfma16(ahi, bv, o_acc[q], T{});
         o_acc[q] = mfma16(alo, bv, o_acc[q], T{});
       }
     }
+    // the next sub-tile's values, then the block-table rows of the one after
+    if (p1 < pe) vr = load_ring_values(p1);
+    pg_cur = pg_next;
+    pg_next = load_pages(p1 + step);
   }
 
   Partial res;

@@ -24,8 +24,11 @@ DEFAULT_SPLIT_TOKENS = 1024
 TAIL_ITEM_TOKENS = 64
 #: decode waves resident per CU (the MFMA kernel's LDS and register budget)
 WAVES_PER_CU = 8
-#: cost of one residual-window (tail) position against one int4 position
-TAIL_POSITION_COST = 8.0
+#: cost of one residual-window (tail) position against one int4 position:
+#: measured on config-3 decode, where 6 balances the pieces best (94.9 us,
+#: against 97.3 at 8 and 97.1 at 5); a tail position moves 3.5x the bytes
+#: of an int4 one and its item waits for memory about once per sub-tile
+TAIL_POSITION_COST = 6.0
 #: largest piece, in int4 positions: more work than one piece per wave slot
 #: of this size runs as several rounds of pieces, dispatched as slots free
 PIECE_MAX_COST = 4096.0
