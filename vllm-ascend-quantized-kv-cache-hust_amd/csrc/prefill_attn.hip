@@ -471,19 +471,18 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
 #pragma unroll
       for (int g2 = 0; g2 < NG; ++g2) {
         float sv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sv[i] = sacc[i / 4][g2][i % 4];
+        if (!full) {  // uniform: one branch, then a compare per score
+          // key kb + 16 kb2 + 4 kg + r is live when 16 kb2 + r <= rel
+          const int rel = (causal ? min(lk - 1, my_pos[g2]) : lk - 1) - kb - 4 * kg;
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            sv[i] = 16 * (i / 4) + i % 4 <= rel ? sv[i] : -INFINITY;
+        }
         float tmax = -INFINITY;
 #pragma unroll
-        for (int kb2 = 0; kb2 < 4; ++kb2)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float x = sacc[kb2][g2][r];
-            if (!full) {
-              const int pos = kb + 16 * kb2 + 4 * kg + r;
-              x = (pos < lk && (!causal || pos <= my_pos[g2])) ? x : -INFINITY;
-            }
-            sv[4 * kb2 + r] = x;
-            tmax = fmaxf(tmax, x);
-          }
+        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sv[i]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
         // lazy offset: the row's exponent offset moves only when its max grows
