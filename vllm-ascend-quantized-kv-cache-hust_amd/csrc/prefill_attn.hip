@@ -253,7 +253,10 @@ prefill_attn_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
 //   V  [64][D]    written by global_load_lds too, row-major; 16-byte column
 //                 c of row r stored at c ^ 2*(r % 4), so that the four rows
 //                 one transposing read covers sit in different banks.
-// While block i is computed, block i+1's K and V are in flight (DMA).
+// Keys run one block ahead of values: the step of block i computes block i's
+// softmax and PV and block i+1's scores, whose MFMAs interleave with block
+// i's exponentials (independent work, one basic block); block i+2's keys and
+// block i+1's values are in flight (DMA) meanwhile.
 //   S^T = K * Q^T: A = 16 keys x 32 dims (one 16-byte read per lane), B = the
 //                  wave's Q^T (registers), each A feeding both column groups.
 //   O^T += V^T * P^T: B = P^T straight from the S^T registers (the lane's
@@ -392,10 +395,6 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
       }
     }
   };
-  auto issue_kv = [&](char* buf, int kb) {
-    issue_rows(kbase, koff, buf, kb);
-    issue_rows(vbase, voff, buf + L::K_BYTES, kb);
-  };
   // PV operand reads: lane s of a 16-lane group addresses V row keybase + s / 4,
   // dims 16j + 4 (s % 4) .. + 3 (swizzled 16-byte column), so that lane n of
   // the group receives V[keybase + k][16j + n], k = 0..3
@@ -421,68 +420,86 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   const uint16_t one = op_bits(1.0f, O{});
   const u8v ones = u8v{one, one, one, one, one, one, one, one};
 
-  // prologue: block 0
-  issue_kv(lds, 0);
-  wait_vmcnt<0>();  // K and V landed in LDS
-  __syncthreads();
+  // LDS: two key buffers and two value buffers.  Keys run one block ahead of
+  // values: step i computes block i's softmax and PV and block i + 1's scores
+  // (the score MFMAs interleaved with the softmax's exponentials, which do not
+  // depend on them), while block i + 2's keys and block i + 1's values arrive.
+  char* const kbuf0 = lds;
+  char* const kbuf1 = lds + L::K_BYTES;
+  char* const vbuf0 = lds + 2 * L::K_BYTES;
+  char* const vbuf1 = lds + 2 * L::K_BYTES + L::V_BYTES;
+  // waves whose rows all precede block i under the causal mask skip it (and
+  // every later block)
+  auto active = [&](int i) {
+    return wrow0 <= wave_last && !(causal && i * kFaBlock > wave_last_pos);
+  };
+  // the K operands of 16-key group kb2 of the block at `sk`
+  auto k_reads = [&](const uint16_t* sk, int kb2, u8v (&a)[KS]) {
+    const int r = 16 * kb2 + n;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int piece = (4 * s + kg) ^ (r % PPR);
+      a[s] = *reinterpret_cast<const u8v*>(sk + r * D + 8 * piece);
+    }
+  };
+  auto k_mfmas = [&](const u8v (&a)[KS], f4 (&acc)[NG]) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int g2 = 0; g2 < NG; ++g2) acc[g2] = mfma16(a[s], qop[g2][s], acc[g2], O{});
+  };
 
-  // One block step: staging of block i + 1 into `nxt` and compute of block i
-  // from `cur`.  The two buffers are __restrict__ within the step, so the
-  // compiler's wait-count pass knows the LDS reads of `cur` cannot alias the
-  // DMA in flight into `nxt` (otherwise it waits for that DMA before the
-  // first read and the double buffer never overlaps).
-  auto step = [&](const char* __restrict__ cur, char* __restrict__ nxt, int i) {
+  // prologue: keys of blocks 0 and 1, values of block 0; scores of block 0
+  issue_rows(kbase, koff, kbuf0, 0);
+  if (nblk > 1) issue_rows(kbase, koff, kbuf1, kFaBlock);
+  issue_rows(vbase, voff, vbuf0, 0);
+  wait_vmcnt<0>();  // landed in LDS
+  __syncthreads();
+  f4 sacc[4][NG];
+#pragma unroll
+  for (int kb2 = 0; kb2 < 4; ++kb2)
+#pragma unroll
+    for (int g2 = 0; g2 < NG; ++g2) sacc[kb2][g2] = f4{0.f, 0.f, 0.f, 0.f};
+  if (active(0)) {
+#pragma unroll
+    for (int kb2 = 0; kb2 < 4; ++kb2) {
+      u8v a[KS];
+      k_reads(reinterpret_cast<const uint16_t*>(kbuf0), kb2, a);
+      k_mfmas(a, sacc[kb2]);
+    }
+  }
+  __syncthreads();  // block 0's keys are read before block 2's overwrite them
+
+  // One block step.  The four buffers are __restrict__ within the step, so
+  // the compiler's wait-count pass knows that the LDS reads of `kn` (block
+  // i + 1's keys) and `vc` (block i's values) cannot alias the DMA in flight
+  // into `kd` and `vd` (otherwise it waits for that DMA before the first read).
+  auto step = [&](const char* __restrict__ kn, const char* __restrict__ vc,
+                  char* __restrict__ kd, char* __restrict__ vd, int i) {
     const int kb = i * kFaBlock;
-    const bool more = i + 1 < nblk;
-    if (more) issue_kv(nxt, kb + kFaBlock);
-    // waves whose rows all precede this block under the causal mask skip it
-    if (wrow0 <= wave_last && !(causal && kb > wave_last_pos)) {
-      const uint16_t* sk = reinterpret_cast<const uint16_t*>(cur);
-      const char* sv_base = cur + L::K_BYTES;
-      // ---- S^T = K * Q^T ----
-      f4 sacc[4][NG];
-#pragma unroll
-      for (int kb2 = 0; kb2 < 4; ++kb2)
-#pragma unroll
-        for (int g2 = 0; g2 < NG; ++g2) sacc[kb2][g2] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb2 = 0; kb2 < 4; ++kb2) {
-        // all k-steps' K operands of this 16-key block first, then the MFMAs:
-        // the LDS reads overlap instead of each waiting for the one before
-        const int r = 16 * kb2 + n;
-        u8v a[KS];
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const int piece = (4 * s + kg) ^ (r % PPR);
-          a[s] = *reinterpret_cast<const u8v*>(sk + r * D + 8 * piece);
-        }
-        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-#pragma unroll
-          for (int g2 = 0; g2 < NG; ++g2)
-            sacc[kb2][g2] = mfma16(a[s], qop[g2][s], sacc[kb2][g2], O{});
-      }
-      // ---- online softmax per query column ----
+    if (i + 2 < nblk) issue_rows(kbase, koff, kd, kb + 2 * kFaBlock);
+    if (i + 1 < nblk) issue_rows(vbase, voff, vd, kb + kFaBlock);
+    if (active(i)) {
+      // ---- online softmax of block i per query column ----
       // the max runs over raw scores (qscale > 0), the exponent is one fma:
       // p = 2^(qscale * s - qscale * m)
       const bool full = kb + kFaBlock <= lk && (!causal || kb + kFaBlock - 1 <= lk - lq + wrow0);
-      u8v pop[NG][2];  // [g2][ks]
+      if (!full) {  // uniform: one branch, then a compare per score
 #pragma unroll
-      for (int g2 = 0; g2 < NG; ++g2) {
-        float sv[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sv[i] = sacc[i / 4][g2][i % 4];
-        if (!full) {  // uniform: one branch, then a compare per score
+        for (int g2 = 0; g2 < NG; ++g2) {
           // key kb + 16 kb2 + 4 kg + r is live when 16 kb2 + r <= rel
           const int rel = (causal ? min(lk - 1, my_pos[g2]) : lk - 1) - kb - 4 * kg;
 #pragma unroll
-          for (int i = 0; i < 16; ++i)
-            sv[i] = 16 * (i / 4) + i % 4 <= rel ? sv[i] : -INFINITY;
+          for (int e = 0; e < 16; ++e)
+            sacc[e / 4][g2][e % 4] = 16 * (e / 4) + e % 4 <= rel ? sacc[e / 4][g2][e % 4] : -INFINITY;
         }
+      }
+      float m_off[NG], alpha[NG];
+#pragma unroll
+      for (int g2 = 0; g2 < NG; ++g2) {
         float tmax = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sv[i]);
+        for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sacc[e / 4][g2][e % 4]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
         // lazy offset: the row's exponent offset moves only when its max grows
@@ -491,39 +508,71 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
         // same softmax whatever offset the row settled on
         const bool grow = tmax > m_run[g2] + lazy_thr;  // raw-score units
         const float m_new = grow ? tmax : m_run[g2];
-        const float m_off = m_new == -INFINITY ? 0.0f : -qscale * m_new;
-        const float alpha =
-            !grow ? 1.0f
-                  : (m_run[g2] == -INFINITY
-                         ? 0.0f
-                         : __builtin_amdgcn_exp2f(__builtin_fmaf(qscale, m_run[g2], m_off)));
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          uint32_t w[4];
-#pragma unroll
-          for (int h = 0; h < 4; ++h) {
-            const int i0 = 2 * h, i1 = 2 * h + 1;
-            const float p0 = __builtin_amdgcn_exp2f(
-                __builtin_fmaf(qscale, sv[4 * (2 * ks + i0 / 4) + (i0 % 4)], m_off));
-            const float p1 = __builtin_amdgcn_exp2f(
-                __builtin_fmaf(qscale, sv[4 * (2 * ks + i1 / 4) + (i1 % 4)], m_off));
-            w[h] = pack_op2(p0, p1, O{});
-          }
-          pop[g2][ks] = __builtin_bit_cast(u8v, make_uint4(w[0], w[1], w[2], w[3]));
-        }
+        m_off[g2] = m_new == -INFINITY ? 0.0f : -qscale * m_new;
+        alpha[g2] = !grow ? 1.0f
+                          : (m_run[g2] == -INFINITY
+                                 ? 0.0f
+                                 : __builtin_amdgcn_exp2f(__builtin_fmaf(qscale, m_run[g2], m_off[g2])));
         m_run[g2] = m_new;
-        if (__any(alpha != 1.0f)) {
-          l_acc[g2] *= alpha;
+      }
+      bool rescale = false;
 #pragma unroll
-          for (int j = 0; j < DB; ++j) o[j][g2] *= alpha;
+      for (int g2 = 0; g2 < NG; ++g2) rescale = rescale || alpha[g2] != 1.0f;
+      if (__any(rescale)) {
+#pragma unroll
+        for (int g2 = 0; g2 < NG; ++g2) {
+          l_acc[g2] *= alpha[g2];
+#pragma unroll
+          for (int j = 0; j < DB; ++j) o[j][g2] *= alpha[g2];
         }
       }
+      // raised wave priority from here to the end of the PV MFMAs: the SIMD's
+      // arbiter then issues this wave's MFMAs first and fills their cycles
+      // with the other wave's row maxima, which pulls the two waves into
+      // alternating phases (+1-3% on config-4 attention)
+      __builtin_amdgcn_s_setprio(1);
+      // ---- P of block i, with block i + 1's score MFMAs in between ----------
+      // 16-key group c: its exponentials (pop[g2][c / 2], half c % 2) beside
+      // the score MFMAs of the next block's group c
+      // (the last step computes scores of stale keys it never uses: one
+      // branch-free block keeps the MFMAs and the exponentials interleavable)
+      f4 snext[4][NG];
+#pragma unroll
+      for (int kb2 = 0; kb2 < 4; ++kb2)
+#pragma unroll
+        for (int g2 = 0; g2 < NG; ++g2) snext[kb2][g2] = f4{0.f, 0.f, 0.f, 0.f};
+      uint32_t pw[NG][2][4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        u8v a[KS];
+        k_reads(reinterpret_cast<const uint16_t*>(kn), c, a);
+#pragma unroll
+        for (int g2 = 0; g2 < NG; ++g2)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(qscale, sacc[c][g2][2 * h], m_off[g2]));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(qscale, sacc[c][g2][2 * h + 1], m_off[g2]));
+            pw[g2][c / 2][2 * (c % 2) + h] = pack_op2(p0, p1, O{});
+          }
+        k_mfmas(a, snext[c]);
+      }
+      u8v pop[NG][2];  // [g2][ks]
+#pragma unroll
+      for (int g2 = 0; g2 < NG; ++g2)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          pop[g2][ks] = __builtin_bit_cast(u8v, make_uint4(pw[g2][ks][0], pw[g2][ks][1],
+                                                           pw[g2][ks][2], pw[g2][ks][3]));
       // ---- O^T += V^T * P^T ----
+      const char* sv_base = vc;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        u8v a[DB];  // every dim block's V^T operand of this k-step, then the MFMAs
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int j = 0; j < DB; ++j) {
+      for (int jh = 0; jh < 2; ++jh) {
+        u8v a[DB / 2];  // half the dim blocks' V^T operands of this k-step, then the MFMAs
+#pragma unroll
+        for (int jj = 0; jj < DB / 2; ++jj) {
+          const int j = jh * (DB / 2) + jj;
           v4s part[2];
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
@@ -533,24 +582,33 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
             part[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (lds_v4s_ptr)(sv_base + r * (2 * D) + 16 * pos + tr_half));
           }
-          a[j] = u8v{static_cast<uint16_t>(part[0][0]), static_cast<uint16_t>(part[0][1]),
-                     static_cast<uint16_t>(part[0][2]), static_cast<uint16_t>(part[0][3]),
-                     static_cast<uint16_t>(part[1][0]), static_cast<uint16_t>(part[1][1]),
-                     static_cast<uint16_t>(part[1][2]), static_cast<uint16_t>(part[1][3])};
+          a[jj] = u8v{static_cast<uint16_t>(part[0][0]), static_cast<uint16_t>(part[0][1]),
+                      static_cast<uint16_t>(part[0][2]), static_cast<uint16_t>(part[0][3]),
+                      static_cast<uint16_t>(part[1][0]), static_cast<uint16_t>(part[1][1]),
+                      static_cast<uint16_t>(part[1][2]), static_cast<uint16_t>(part[1][3])};
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
-        for (int j = 0; j < DB; ++j)
+        for (int jj = 0; jj < DB / 2; ++jj)
 #pragma unroll
-          for (int g2 = 0; g2 < NG; ++g2) o[j][g2] = mfma16(a[j], pop[g2][ks], o[j][g2], O{});
+          for (int g2 = 0; g2 < NG; ++g2)
+            o[jh * (DB / 2) + jj][g2] = mfma16(a[jj], pop[g2][ks], o[jh * (DB / 2) + jj][g2], O{});
+        if (jh == 1) {
 #pragma unroll
-        for (int g2 = 0; g2 < NG; ++g2) l_acc[g2] = mfma16(ones, pop[g2][ks], l_acc[g2], O{});
+          for (int g2 = 0; g2 < NG; ++g2) l_acc[g2] = mfma16(ones, pop[g2][ks], l_acc[g2], O{});
+        }
       }
+      __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+      for (int kb2 = 0; kb2 < 4; ++kb2)
+#pragma unroll
+        for (int g2 = 0; g2 < NG; ++g2) sacc[kb2][g2] = snext[kb2][g2];
     }
-    if (more) wait_vmcnt<0>();  // next K and V landed in LDS
+    if (i + 1 < nblk) wait_vmcnt<0>();  // block i + 2's keys and i + 1's values landed
   };
   for (int i = 0; i < nblk; ++i) {
-    step(lds + (i & 1) * L::BUF, lds + ((i + 1) & 1) * L::BUF, i);
+    const int odd = i & 1;
+    step(odd ? kbuf0 : kbuf1, odd ? vbuf1 : vbuf0, odd ? kbuf1 : kbuf0, odd ? vbuf0 : vbuf1, i);
     __syncthreads();
   }
 
