@@ -372,25 +372,28 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
     // ---- key rows: int4 rows [0, mk) as hi and lo parts, ring rows [mk, nt)
     // as they are (their lo parts zero, read only when the sub-tile has int4 rows)
     if (mk > 0) {
-      const int first = p0 & ~7;
-      const int ga = p0 >> gsh;
+      // words realigned to the sub-tile (word k: positions p0 + 8k .. + 7), so
+      // that row t = 8k + j is nibble j of word k and no row needs a test:
+      // rows past mk are overwritten by the ring rows below or masked
+      const int sh = 4 * (p0 & 7);
+      // rows from tb on fall in the next key group (g >= 32: at most one boundary)
+      const int tb = (((p0 >> gsh) + 1) << gsh) - p0;
 #pragma unroll
-      for (int k = 0; k < kKW; ++k) {
-        const int q = first + 8 * k;
-        const bool gb = ((q < p0 ? p0 : q) >> gsh) != ga;  // selects, not an index: registers
-        const float sc0 = gb ? kw.sc[0][1] : kw.sc[0][0], mn0 = gb ? kw.mn[0][1] : kw.mn[0][0];
-        const float sc1 = gb ? kw.sc[1][1] : kw.sc[1][0], mn1 = gb ? kw.mn[1][1] : kw.mn[1][0];
+      for (int k = 0; k < kTT / 8; ++k) {
+        const uint32_t a0 = __builtin_amdgcn_alignbit(kw.w[0][k + 1], kw.w[0][k], sh);
+        const uint32_t a1 = __builtin_amdgcn_alignbit(kw.w[1][k + 1], kw.w[1][k], sh);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int t = q + j - p0;
-          if (t >= 0 && t < mk) {
-            const float x0 = kivi_dequant((kw.w[0][k] >> (4 * j)) & 0xfu, sc0, mn0);
-            const float x1 = kivi_dequant((kw.w[1][k] >> (4 * j)) & 0xfu, sc1, mn1);
-            const uint32_t hi = pack2<T>(x0, x1);
-            *reinterpret_cast<uint32_t*>(sk + t * kKP + c0) = hi;
-            *reinterpret_cast<uint32_t*>(skl + t * kKP + c0) =
-                pack2<T>(x0 - half_f32<T>(hi, 0), x1 - half_f32<T>(hi, 1));
-          }
+          const int t = 8 * k + j;
+          const bool gb = t >= tb;  // selects, not an index: registers
+          const float x0 = kivi_dequant((a0 >> (4 * j)) & 0xfu, gb ? kw.sc[0][1] : kw.sc[0][0],
+                                        gb ? kw.mn[0][1] : kw.mn[0][0]);
+          const float x1 = kivi_dequant((a1 >> (4 * j)) & 0xfu, gb ? kw.sc[1][1] : kw.sc[1][0],
+                                        gb ? kw.mn[1][1] : kw.mn[1][0]);
+          const uint32_t hi = pack2<T>(x0, x1);
+          *reinterpret_cast<uint32_t*>(sk + t * kKP + c0) = hi;
+          *reinterpret_cast<uint32_t*>(skl + t * kKP + c0) =
+              pack2<T>(x0 - half_f32<T>(hi, 0), x1 - half_f32<T>(hi, 1));
         }
       }
     }
