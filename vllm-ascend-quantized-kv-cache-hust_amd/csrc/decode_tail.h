@@ -29,6 +29,8 @@
 #include "kvq_common.h"
 #include "kvq_decode.h"
 
+#include <type_traits>
+
 namespace kvq {
 namespace tail {
 
@@ -361,9 +363,10 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
   const int tr_half = 8 * (n & 1);
 
   for (int p0 = p_first; p0 < pe; p0 += step) {
-    const int nt = (pe - p0) < kTT ? (pe - p0) : kTT;
-    const int mk = count(p0, khist);
-    const int mv = count(p0, vhist);
+    // wave-uniform (scalar registers: the branches on them are scalar branches)
+    const int nt = __builtin_amdgcn_readfirstlane((pe - p0) < kTT ? (pe - p0) : kTT);
+    const int mk = __builtin_amdgcn_readfirstlane(count(p0, khist));
+    const int mv = __builtin_amdgcn_readfirstlane(count(p0, vhist));
     const int p1 = p0 + step;
     // the ring key rows, in flight while the int4 keys are staged
     const Rows8 kr = load_ring_keys(p0);
@@ -413,20 +416,27 @@ __device__ __forceinline__ Partial tail_item(char* __restrict__ lds_raw, const T
     }
     // ---- scores: S^T[token][head] for kTT/16 x 16 tokens ------------------------
     f4 sacc[kTT / 16];
+    // the key lo parts exist only for int4 keys: one uniform branch for the block
+    auto scores = [&](auto with_lo) {
 #pragma unroll
-    for (int jm = 0; jm < kTT / 16; ++jm) {
-      sacc[jm] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int jm = 0; jm < kTT / 16; ++jm) {
+        sacc[jm] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const int o = (16 * jm + n) * kKP + 32 * s4 + 8 * kg;
-        const u8v a = *reinterpret_cast<const u8v*>(sk + o);
-        sacc[jm] = mfma16(a, qb[s4], sacc[jm], T{});
-        if (mk > 0) {  // uniform: key lo parts exist only for int4 keys
-          const u8v al = *reinterpret_cast<const u8v*>(skl + o);
-          sacc[jm] = mfma16(al, qb[s4], sacc[jm], T{});
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const int o = (16 * jm + n) * kKP + 32 * s4 + 8 * kg;
+          const u8v a = *reinterpret_cast<const u8v*>(sk + o);
+          sacc[jm] = mfma16(a, qb[s4], sacc[jm], T{});
+          if constexpr (decltype(with_lo)::value) {
+            const u8v al = *reinterpret_cast<const u8v*>(skl + o);
+            sacc[jm] = mfma16(al, qb[s4], sacc[jm], T{});
+          }
         }
       }
-    }
+    };
+    if (mk > 0)
+      scores(std::true_type{});
+    else
+      scores(std::false_type{});
     if (p1 < pe) load_key_words(p1, pg_next, kw);  // uniform: the next sub-tile's int4 keys
     float tmax = -INFINITY;
 #pragma unroll
