@@ -342,8 +342,18 @@ decode_combine_kernel(int hq, int d, const int32_t* __restrict__ seq_meta, int m
       // column 0) and never used
       pre[j][k] = rows[(j < nw ? j * stride : 0) + (c < d ? c : 0)];
     }
-  float mx = -INFINITY;
-  for (int s0 = 0; s0 < nw; s0 += 64) {
+  // (m, l) of the first 64 items in one 8-byte load per lane, kept for the
+  // weights below: one round trip to memory for the whole combine when the
+  // request has at most 64 items
+  float m0 = -INFINITY, l0 = 0.0f;
+  if (lane < nw) {
+    const float2 ml = *reinterpret_cast<const float2*>(
+        ws_ml + 2 * (static_cast<int64_t>(fw + lane) * hq + hh));
+    m0 = ml.x;
+    l0 = ml.y;
+  }
+  float mx = m0;
+  for (int s0 = 64; s0 < nw; s0 += 64) {
     const int s = s0 + lane;
     if (s < nw) mx = fmaxf(mx, ws_ml[2 * (static_cast<int64_t>(fw + s) * hq + hh)]);
   }
@@ -357,11 +367,15 @@ decode_combine_kernel(int hq, int d, const int32_t* __restrict__ seq_meta, int m
     const int s = s0 + lane;
     float wgt = 0.0f;
     if (s < nw) {
-      const int64_t idx = static_cast<int64_t>(fw + s) * hq + hh;
-      const float ms = ws_ml[2 * idx];
+      float ms = m0, ls = l0;
+      if (s0 > 0) {
+        const int64_t idx = static_cast<int64_t>(fw + s) * hq + hh;
+        ms = ws_ml[2 * idx];
+        ls = ws_ml[2 * idx + 1];
+      }
       if (ms != -INFINITY) {
         wgt = exp2f(ms - mx);
-        wsum += wgt * ws_ml[2 * idx + 1];
+        wsum += wgt * ls;
       }
     }
     const int cnt = nw - s0 < 64 ? nw - s0 : 64;
