@@ -697,7 +697,7 @@ def bench_int8_decode(torch, dev, *, reps=20, seed=0, layers=2):
         caches.append((kc, vc, k_aq, v_aq))
     q = torch.randn((b, hq, d), generator=gdev, device=dev).to(torch.bfloat16)
     lens = [n] * b
-    meta, work = plan_int8_work(lens, int8_split_tokens(sum(lens), kvh))
+    meta, work = plan_int8_work(lens, int8_split_tokens(sum(lens), kvh, seq_lens=lens))
     plan = (torch.from_numpy(meta).to(dev), torch.from_numpy(work).to(dev))
     out = torch.empty_like(q)
 

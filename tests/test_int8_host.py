@@ -208,3 +208,28 @@ def test_chunked_prefill_splits_decode_rows_and_history_aware_prompts(cpu_ops):
     assert cpu_ops["dense"][-1] == ([4], [4])
     want = ref.attention(q[1:5], k[1:5], v[1:5], [4], [4], D ** -0.5, True)
     torch.testing.assert_close(out[1:5].float(), want, atol=1e-2, rtol=1e-2)
+
+
+def test_int8_split_fills_one_round_of_workgroups():
+    """The INT8 decode split: one item per CU for up to 8 KV heads (config 2:
+    64 x 4096 tokens -> 1024-position items, 256 of them), more waves per CU
+    with more heads, and per-request cuts that never overflow one round."""
+    from vllm_ascend_quantized_kv_cache.ops.int8_ops import int8_split_tokens
+
+    assert int8_split_tokens(64 * 4096, 8, seq_lens=[4096] * 64) == 1024
+    assert int8_split_tokens(64 * 4096, 8) == 1024
+    assert int8_split_tokens(64 * 4096, 16) == 4096  # one wave per head: 4 per CU
+    gen = torch.Generator().manual_seed(3)
+    for trial in range(200):
+        b = int(torch.randint(1, 300, (1,), generator=gen))
+        lens = torch.randint(1, 20000, (b,), generator=gen).tolist()
+        kvh = [1, 2, 4, 8][trial % 4]
+        target = 256 * 8 // kvh
+        split = int8_split_tokens(sum(lens), kvh, seq_lens=lens)
+        assert split % 128 == 0 and 256 <= split <= 4096
+        items = sum(-(-n // split) for n in lens)
+        # within one round unless even 4096-position items cannot make it
+        assert items <= target or split == 4096
+        # and no longer than needed: one step down would overflow (or is the floor)
+        if split > max(256, -(-(-(-sum(lens) // target)) // 128) * 128):
+            assert sum(-(-n // (split - 128)) for n in lens) > target

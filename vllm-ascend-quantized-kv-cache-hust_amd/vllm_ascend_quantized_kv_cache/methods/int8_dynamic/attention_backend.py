@@ -197,7 +197,7 @@ class AscendInt8AttentionBackendMixin:
                 f"int8_decode_attention: a sequence length exceeds its block table "
                 f"({max(lens)} > {table.shape[1]} x {bs})"
             )
-        split = int8_split_tokens(sum(lens), self.num_kv_heads)
+        split = int8_split_tokens(sum(lens), self.num_kv_heads, seq_lens=lens)
         need = b + sum(-(-n // split) for n in lens)
         bufs = getattr(self, "_int8_step_bufs", None)
         if bufs is None or bufs.batch < b or bufs.work_cap < need:

@@ -138,7 +138,7 @@ class Int8DecodeGraph:
         if len(lens) != self.batch or max(lens) > self.max_len:
             raise RuntimeError("INT8 decode graph: the step does not fit the captured shape.")
         slots = impl._int8_host_slots(attn_metadata, len(lens))
-        split = int8_split_tokens(sum(lens), impl.num_kv_heads)
+        split = int8_split_tokens(sum(lens), impl.num_kv_heads, seq_lens=lens)
         self.num_work = self.bufs.stage(slots, lens, split, fixed=True)
         table = attn_metadata.block_tables[: self.batch]
         self.table[:, : table.shape[1]].copy_(table, non_blocking=True)

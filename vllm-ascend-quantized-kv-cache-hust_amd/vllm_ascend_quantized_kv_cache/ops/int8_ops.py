@@ -12,21 +12,34 @@ import torch
 
 from . import _native
 
-#: INT8 decode waves per CU the default plan aims at.  Its waves are long
-#: streams of 128-byte rows whose setup (Q' split, epilogue, one partial per
-#: item for the combine) costs as much as a few tiles: on config 2 (64 x 4096
-#: tokens, 8 KV heads) items of 2048 positions (4 waves per CU) decode in 112
-#: us against 119 us for 1024 (8 per CU), 130 us for 1536 and 169 us for 4096.
+#: INT8 decode waves per CU the default plan aims at.  Up to 8 KV heads, the
+#: kernel runs all heads of an item as one workgroup kept in step (one tile
+#: buffer pair per head, 8 x 16 KB of LDS: one such workgroup per CU), so the
+#: plan aims at one item per CU: on config 2 (64 x 4096 tokens, 8 KV heads)
+#: items of 1024 positions decode in 101 us against 130 us for 2048 (two
+#: rounds) and 246-288 us for 4096.  With more heads the kernel runs one wave
+#: per head, and 4 waves per CU were best (2048-position items: 112 us, against
+#: 119 us for 1024, 130 us for 1536 and 169 us for 4096).
 INT8_DECODE_WAVES_PER_CU = 4
+INT8_DECODE_WAVES_PER_CU_GROUPED = 8
 
 
-def int8_split_tokens(total_positions: int, num_kv_heads: int, cu_count: int = 256) -> int:
+def int8_split_tokens(total_positions: int, num_kv_heads: int, cu_count: int = 256,
+                      seq_lens=None) -> int:
     """Positions per INT8 decode item: about INT8_DECODE_WAVES_PER_CU waves
-    per CU, in [256, 4096], a multiple of 128."""
-    target_items = max(1, (cu_count * INT8_DECODE_WAVES_PER_CU) // max(1, num_kv_heads))
+    per CU (INT8_DECODE_WAVES_PER_CU_GROUPED for up to 8 KV heads, one
+    workgroup per item), in [256, 4096], a multiple of 128.  With ``seq_lens``
+    the split grows until the requests, each cut on its own, make no more
+    items than that: a partial second round of workgroups costs more than
+    longer items."""
+    waves = INT8_DECODE_WAVES_PER_CU_GROUPED if num_kv_heads <= 8 else INT8_DECODE_WAVES_PER_CU
+    target_items = max(1, (cu_count * waves) // max(1, num_kv_heads))
     per_item = -(-total_positions // target_items)
-    per_item = -(-per_item // 128) * 128
-    return int(min(4096, max(256, per_item)))
+    per_item = int(min(4096, max(256, -(-per_item // 128) * 128)))
+    if seq_lens is not None:
+        while per_item < 4096 and sum(-(-int(n) // per_item) for n in seq_lens) > target_items:
+            per_item += 128
+    return per_item
 
 
 def int8_calc_scales(key: torch.Tensor, value: torch.Tensor):
@@ -166,7 +179,7 @@ def int8_decode_attention(
         )
     if plan is None:
         if split_tokens is None:
-            split_tokens = int8_split_tokens(int(sum(seq_lens)), kvh)
+            split_tokens = int8_split_tokens(int(sum(seq_lens)), kvh, seq_lens=seq_lens)
         meta_np, work_np = plan_int8_work(seq_lens, split_tokens)
         meta = torch.from_numpy(meta_np).to(query.device)
         work = torch.from_numpy(work_np).to(query.device)
@@ -219,6 +232,7 @@ def int8_dequantize(x: torch.Tensor, inv: torch.Tensor, target_dtype) -> torch.T
 
 __all__ = [
     "INT8_DECODE_WAVES_PER_CU",
+    "INT8_DECODE_WAVES_PER_CU_GROUPED",
     "int8_calc_scales",
     "int8_decode_attention",
     "int8_dequant_gather",
