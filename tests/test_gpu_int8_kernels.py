@@ -93,7 +93,7 @@ def test_int8_dequant_gather_bit_exact(gpu_device, dtype):
 
 
 @pytest.mark.parametrize("rep", [1, 4, 8])
-@pytest.mark.parametrize("kvh,d,bs", [(2, 64, 16), (8, 128, 128), (4, 128, 32)])
+@pytest.mark.parametrize("kvh,d,bs", [(2, 64, 16), (8, 128, 128), (4, 128, 32), (16, 128, 64)])
 def test_int8_decode_matches_oracle(gpu_device, rep, kvh, d, bs):
     from vllm_ascend_quantized_kv_cache.ops.int8_ops import int8_decode_attention
 
