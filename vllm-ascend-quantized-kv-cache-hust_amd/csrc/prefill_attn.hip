@@ -251,8 +251,9 @@ prefill_attn_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
 //                 column of each row is XOR-swizzled by the row so that the
 //                 16 rows one score MFMA reads sit in different banks;
 //   V  [64][D]    written by global_load_lds too, row-major; 16-byte column
-//                 c of row r stored at c ^ 2*(r % 4), so that the four rows
-//                 one transposing read covers sit in different banks.
+//                 c of row r stored at c ^ (2*(r % 4) + 8*((r / 4) % 2)) (the
+//                 second term at D = 128), so that the rows the transposing
+//                 reads of one LDS cycle cover sit in different banks.
 // Keys run one block ahead of values: the step of block i computes block i's
 // softmax and PV and block i+1's scores, whose MFMAs interleave with block
 // i's exponentials (independent work, one basic block); block i+2's keys and
@@ -306,6 +307,11 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   constexpr int KINST = kFaBlock / RPI / kFaWaves;  // DMA instructions per wave per block
   static_assert(KINST >= 1 && kFaBlock % (RPI * kFaWaves) == 0, "K / V DMA split");
   static_assert(PPR >= 8, "V swizzle 2 * (r % 4) stays inside the row");
+  // V's 16-byte column c of row r sits at c ^ vswz(r): 2 (r % 4) spreads the
+  // four rows one transposing read covers over the banks, and with 16 columns
+  // a row (D = 128) 8 ((r / 4) % 2) also parts the rows 4 apart that the two
+  // 16-lane groups of one LDS cycle read
+  auto vswz = [](int r) { return 2 * (r % 4) + (PPR >= 16 ? 8 * ((r / 4) % 2) : 0); };
   extern __shared__ __align__(16) char lds[];
 
   // Workgroup ids go to the XCDs round-robin.  The rep * qblocks workgroups
@@ -376,7 +382,7 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
     const int r = inst * RPI + lane / PPR;  // block row of this lane
     krow[i] = r;
     koff[i] = static_cast<uint32_t>((r * row_stride + 8 * ((lane % PPR) ^ (r % PPR))) * 2);
-    voff[i] = static_cast<uint32_t>((r * row_stride + 8 * ((lane % PPR) ^ (2 * (r % 4)))) * 2);
+    voff[i] = static_cast<uint32_t>((r * row_stride + 8 * ((lane % PPR) ^ vswz(r))) * 2);
   }
   // DMA of block rows kb .. kb + 63 of `base` into `dst` with the lane
   // offsets `off`; in the last block rows past the end read the last row
@@ -578,7 +584,7 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
           for (int hh = 0; hh < 2; ++hh) {
             // keys 32 ks + 16 hh + 4 kg + k, k = 0..3
             const int r = 32 * ks + 16 * hh + 4 * kg + tr_row;
-            const int pos = (2 * j + tr_chunk) ^ (2 * (r % 4));
+            const int pos = (2 * j + tr_chunk) ^ vswz(r);
             part[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (lds_v4s_ptr)(sv_base + r * (2 * D) + 16 * pos + tr_half));
           }
