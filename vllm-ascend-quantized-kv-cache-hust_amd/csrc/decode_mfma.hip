@@ -899,6 +899,12 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, int hpw, 
     // tiles are GT-aligned and GT divides g: the wave's first tile, or one in
     // another key group than its previous tile, prepares the group's Q'
     if (new_group) prepare_group<TQ, CPG, FOLD, KSV>(W, n, kg, qv, qscale, qg);
+    // single-round piece plans: raised wave priority over the tile's compute,
+    // so a SIMD's arbiter finishes one wave's tile while the other's DMA is in
+    // flight (config 3: 94.4 -> 93.5 us; over the many rounds of a split plan
+    // it starves the waves that would issue the next DMA: config 5 2.58 ->
+    // 2.94 ms, so those keep the default)
+    if (pieces) __builtin_amdgcn_s_setprio(1);
     const WaveValues<CPG, VG1> vals(W, kg, n % CPG);
     if (p0 + GT <= pe)
       compute_tile<TQ, CPG, VG1, true, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run,
@@ -906,6 +912,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, int hpw, 
     else
       compute_tile<TQ, CPG, VG1, false, FOLD>(W, vals, p0, pe, n, kg, qg, qscale, ln, acc.m_run,
                                               acc.l_run, acc.o_acc, acc.c_acc, acc.bias_v);
+    if (pieces) __builtin_amdgcn_s_setprio(0);
   };
   if (p_first < pe) issue(my_lds, p_first, true);  // prologue: tile 0 into buffer 0
   int cur = 0;
