@@ -200,12 +200,14 @@ def test_decode_step_graph_replays_match_eager_twin_and_oracle(gpu_device):
         q_s.copy_(q)
         k_s.copy_(k)
         v_s.copy_(v)
-        gstep.prepare(md, k_s, v_s)
+        graphed.prepare_kivi_graph_replay(md, k_s, v_s)  # the host's per-replay hook
         if graph is None:
             torch.cuda.synchronize()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                gstep.launch(q_s, k_s, v_s, out_s)
+                # the host records forward() itself: under capture it routes
+                # the decode to the batch's capturable step
+                graphed.forward(None, q_s, k_s, v_s, None, md, out_s)
         graph.replay()
         out = torch.zeros_like(q_s)
         eager.forward(None, q, k, v, None, md, out)
@@ -215,3 +217,103 @@ def test_decode_step_graph_replays_match_eager_twin_and_oracle(gpu_device):
             _same_state(graphed, eager)
             case.oracle(graphed, j, out_s)
     assert graphed.kivi_host_reads == 0
+    assert graphed._kivi_capture_graphs == {case.b: gstep}
+
+
+def test_decode_graph_prepare_refuses_before_the_mirror_moves(gpu_device):
+    """Every check of ``KiviDecodeGraph.prepare`` that can refuse a step runs
+    before the window mirror moves: a batch other than the captured one, a
+    wider block table, or an activation dtype the planned store does not
+    cover.  The mirror (and so the device pages) stay as they were."""
+    case = _Case(gpu_device, b=4, steps=3, seed=6)
+    impl = case.build()
+    gstep = impl.kivi_decode_graph(case.b + 1, max_blocks=case.table.shape[1])
+    ring = impl._kivi_ring
+    before = ring.state()
+    md, q, k, v = case.step(0)
+    with pytest.raises(RuntimeError, match="captured for batch"):
+        gstep.prepare(md, k, v)
+    assert ring.state() == before
+    narrow = impl.kivi_decode_graph(case.b, max_blocks=case.table.shape[1] - 1)
+    with pytest.raises(RuntimeError, match="wider than captured"):
+        narrow.prepare(md, k, v)
+    assert ring.state() == before
+    with pytest.raises(RuntimeError, match="geometry or activation dtype"):
+        impl.kivi_decode_graph(case.b, max_blocks=case.table.shape[1]).prepare(
+            md, k.float(), v.float())
+    assert ring.state() == before and ring.dtype == torch.bfloat16
+    with pytest.raises(RuntimeError, match="prepare\\(\\) once before"):
+        gstep.launch(q, k, v, torch.zeros_like(q))
+
+
+def test_forward_under_real_capture_without_a_graph_is_refused(gpu_device):
+    """The capture check reads the stream's real capture status: forward()
+    inside ``torch.cuda.graph`` with no capturable step for the batch raises
+    before anything is recorded."""
+    case = _Case(gpu_device, b=3, steps=2, seed=7)
+    impl = case.build()
+    md, q, k, v = case.step(0)
+    before = impl._kivi_ring.state()
+    out = torch.zeros((case.b, case.hq, case.d), dtype=torch.bfloat16, device=gpu_device)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="graph capture"):
+        with torch.cuda.graph(graph):
+            impl.forward(None, q, k, v, None, md, out)
+    torch.cuda.synchronize()
+    assert impl._kivi_ring.state() == before
+    impl.forward(None, q, k, v, None, md, out)  # eager, outside the capture: runs
+    torch.cuda.synchronize()
+    case.oracle(impl, 0, out)
+
+
+@pytest.mark.parametrize("g", [128, 64])
+def test_host_kv_tensor_shape_runs_decode_against_oracle(gpu_device, g):
+    """The host allocates one ``(2, NB, Bs, KVH, S)`` uint8 tensor through
+    ``host_integration.kivi_int4_kv_cache_shape`` and hands ``(kv[0], kv[1])``
+    to every forward (as the patched runner slices it); prefill writes and
+    decode steps through ``forward`` leave pages and outputs that match the
+    oracle, and the K and V halves hold exactly the two byte regions."""
+    from vllm_ascend_quantized_kv_cache import host_integration as hi
+
+    case = _Case(gpu_device, b=4, steps=131, seed=8 + g)
+    shape = hi.kivi_int4_kv_cache_shape(case.nb, case.bs, case.kvh, case.d, g)
+    assert shape == (2, case.nb, case.bs, case.kvh, case.d // 2 + 8 * case.d // g)
+    kv = torch.zeros(shape, dtype=torch.uint8, device=gpu_device)
+    case.g = g
+
+    class Impl(ab.AscendKiviInt4AttentionBackendMixin):
+        pass
+
+    impl = Impl()
+    impl.num_heads, impl.num_kv_heads, impl.head_size = case.hq, case.kvh, case.d
+    impl.scale = case.d ** -0.5
+    impl._init_kivi_state("kivi_int4")
+    impl.kivi_group_size, impl.kivi_max_num_seqs = g, case.b
+    for i, n in enumerate(case.lens):  # prefill: all-new prompts
+        sl = torch.tensor([case.slot(i, p) for p in range(n)], device=gpu_device)
+        md = SimpleNamespace(attn_state=SimpleNamespace(name="PrefillNoCache"), causal=True,
+                             finished_req_ids=None, seq_lens_list=[n],
+                             actual_seq_lengths_q=[n], slot_mapping=sl,
+                             block_tables=case.table_dev[i:i + 1], req_ids=[case.reqs[i]],
+                             num_actual_tokens=n)
+        q = torch.randn(n, case.hq, case.d, device=gpu_device).to(torch.bfloat16)
+        impl.forward(None, q, case.keys[i][:n].to(gpu_device),
+                     case.values[i][:n].to(gpu_device), (kv[0], kv[1]), md,
+                     torch.zeros_like(q))
+    assert impl.k_quant_cache.untyped_storage().data_ptr() == kv.untyped_storage().data_ptr()
+    for j in range(131):  # a key window flushes for every request
+        md, q, k, v = case.step(j)
+        out = torch.zeros((case.b, case.hq, case.d), dtype=torch.bfloat16, device=gpu_device)
+        impl.forward(None, q, k, v, (kv[0], kv[1]), md, out)
+        if j in (0, 130):
+            torch.cuda.synchronize()
+            case.oracle(impl, j, out)
+    # the six views cover the two halves exactly: K views inside kv[0], V inside kv[1]
+    k0, k1 = kv[0].data_ptr(), kv[0].data_ptr() + kv[0].numel()
+    v0 = kv[1].data_ptr()
+    caches = impl._kivi_caches()
+    for t in caches[:3]:
+        assert k0 <= t.data_ptr() and t.data_ptr() + t.numel() * t.element_size() <= k1
+    for t in caches[3:]:
+        assert v0 <= t.data_ptr() < v0 + kv[1].numel()

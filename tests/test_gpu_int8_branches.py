@@ -251,12 +251,14 @@ def test_int8_decode_graph_replays_match_eager_twin_and_oracle(gpu_device):
         q_s.copy_(q)
         k_s.copy_(k)
         v_s.copy_(v)
-        gstep.prepare(md)
+        g.prepare_int8_graph_replay(md)  # the host's per-replay hook (gstep.prepare)
         if graph is None:
             torch.cuda.synchronize()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                gstep.launch(q_s, k_s, v_s, out_s)
+                # the host records forward() itself: under capture it routes
+                # the decode to the batch's capturable step
+                g.forward(lg, q_s, k_s, v_s, cg, md, out_s)
         graph.replay()
         out = torch.zeros_like(q_s)
         e.forward(le, q, k, v, ce, md, out)
@@ -266,3 +268,4 @@ def test_int8_decode_graph_replays_match_eager_twin_and_oracle(gpu_device):
         if j in (0, steps - 1):
             case.oracle(lg, cg, j, out_s)
     assert getattr(g, "int8_host_reads", 0) == 0
+    assert g._int8_capture_graphs == {len(case.reqs): gstep}

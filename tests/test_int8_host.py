@@ -233,3 +233,54 @@ def test_int8_split_fills_one_round_of_workgroups():
         # and no longer than needed: one step down would overflow (or is the floor)
         if split > max(256, -(-(-(-sum(lens) // target)) // 128) * 128):
             assert sum(-(-n // (split - 128)) for n in lens) > target
+
+
+def _capturing(monkeypatch):
+    from vllm_ascend_quantized_kv_cache.methods.int8_dynamic import attention_backend as i8ab
+
+    monkeypatch.setattr(i8ab, "stream_capturing", lambda: True)
+
+
+def test_forward_under_capture_without_graph_is_refused(cpu_ops, monkeypatch):
+    """A captured forward() would record one step's staged plan and replay it
+    forever; with no capturable step created for the batch it raises before
+    anything is written or launched (``i8ab.py:97-104`` routes capture to the
+    host's graph path instead)."""
+    impl = _Impl()
+    layer = _layer()
+    cache = _cache()
+    k, v = make_kv(2, KVH, D, dtype=torch.bfloat16, seed=3)
+    md = _md("DecodeOnly", seq_lens_list=[3, 5], block_tables=torch.tensor([[0], [1]]),
+             slot_mapping=torch.tensor([2, 12]), num_actual_tokens=2)
+    q = torch.randn(2, HQ, D).to(torch.bfloat16)
+    _capturing(monkeypatch)
+    for state in ("DecodeOnly", "ChunkedPrefill", "PrefillNoCache"):
+        md.attn_state = SimpleNamespace(name=state)
+        with pytest.raises(RuntimeError, match="graph capture"):
+            impl.forward(layer, q, k, v, cache, md, torch.zeros_like(q))
+    assert not cache.any() and not getattr(layer, "_int8_scales_ready", False)
+    assert cpu_ops == {"decode": [], "dense": [], "dequant": []}
+
+
+def test_forward_under_capture_routes_decode_to_the_batch_graph(cpu_ops, monkeypatch):
+    impl = _Impl()
+    launched = []
+
+    class _Graph:
+        def launch(self, query, key, value, output):
+            launched.append(query.shape[0])
+            return output
+
+    impl._int8_capture_graphs = {2: _Graph()}
+    md = _md("DecodeOnly", seq_lens_list=[3, 5], block_tables=torch.tensor([[0], [1]]))
+    q = torch.randn(2, HQ, D)
+    out = torch.zeros_like(q)
+    _capturing(monkeypatch)
+    assert impl.forward(_layer(), q, None, None, _cache(), md, out) is out
+    assert launched == [2]
+    md.seq_lens_list = [3, 5, 7]  # no capturable step for batch 3
+    with pytest.raises(RuntimeError, match="batch-3"):
+        impl.forward(_layer(), torch.randn(3, HQ, D), None, None, _cache(), md,
+                     torch.zeros(3, HQ, D))
+    with pytest.raises(RuntimeError, match="no capturable step for batch 3"):
+        impl.prepare_int8_graph_replay(md)

@@ -1127,3 +1127,60 @@ def test_native_step_check_matches_the_python_checks():
         else:
             seen["err"] += 1
     assert min(seen.values()) > 10, seen
+
+
+def test_forward_under_capture_is_refused_or_routed(monkeypatch):
+    """KIVI has no graph path in the reference (``--enforce-eager``,
+    ``docs/int4-host-integration.md:137-138``).  Under capture, forward()
+    records only a capturable decode step created for the batch, and refuses
+    anything else before the mirror or the caches change."""
+    impl = _make_impl()
+    monkeypatch.setattr(ab, "stream_capturing", lambda: True)
+    k = torch.randn(1, KVH, HEAD)
+    md = _metadata(1, attn_state=SimpleNamespace(name="DecodeOnly"), seq_lens_list=[5],
+                   slot_mapping=torch.tensor([4]))
+    q = torch.randn(1, KVH, HEAD)
+    state = impl._ensure_kivi_residual_buffers().state()
+    for name in ("DecodeOnly", "PrefillNoCache", "ChunkedPrefill"):
+        md.attn_state = SimpleNamespace(name=name)
+        with pytest.raises(RuntimeError, match="graph capture"):
+            impl.forward(None, q, k, k, None, md, torch.zeros_like(q))
+    assert impl._kivi_ring.state() == state and not impl.kivi_residual_req_to_row
+    assert all(not impl.calls[c] for c in impl.calls)
+
+    launched = []
+
+    class _Graph:
+        def launch(self, query, key, value, output):
+            launched.append(query.shape[0])
+            return output
+
+    impl._kivi_capture_graphs = {1: _Graph()}
+    md.attn_state = SimpleNamespace(name="DecodeOnly")
+    out = torch.zeros_like(q)
+    assert impl.forward(None, q, k, k, None, md, out) is out and launched == [1]
+
+
+def test_plan_decode_step_rolls_back_when_a_later_stage_raises():
+    """The decode step plans the whole batch on the mirror, then stages and
+    launches; an error after the planning (here: staging) must leave the
+    mirror exactly as it was, flushed key windows included."""
+    impl = _make_impl(residual=GROUP, max_seqs=3)
+    ring = impl._ensure_kivi_residual_buffers()
+    rows = np.asarray([impl._get_kivi_residual_row(k, create=True) for k in ("a", "b")])
+    bs = BLOCK
+    # row a: a full key window (one aligned group) in block 0; row b: two tokens
+    ring.load_row(int(rows[0]), is_key=True, slots=list(range(GROUP)))
+    ring.load_row(int(rows[0]), is_key=False, slots=list(range(GROUP)))
+    ring.load_row(int(rows[1]), is_key=True, slots=[bs, bs + 1])
+    ring.load_row(int(rows[1]), is_key=False, slots=[bs, bs + 1])
+    before = ring.state()
+    slots = np.asarray([GROUP, bs + 2])
+    with pytest.raises(RuntimeError, match="staging failed"):
+        with impl._kivi_planning():
+            jobs = ring.plan_decode_step(rows, slots, slots % bs, np.arange(2),
+                                         block_size=bs, group_size=GROUP)
+            assert jobs is not None and jobs.key_pack_src.size == GROUP
+            assert ring.state() != before
+            raise RuntimeError("staging failed")
+    assert ring.state() == before

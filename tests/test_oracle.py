@@ -248,6 +248,51 @@ def test_int8_quantize_bf16_matches_c_and_rounds_half_even():
     assert ref.int8_quantize(x, inv).tolist() == [2, -2, 127, -128]
 
 
+@pytest.mark.parametrize("bs,nb", [(16, 7), (128, 5)])
+def test_int8_reshape_and_cache_matches_per_slot_loop(bs, nb):
+    """The scatter half of ``int8_reshape_and_cache`` (the host
+    ``reshape_and_cache``, ``i8ab.py:86-88``), pinned by a per-slot loop.
+
+    The codes come from the independent C restatement (bf16 product, then
+    round half to even, then the clamp); the loop writes token ``i`` to page
+    ``s // Bs``, row ``s % Bs`` for every slot ``s >= 0`` and skips padding.
+    Slots cover a shuffled pool, the pool's last row and negative padding;
+    every byte the loop does not write must keep its sentinel, on both sides.
+    """
+    kvh, d = 2, 16
+    g = torch.Generator().manual_seed(21)
+    pool = torch.randperm(nb * bs, generator=g)[: nb * bs // 2].tolist()
+    slots = pool + [nb * bs - 1, -1, -7, 0]
+    slots = list(dict.fromkeys(slots))  # distinct live slots; padding may repeat
+    n = len(slots)
+    key, value = make_kv(n, kvh, d, dtype=torch.bfloat16, seed=22)
+    key[3] *= 400  # codes that clamp at both ends
+    key[4] *= -400
+    k_inv, v_inv, _, _ = ref.int8_calc_scales(key, value)
+    sentinel = 77
+    kc = torch.full((nb, bs, kvh, d), sentinel, dtype=torch.int8)
+    vc = torch.full_like(kc, sentinel)
+    ref.int8_reshape_and_cache(key, value, k_inv, v_inv, torch.tensor(slots), kc, vc)
+
+    want_k = torch.full_like(kc, sentinel)
+    want_v = torch.full_like(vc, sentinel)
+    codes_k = ck.c_int8_quant_bf16(key.float().reshape(n, -1).contiguous(),
+                                   k_inv.float().flatten().contiguous()).reshape(n, kvh, d)
+    codes_v = ck.c_int8_quant_bf16(value.float().reshape(n, -1).contiguous(),
+                                   v_inv.float().flatten().contiguous()).reshape(n, kvh, d)
+    assert codes_k.max() == 127 and codes_k.min() == -128
+    for i, s in enumerate(slots):
+        if s < 0:
+            continue
+        for h in range(kvh):
+            for c in range(d):
+                want_k[s // bs, s % bs, h, c] = codes_k[i, h, c]
+                want_v[s // bs, s % bs, h, c] = codes_v[i, h, c]
+    assert torch.equal(kc, want_k)
+    assert torch.equal(vc, want_v)
+    assert int((kc != sentinel).any(dim=(2, 3)).sum()) == len([s for s in slots if s >= 0])
+
+
 def test_int8_scales_closed_form_fp32():
     x = torch.tensor([[0.5, -4.0, 0.0], [-1.0, 2.0, 0.0]])
     k_inv, _, k_aq, _ = ref.int8_calc_scales(x, x)

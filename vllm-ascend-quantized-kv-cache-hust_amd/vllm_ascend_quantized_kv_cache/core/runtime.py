@@ -39,6 +39,20 @@ def gpu_available() -> bool:
         return False
 
 
+def stream_capturing() -> bool:
+    """True while the caller's current HIP stream is recording a graph.
+
+    Checked at the entry of each mixin's ``forward``: a step that stages a
+    one-step plan from host memory must not be recorded into a graph that
+    later replays it with other sequence lengths and slots.
+    """
+    try:
+        torch = importlib.import_module("torch")
+    except ImportError:
+        return False
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+
+
 def require_gpu(what: str) -> None:
     if not gpu_available():
         raise RuntimeError(
@@ -48,4 +62,5 @@ def require_gpu(what: str) -> None:
         )
 
 
-__all__ = ["gpu_available", "import_torch", "module_available", "require_gpu"]
+__all__ = ["gpu_available", "import_torch", "module_available", "require_gpu",
+           "stream_capturing"]

@@ -9,9 +9,12 @@ chunked prefill or prefill.  Here the quantize and the page write are one
 HIP kernel (the reference quantizes in torch and hands the codes to the
 host's ``reshape_and_cache``), decode is a fused HIP kernel with per-channel
 antiquant, and prefill over cached pages dequantizes to dense TND and runs
-the MFMA attention kernel.  Host-only features of the reference's branch
-table (pooling encoders, ACL graph capture) stay with the host and are
-refused here.
+the MFMA attention kernel.  Pooling encoders stay with the host and are
+refused here.  Under graph capture the reference hands the decode to the
+host's ``full_graph_fia`` (``i8ab.py:97-104``); here a captured ``forward``
+records the layer's capturable decode step (``int8_decode_graph``), whose
+plan the host stages before every replay (``prepare_int8_graph_replay``),
+and refuses every other capture.
 """
 
 from __future__ import annotations
@@ -20,6 +23,8 @@ from typing import Any
 
 import numpy as np
 import torch
+
+from ...core.runtime import stream_capturing
 
 
 def _state(attn_metadata: Any) -> str:
@@ -34,6 +39,8 @@ class AscendInt8AttentionBackendMixin:
 
     key_cache: Any = None
     value_cache: Any = None
+    #: capturable decode steps by batch size (``int8_decode_graph``)
+    _int8_capture_graphs: dict | None = None
 
     def forward(
         self,
@@ -58,6 +65,8 @@ class AscendInt8AttentionBackendMixin:
         assert getattr(layer, "_v_scale_float", 1.0) == 1.0
         if attn_metadata is None:
             return output.fill_(0)
+        if stream_capturing():
+            return self._forward_int8_captured(query, key, value, attn_metadata, output)
 
         if self.key_cache is None and kv_cache is not None:
             if (isinstance(kv_cache, torch.Tensor) and kv_cache.dim() > 0
@@ -105,6 +114,40 @@ class AscendInt8AttentionBackendMixin:
         return self._forward_int8_prefill(
             query, float_key, float_value, attn_metadata, output, layer
         )
+
+    def _forward_int8_captured(self, query: Any, key: Any, value: Any, attn_metadata: Any,
+                               output: Any) -> Any:
+        """``forward`` while the host records a HIP graph (``i8ab.py:97-104``).
+
+        The eager decode stages a one-step plan (slots, lengths, the split-K
+        work list) from host memory, and a recorded copy of it would replay
+        that one step forever.  Only the decode step of a batch whose
+        capturable form the host created beforehand (``int8_decode_graph``) is
+        recorded: its launches read a persistent plan buffer that
+        ``prepare_int8_graph_replay`` refills before each replay.  Prefill,
+        chunked prefill and uncalibrated layers are refused.
+        """
+        b = len(attn_metadata.seq_lens_list)
+        graph = self._int8_capture_graphs.get(b) if self._int8_capture_graphs else None
+        if _state(attn_metadata) != "DecodeOnly" or graph is None:
+            raise RuntimeError(
+                "INT8 forward() was called under HIP graph capture: its eager step stages a "
+                "one-step plan that every replay would reuse. Capture only decode steps, after "
+                f"creating the batch-{b} capturable step with "
+                "impl.int8_decode_graph(layer, batch, max_blocks=...), and call "
+                "impl.prepare_int8_graph_replay(attn_metadata) before every replay; or run the "
+                "layer eagerly."
+            )
+        return graph.launch(query, key, value, output)
+
+    def prepare_int8_graph_replay(self, attn_metadata: Any) -> None:
+        """Stage the plan of the step a captured ``forward`` will replay next
+        (the batch's ``Int8DecodeGraph.prepare``)."""
+        b = len(attn_metadata.seq_lens_list)
+        graph = self._int8_capture_graphs.get(b) if self._int8_capture_graphs else None
+        if graph is None:
+            raise RuntimeError(f"INT8 decode graph: no capturable step for batch {b}.")
+        graph.prepare(attn_metadata)
 
     # -- scales and quantize (i8ab.py:130-171) ------------------------------
 
@@ -221,7 +264,11 @@ class AscendInt8AttentionBackendMixin:
         and replayed every step after ``prepare`` stages that step's plan."""
         from .decode_step import Int8DecodeGraph
 
-        return Int8DecodeGraph(self, layer, batch, max_blocks=max_blocks)
+        graph = Int8DecodeGraph(self, layer, batch, max_blocks=max_blocks)
+        if self._int8_capture_graphs is None:
+            self._int8_capture_graphs = {}
+        self._int8_capture_graphs[batch] = graph  # what a captured forward() launches
+        return graph
 
     def _dense_attention(self, q: Any, k: Any, v: Any, q_lens: list[int], kv_lens: list[int],
                          causal: bool, out: Any) -> Any:

@@ -131,20 +131,33 @@ class Int8DecodeGraph:
                                     num_heads=impl.num_heads, head_size=impl.head_size)
         self.table = torch.zeros((batch, max_blocks), dtype=torch.int32, device=dev)
         self.num_work = work_cap
+        self.prepared = False
 
     def prepare(self, attn_metadata) -> None:
+        from ...core.runtime import stream_capturing
+
         impl = self.impl
+        if stream_capturing():
+            raise RuntimeError(
+                "INT8 decode graph: prepare() stages the step's plan from host memory and "
+                "must run before a replay, not inside the capture."
+            )
         lens = [int(x) for x in attn_metadata.seq_lens_list]
         if len(lens) != self.batch or max(lens) > self.max_len:
             raise RuntimeError("INT8 decode graph: the step does not fit the captured shape.")
+        if attn_metadata.block_tables.shape[1] > self.table.shape[1]:
+            raise RuntimeError("INT8 decode graph: block table wider than captured.")
         slots = impl._int8_host_slots(attn_metadata, len(lens))
         split = int8_split_tokens(sum(lens), impl.num_kv_heads, seq_lens=lens)
         self.num_work = self.bufs.stage(slots, lens, split, fixed=True)
         table = attn_metadata.block_tables[: self.batch]
         self.table[:, : table.shape[1]].copy_(table, non_blocking=True)
+        self.prepared = True
 
     def launch(self, query, key, value, output) -> torch.Tensor:
         impl = self.impl
+        if not self.prepared:
+            raise RuntimeError("INT8 decode graph: call prepare() once before the capture.")
         b = self.batch
         q = query[:b].reshape(b, impl.num_heads, impl.head_size)
         out = output[:b].view(b, impl.num_heads, impl.head_size)

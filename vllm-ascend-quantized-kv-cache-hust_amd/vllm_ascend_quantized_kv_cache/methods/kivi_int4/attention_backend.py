@@ -23,6 +23,7 @@ from typing import Any
 import numpy as np
 import torch
 
+from ...core.runtime import stream_capturing
 from .byte_cache import kivi_byte_cache_layout, kivi_caches_from_byte_tensors
 from .geometry import validate_kivi_geometry
 from .residual import KiviResidualRing, StorePlan
@@ -67,6 +68,9 @@ def _gather_rows(src_a: Any, src_b: Any, src_index: Any) -> Any:
 class AscendKiviInt4AttentionBackendMixin:
     """KIVI INT4 (int4 history + full-precision residual window) attention path."""
 
+    #: capturable decode steps by batch size (``kivi_decode_graph``)
+    _kivi_capture_graphs: dict | None = None
+
     # ------------------------------------------------------------------
     # state (ab.py:50-133)
     # ------------------------------------------------------------------
@@ -101,6 +105,7 @@ class AscendKiviInt4AttentionBackendMixin:
         # its own copies of slot_mapping and block_tables)
         self.kivi_host_reads = 0
         self._kivi_step_bufs = None
+        self._kivi_capture_graphs = None
 
     def _validate_kivi_geometry(self) -> None:
         validate_kivi_geometry(
@@ -877,7 +882,43 @@ class AscendKiviInt4AttentionBackendMixin:
             )
         if attn_metadata is None:
             return output.fill_(0)
+        if stream_capturing():
+            return self._forward_kivi_captured(query, key, value, attn_metadata, output)
         return self._forward_kivi_attention(query, key, value, attn_metadata, output, kv_cache)
+
+    def _forward_kivi_captured(self, query: Any, key: Any, value: Any, attn_metadata: Any,
+                               output: Any) -> Any:
+        """``forward`` while the host records a HIP graph.
+
+        The reference has no graph path for KIVI (it runs ``--enforce-eager``,
+        ``docs/int4-host-integration.md:137-138``).  The eager step here
+        stages a one-step plan (window flushes, slots, lengths) from host
+        memory, and a recorded copy of it would replay that one step forever.
+        Only a decode step whose capturable form the host created beforehand
+        (``kivi_decode_graph``, whose ``prepare`` the host calls before every
+        replay) is recorded; anything else is refused.
+        """
+        b = len(attn_metadata.seq_lens_list)
+        graph = self._kivi_capture_graphs.get(b) if self._kivi_capture_graphs else None
+        if _attn_state_name(attn_metadata) != "DecodeOnly" or graph is None:
+            raise RuntimeError(
+                "KIVI INT4 forward() was called under HIP graph capture: its eager step stages "
+                "a one-step plan that every replay would reuse. Capture only decode steps, "
+                f"after creating the batch-{b} capturable step with "
+                "impl.kivi_decode_graph(batch, max_blocks=...), and call "
+                "impl.prepare_kivi_graph_replay(attn_metadata, key, value) before every replay; "
+                "or run the layer eagerly."
+            )
+        return graph.launch(query, key, value, output)
+
+    def prepare_kivi_graph_replay(self, attn_metadata: Any, key: Any, value: Any) -> None:
+        """Stage the plan of the step a captured ``forward`` will replay next
+        (the batch's ``KiviDecodeGraph.prepare``)."""
+        b = len(attn_metadata.seq_lens_list)
+        graph = self._kivi_capture_graphs.get(b) if self._kivi_capture_graphs else None
+        if graph is None:
+            raise RuntimeError(f"KIVI decode graph: no capturable step for batch {b}.")
+        graph.prepare(attn_metadata, key, value)
 
     def _forward_kivi_attention(
         self, query: Any, key: Any, value: Any, attn_metadata: Any, output: Any,
@@ -1064,35 +1105,41 @@ class AscendKiviInt4AttentionBackendMixin:
         from ...ops.kivi_decode import _cu_count
         from .decode_step import DecodeStepBuffers, KiviDecodeLauncher, eager_capacities
 
-        plan = self._plan_kivi_decode_step(attn_metadata, key, value)
-        if plan is None:
-            return None
-        jobs, seqs, table_dev = plan
-        b = seqs.shape[0]
-        dev = query.device
-        cu = _cu_count(dev)
-        work_cap, pieces_cap = eager_capacities(b, self.num_kv_heads, cu, seqs)
-        bufs = self._kivi_step_bufs
-        if bufs is None or not bufs.fits(b, work_cap, pieces_cap):
-            # grow with headroom so a serving loop settles on one buffer
-            bufs = DecodeStepBuffers(dev, batch=max(b, 2 * (bufs.batch if bufs else 0), 8),
-                                     window=self.kivi_residual_length, num_heads=self.num_heads,
-                                     head_size=self.head_size, work_cap=2 * work_cap,
-                                     pieces_cap=2 * pieces_cap)
-            self._kivi_step_bufs = bufs
         from ...ops import _native
 
-        staged = bufs.stage(jobs, seqs, num_kv_heads=self.num_kv_heads, cu_count=cu,
-                            mode=_native.KVQ_PLAN_DEFAULT, fixed=False)
-        launcher = KiviDecodeLauncher(self)
-        if jobs is not None:
-            ring = self._kivi_ring
-            kin = key[:b].reshape(b, self.num_kv_heads, self.head_size).to(ring.dtype).contiguous()
-            vin = value[:b].reshape(b, self.num_kv_heads, self.head_size).to(ring.dtype).contiguous()
-            launcher.store(bufs, staged, kin, vin)
-        q = query[:b].reshape(b, self.num_heads, self.head_size).contiguous()
-        out = output[:b].view(b, self.num_heads, self.head_size)
-        table = table_dev.to(device=dev, dtype=torch.int32).contiguous()
+        # the window mirror advances in the planning; the transaction stays
+        # open through staging and both launches, so an error anywhere before
+        # the store is queued leaves the mirror describing the device
+        with self._kivi_planning():
+            plan = self._plan_kivi_decode_step(attn_metadata, key, value)
+            if plan is None:
+                return None
+            jobs, seqs, table_dev = plan
+            b = seqs.shape[0]
+            dev = query.device
+            cu = _cu_count(dev)
+            work_cap, pieces_cap = eager_capacities(b, self.num_kv_heads, cu, seqs)
+            bufs = self._kivi_step_bufs
+            if bufs is None or not bufs.fits(b, work_cap, pieces_cap):
+                # grow with headroom so a serving loop settles on one buffer
+                bufs = DecodeStepBuffers(dev, batch=max(b, 2 * (bufs.batch if bufs else 0), 8),
+                                         window=self.kivi_residual_length,
+                                         num_heads=self.num_heads, head_size=self.head_size,
+                                         work_cap=2 * work_cap, pieces_cap=2 * pieces_cap)
+                self._kivi_step_bufs = bufs
+            staged = bufs.stage(jobs, seqs, num_kv_heads=self.num_kv_heads, cu_count=cu,
+                                mode=_native.KVQ_PLAN_DEFAULT, fixed=False)
+            launcher = KiviDecodeLauncher(self)
+            q = query[:b].reshape(b, self.num_heads, self.head_size).contiguous()
+            out = output[:b].view(b, self.num_heads, self.head_size)
+            table = table_dev.to(device=dev, dtype=torch.int32).contiguous()
+            if jobs is not None:
+                ring = self._kivi_ring
+                kin = key[:b].reshape(b, self.num_kv_heads, self.head_size).to(
+                    ring.dtype).contiguous()
+                vin = value[:b].reshape(b, self.num_kv_heads, self.head_size).to(
+                    ring.dtype).contiguous()
+                launcher.store(bufs, staged, kin, vin)
         launcher.decode(bufs, staged, q, table, out)
         return output
 
@@ -1102,7 +1149,11 @@ class AscendKiviInt4AttentionBackendMixin:
         ``prepare`` stages that step's plan."""
         from .decode_step import KiviDecodeGraph
 
-        return KiviDecodeGraph(self, batch, max_blocks=max_blocks, rounds=rounds)
+        graph = KiviDecodeGraph(self, batch, max_blocks=max_blocks, rounds=rounds)
+        if self._kivi_capture_graphs is None:
+            self._kivi_capture_graphs = {}
+        self._kivi_capture_graphs[batch] = graph  # what a captured forward() launches
+        return graph
 
     def _forward_kivi_paged_decode_attention(
         self, query: Any, block_table: Any, seq_lens: list[int], req_ids: list[str] | None,

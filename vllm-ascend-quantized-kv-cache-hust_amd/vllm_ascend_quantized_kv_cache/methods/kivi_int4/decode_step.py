@@ -156,6 +156,9 @@ class DecodeStepBuffers:
         if fixed:
             if npc == 0:
                 raise RuntimeError("KIVI decode step: a fixed launch needs a plan in pieces.")
+            # a launch over the whole capacity finds empty items past the plan
+            # (request 0, no positions: m = -inf into the item's own partial)
+            work[n:] = 0
             pieces_off = self.pieces_off
             pieces = h[pieces_off:].view(np.int32)
             pieces[: npc + 1] = self._pieces[: npc + 1]
@@ -282,29 +285,58 @@ class KiviDecodeGraph:
         self.staged: StagedPlan | None = None
 
     def prepare(self, attn_metadata, key: torch.Tensor, value: torch.Tensor) -> None:
+        """Stage one step's plan for the next replay (outside any capture).
+
+        Every check that can refuse the step runs before the window mirror
+        moves, and the planning, staging and table refresh form one
+        transaction: a step that raises leaves the mirror as it was.
+        """
+        from ...core.runtime import stream_capturing
+
         impl = self.impl
-        plan = impl._plan_kivi_decode_step(attn_metadata, key, value, allow_compaction=False)
-        if plan is None:
+        if stream_capturing():
             raise RuntimeError(
-                "KIVI decode graph: this step is not one token per request with slots that "
-                "follow the block table; run it eagerly through forward."
+                "KIVI decode graph: prepare() stages the step's plan from host memory and "
+                "must run before a replay, not inside the capture."
             )
-        jobs, seqs, table_dev = plan
-        if seqs.shape[0] != self.bufs.batch:
+        b = len(attn_metadata.seq_lens_list)
+        if b != self.bufs.batch:
             raise RuntimeError(
-                f"KIVI decode graph was captured for batch {self.bufs.batch}, got {seqs.shape[0]}."
+                f"KIVI decode graph was captured for batch {self.bufs.batch}, got {b}."
             )
-        self.staged = self.bufs.stage(jobs, seqs, num_kv_heads=impl.num_kv_heads,
-                                      cu_count=self.cu_count, mode=_native.KVQ_PLAN_PIECES,
-                                      fixed=True)
-        rows, cols = table_dev.shape
-        if cols > self.table.shape[1]:
+        if attn_metadata.block_tables.shape[1] > self.table.shape[1]:
             raise RuntimeError("KIVI decode graph: block table wider than captured.")
-        self.table[:rows, :cols].copy_(table_dev, non_blocking=True)
+        ring = impl._ensure_kivi_residual_buffers()
+        ok = key.dtype in (torch.bfloat16, torch.float16) and value.dtype == key.dtype
+        if ok and not ring.written:
+            ring.adopt_dtype(key.dtype)  # a ring with no data takes the activation dtype
+        if not ok or ring.dtype != key.dtype or not step_geometry_ok(impl, key):
+            raise RuntimeError(
+                "KIVI decode graph: the layer's geometry or activation dtype is not one the "
+                "planned store and the pieces decode cover (head size 128, group 64 or 128, "
+                "16-bit activations shared with the ring, at most 16 query heads per kv head, "
+                "a power-of-two block size); run it eagerly through forward."
+            )
+        with impl._kivi_planning():
+            plan = impl._plan_kivi_decode_step(attn_metadata, key, value, allow_compaction=False)
+            if plan is None:
+                raise RuntimeError(
+                    "KIVI decode graph: this step is not one token per request with slots that "
+                    "follow the block table; run it eagerly through forward."
+                )
+            jobs, seqs, table_dev = plan
+            staged = self.bufs.stage(jobs, seqs, num_kv_heads=impl.num_kv_heads,
+                                     cu_count=self.cu_count, mode=_native.KVQ_PLAN_PIECES,
+                                     fixed=True)
+            rows, cols = table_dev.shape
+            self.table[:rows, :cols].copy_(table_dev, non_blocking=True)
+        self.staged = staged
 
     def launch(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                output: torch.Tensor) -> torch.Tensor:
         impl = self.impl
+        if self.staged is None:
+            raise RuntimeError("KIVI decode graph: call prepare() once before the capture.")
         b = self.bufs.batch
         q = query[:b].view(b, impl.num_heads, impl.head_size)
         out = output[:b].view(b, impl.num_heads, impl.head_size)

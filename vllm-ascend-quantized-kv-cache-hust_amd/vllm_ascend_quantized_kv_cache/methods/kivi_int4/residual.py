@@ -144,6 +144,8 @@ class KiviResidualRing:
         self.lane_slot = {s: np.full((rows, ring_len), -1, dtype=np.int64) for s in _SIDES}
         self.lane_pos = {s: np.full((rows, ring_len), -1, dtype=np.int64) for s in _SIDES}
         self._saved: dict[int, tuple] | None = None
+        # vectorized snapshots of whole batches of rows: (rows, per-side arrays)
+        self._saved_batches: list[tuple[np.ndarray, tuple]] = []
 
     # -- all-or-nothing planning ----------------------------------------------
 
@@ -161,14 +163,43 @@ class KiviResidualRing:
             yield
             return
         self._saved = {}
+        self._saved_batches = []
         try:
             yield
         except BaseException:
             for row, state in self._saved.items():
-                self._restore(row, state)
+                if state is not None:
+                    self._restore(row, state)
+            for rows, snap in self._saved_batches:
+                for k, (start, length, ls, lp) in zip(_SIDES, snap):
+                    self.start[k][rows] = start
+                    self.length[k][rows] = length
+                    self.lane_slot[k][rows] = ls
+                    self.lane_pos[k][rows] = lp
             raise
         finally:
             self._saved = None
+            self._saved_batches = []
+
+    def _touch_rows(self, rows: np.ndarray) -> None:
+        """``_touch`` for a batch of distinct rows, as one vectorized copy.
+
+        Rows already saved keep their earlier snapshot; the rest are marked
+        saved (the per-row map holds ``None`` for them) so later touches do
+        not snapshot them again.
+        """
+        if self._saved is None:
+            return
+        new = [r for r in rows.tolist() if r not in self._saved]
+        if not new:
+            return
+        idx = np.asarray(new, dtype=np.int64)
+        self._saved_batches.append((idx, tuple(
+            (self.start[k][idx].copy(), self.length[k][idx].copy(),
+             self.lane_slot[k][idx].copy(), self.lane_pos[k][idx].copy())
+            for k in _SIDES)))
+        for r in new:
+            self._saved[r] = None
 
     def _touch(self, row: int) -> None:
         if self._saved is not None and row not in self._saved:
@@ -526,7 +557,9 @@ class KiviResidualRing:
         k_ev = self.lane_slot[True][fk[:, None], k_lanes]
         if fk.size and not self._aligned_windows(k_ev, block_size, group_size):
             raise RuntimeError(_FLUSH_ERROR)
-        # nothing below raises, so no row needs a snapshot for a rollback
+        # inside a transaction the rows are snapshotted, so an error after the
+        # planning (staging, a launch) still rolls the whole batch back
+        self._touch_rows(rows)
         # keys: flush whole windows
         kp_src = (fk[:, None] * r + k_lanes).ravel()
         kp_slot = k_ev.ravel()
