@@ -512,6 +512,139 @@ def cpu_baseline_decode(torch, st, q, seqs, *, hq, kvh, d, g, bs, scale, sample=
     }
 
 
+def _cpu_median(fn, runs=3):
+    """Median wall time (s) of ``runs`` calls after one untimed call."""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def _cpu_random_kivi_pages(torch, nb, bs, kvh, d, g, gen):
+    """Int4 pages with random codes and plausible scales/mins (the oracle's
+    dequant costs the same whatever the codes are)."""
+    words = torch.randint(-2**31, 2**31, (nb, kvh, d, bs // 8), generator=gen, dtype=torch.int64)
+    kq = words.to(torch.int32)
+    ks = torch.rand((nb, kvh, d, bs // g), generator=gen) * 0.5 + 0.01
+    km = torch.randn((nb, kvh, d, bs // g), generator=gen)
+    vq = torch.randint(-2**31, 2**31, (nb, bs, kvh, d // 8), generator=gen,
+                       dtype=torch.int64).to(torch.int32)
+    vs = torch.rand((nb, bs, kvh, d // g), generator=gen) * 0.5 + 0.01
+    vm = torch.randn((nb, bs, kvh, d // g), generator=gen)
+    return kq, ks, km, vq, vs, vm
+
+
+def cpu_baselines_rest(torch) -> dict:
+    """The oracle (the reference's algorithms restated in torch on the CPU)
+    timed on the rest of the path, on this host's cores: median of 3 runs
+    after one untimed run, GB/s of the same algorithmic bytes as the GPU legs.
+
+    * config 1: pack 896 history tokens (both sides) and gather-dequant the
+      1024-token sequence with its 128-token residual overlaid;
+    * config 4: pack the 8 x 2048-token chunk, and gather 8 x 10240 tokens
+      (10112 int4 + 128 residual per side and request);
+    * config 2: INT8 paged dequant to dense + fp32 SDPA, 64 x 4096 tokens;
+    * config 5: 8 of the 256 sequences (32768 tokens each, G 64): int4
+      gather-dequant + residual overlay + fp32 SDPA, the sample's own bytes
+      and time (the rate of the whole batch is the same per sequence).
+    """
+    from oracle import kvq_oracle as ref
+
+    info = cpu_info()
+    torch.set_num_threads(info["cores"])
+    gen = torch.Generator().manual_seed(0)
+    out = {}
+
+    def entry(name, nbytes, t, sample):
+        out[name] = {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s",
+                     "ms": round(t * 1e3, 2), "sample": sample}
+
+    kvh, d = 8, 128
+    # --- configs 1 and 4: pack and gather (G = R = Bs = 128) ---------------
+    for name, b, n_pack, hist, res in (("config1", 1, 896, 896, 128),
+                                       ("config4", 8, 2048, 10112, 128)):
+        g = bs = 128
+        s = d // 2 + 8 * d // g
+        lens = [hist + res] * b
+        maxb = -(-lens[0] // bs)
+        nb = b * maxb
+        caches = _cpu_random_kivi_pages(torch, nb, bs, kvh, d, g, gen)
+        table = torch.randperm(nb, generator=gen).view(b, maxb)
+        scales = torch.exp(torch.randn((kvh, d), generator=gen))
+        key = (torch.randn((b * n_pack, kvh, d), generator=gen) * scales).to(torch.bfloat16)
+        value = torch.randn((b * n_pack, kvh, d), generator=gen).to(torch.bfloat16)
+        p0 = hist - n_pack  # the packed tokens end where the residual starts
+        slots = torch.tensor([int(table[i, p // bs]) * bs + p % bs
+                              for i in range(b) for p in range(p0, hist)])
+
+        def pack():
+            ref.pack_key_cache(key.float(), slots, *caches[:3], g)
+            ref.pack_value_cache(value.float(), slots, *caches[3:], g)
+
+        t = _cpu_median(pack)
+        entry(f"{name}_pack", b * n_pack * kvh * 2 * (2 * d + s), t,
+              f"{b} x {n_pack} tokens, key + value pack (fp32 cast, group min/max, "
+              "quantize, word pack, slot scatter)")
+        ring = [torch.randn((res, kvh, d), generator=gen).to(torch.bfloat16) for _ in range(b)]
+
+        def gather():
+            dk, dv = ref.dequant_gather(*caches, table, torch.tensor(lens), torch.bfloat16, g)
+            return ref.overlay_residual(dk, lens, ring), ref.overlay_residual(dv, lens, ring)
+
+        t = _cpu_median(gather)
+        # per (token, head, side): int4 S bytes read + bf16 row written; the
+        # residual rows are read and written in bf16
+        entry(f"{name}_gather", b * 2 * hist * kvh * (s + 2 * d) + b * 2 * res * kvh * d * 4, t,
+              f"{b} x {lens[0]} tokens ({hist} int4 + {res} residual per side): "
+              "dequant-gather to dense bf16 TND + residual overlay")
+    # --- config 2: INT8 paged dequant + SDPA -------------------------------
+    b, hq, n, bs = 64, 32, 4096, 128
+    nb = b * n // bs
+    kc = torch.randint(-128, 128, (nb, bs, kvh, d), generator=gen, dtype=torch.int8)
+    vc = torch.randint(-128, 128, (nb, bs, kvh, d), generator=gen, dtype=torch.int8)
+    inv = (torch.rand((1, kvh, d), generator=gen) * 100 + 1).to(torch.bfloat16)
+    table = torch.randperm(nb, generator=gen).view(b, n // bs)
+    q = torch.randn((b, hq, d), generator=gen).to(torch.bfloat16)
+
+    def int8_decode():
+        dk, dv = ref.int8_paged_dequant(kc, vc, table, [n] * b, torch.bfloat16, inv, inv)
+        return ref.attention(q, dk, dv, [1] * b, [n] * b, d ** -0.5, causal=True)
+
+    t = _cpu_median(int8_decode)
+    entry("config2_int8_decode", b * (2 * n * kvh * d + 2 * hq * d * 2 + 4 * (n // bs)), t,
+          f"{b} x {n} tokens: int8 paged dequant to dense bf16 + fp32 SDPA")
+    # --- config 5 subset ----------------------------------------------------
+    sub, hq, g, r, n, bs = 8, 64, 64, 128, 32768, 128
+    s = d // 2 + 8 * d // g
+    hist_k = (n - 1) // r * r
+    hist_v = n - r
+    maxb = n // bs
+    nb = sub * maxb
+    caches = _cpu_random_kivi_pages(torch, nb, bs, kvh, d, g, gen)
+    table = torch.randperm(nb, generator=gen).view(sub, maxb)
+    q = torch.randn((sub, hq, d), generator=gen).to(torch.bfloat16)
+    rk = [torch.randn((n - hist_k, kvh, d), generator=gen).to(torch.bfloat16) for _ in range(sub)]
+    rv = [torch.randn((n - hist_v, kvh, d), generator=gen).to(torch.bfloat16) for _ in range(sub)]
+    lens = [n] * sub
+
+    def c5():
+        dk, dv = ref.dequant_gather(*caches, table, torch.tensor(lens), torch.bfloat16, g)
+        dk = ref.overlay_residual(dk, lens, rk)
+        dv = ref.overlay_residual(dv, lens, rv)
+        return ref.attention(q, dk, dv, [1] * sub, lens, d ** -0.5, causal=True)
+
+    t = _cpu_median(c5)
+    nbytes = sub * ((hist_k + hist_v) * kvh * s + (2 * n - hist_k - hist_v) * kvh * d * 2
+                    + 2 * hq * d * 2 + 4 * maxb)
+    entry("config5_int4_decode", nbytes, t,
+          f"{sub} of 256 sequences x {n} tokens (G 64): dequant-gather + residual overlay "
+          "+ fp32 SDPA")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # extras
 # ---------------------------------------------------------------------------
@@ -936,6 +1069,11 @@ def main() -> int:
     if "cpu" in main_res:
         c = dict(main_res["cpu"])
         c.pop("ms", None)
+        # the rest of the path (pack, gather, INT8 decode, config 5) on the
+        # same cores, beside the headline's config-3 decode
+        log("cpu baseline: oracle pack / gather (configs 1, 4), int8 decode (config 2), "
+            "config-5 sample")
+        c["extra"] = cpu_baselines_rest(torch)
         line["cpu_baseline"] = c
     print(json.dumps(line), flush=True)
     return 0
