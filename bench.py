@@ -199,6 +199,7 @@ def bench_kivi_decode(torch, dev, *, b, hq, kvh, d, g, r, bs, lens, steps, warmu
     from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
         _cu_count,
         kivi_decode_attention,
+        page_streaming_applies,
         plan_decode,
         plan_decode_work,
     )
@@ -247,7 +248,9 @@ def bench_kivi_decode(torch, dev, *, b, hq, kvh, d, g, r, bs, lens, steps, warmu
                 meta_np, work_np = plan_decode_work(seqs, split_tokens)
                 pieces_np = None
             else:
-                meta_np, work_np, pieces_np = plan_decode(seqs, kvh, _cu_count(dev))
+                paged = page_streaming_applies(hq, kvh, d, bs, g, torch.bfloat16, ring.dtype)
+                meta_np, work_np, pieces_np = plan_decode(seqs, kvh, _cu_count(dev),
+                                                          page_streaming=paged)
             p = {
                 "kidx": dev_t(plan.key.pack_src), "kslots": dev_t(plan.key.pack_slots),
                 "vidx": dev_t(plan.value.pack_src), "vslots": dev_t(plan.value.pack_slots),

@@ -168,10 +168,16 @@ int kvq_kivi_gather_dequant(const int32_t* k_quant, const float* k_scale, const 
  *                       share the range's key lines through its L2.
  *               a request's items are contiguous, from first_work on
  *   pieces      int32 [num_pieces + 1] or NULL: piece k is work items
- *               [pieces[k], pieces[k+1]).  Where the MFMA kernel runs both
- *               kinds, one wave per (piece, kv head) runs its piece's items
- *               in order in a single pass, so pieces of equal cost end
- *               together; elsewhere the pieces are ignored.
+ *               [pieces[k], pieces[k+1]).  At num_kv_heads 8, D 128,
+ *               block_size 128, group_size 64 or 128, at most 16 query
+ *               heads per kv head and 16-bit query and ring, one workgroup
+ *               per piece streams the piece's kind-0 items page by page for
+ *               all kv heads, then runs its tail items (plan with
+ *               split_tokens 128 so that no two pieces share a page).
+ *               Elsewhere, where the MFMA kernel runs both kinds, one wave
+ *               per (piece, kv head) runs its piece's items in order in a
+ *               single pass, so pieces of equal cost end together; else the
+ *               pieces are ignored.
  *   workspace   >= kvq_kivi_decode_workspace_bytes(num_work, num_heads, D)
  *   block_table int32 [batch, max_blocks]
  * Replaces the decode branch: _forward_kivi_paged_decode_attention
@@ -219,8 +225,11 @@ int kvq_kivi_decode_attn_noalloc(const void* query, int q_dtype, int64_t batch, 
  *             k_first_lane, v_first_lane} (the seq_meta columns it fills)
  *   seq_meta  int32 [batch, 8]; work int32 [cap_work, 4];
  *   pieces    int32 [cap_pieces + 1] (KVQ_PLAN_PIECES / DEFAULT)
- *   mode      KVQ_PLAN_*; split_tokens for the SPLIT modes; tail_cost = the
- *             cost of one residual-window position in int4 positions
+ *   mode      KVQ_PLAN_*; split_tokens for the SPLIT modes, and for
+ *             KVQ_PLAN_PIECES the int4 tile (0 or 64: kind-0 items cut on
+ *             64-position bounds; 128: on 128-position bounds, the pages of
+ *             the page-streaming decode); tail_cost = the cost of one
+ *             residual-window position in int4 positions
  * Returns the number of work items, *num_pieces (0 for split plans), or
  * KVQ_ERR_INVALID / KVQ_ERR_CAPACITY.  Replaces the per-step decode planning
  * a host does before _forward_kivi_paged_decode_attention

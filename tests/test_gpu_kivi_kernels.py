@@ -161,11 +161,14 @@ def test_gather_bit_exact(gpu_device, d, kvh, g, bs):
         assert torch.equal(want_v, got_v.cpu()), out_dtype
 
 
-def _ring_case(dev, d, kvh, g, bs, r_len, lens, seed, ring_dtype=torch.float32, split=None):
+def _ring_case(dev, d, kvh, g, bs, r_len, lens, seed, ring_dtype=torch.float32, split=None,
+               stale=False):
     """Packed history for several requests plus residual rings (FIFO, wrapped).
 
     ``split(n) -> (hist_k, hist_v)``: the int4 history of each side (default:
-    the incremental rule, ``ref.incremental_split``)."""
+    the incremental rule, ``ref.incremental_split``).  ``stale``: the bytes no
+    pack writes hold NaN scales and minima and nonzero codes, as a reused
+    page would, so a read past a request's int4 history shows."""
     nb = sum(-(-n // bs) for n in lens) + 2
     maxb = max(-(-n // bs) for n in lens)
     table = torch.full((len(lens), maxb), -1, dtype=torch.int32)
@@ -176,6 +179,11 @@ def _ring_case(dev, d, kvh, g, bs, r_len, lens, seed, ring_dtype=torch.float32, 
         table[r, :nblk] = perm[used : used + nblk]
         used += nblk
     cpu = empty_kivi_caches(nb, bs, kvh, d, g)
+    if stale:
+        for t in (cpu[1], cpu[2], cpu[4], cpu[5]):
+            t.fill_(float("nan"))
+        cpu[0].fill_(0x77777777)
+        cpu[3].fill_(0x77777777)
     ring_k = torch.zeros(len(lens) + 1, r_len, kvh, d, dtype=ring_dtype)
     ring_v = torch.zeros_like(ring_k)
     seqs, windows_k, windows_v, keys, values = [], [], [], [], []
@@ -377,6 +385,50 @@ def test_decode_pieces_match_oracle(gpu_device, kvh, g, bs, rep, cu_count):
     )
     # rows of empty requests are the empty sum (zeros) in both
     torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("g,rep,dtype", [(128, 5, torch.bfloat16), (64, 8, torch.float16),
+                                         (64, 16, torch.bfloat16), (128, 12, torch.float16)])
+@pytest.mark.parametrize("tile,cu_count", [(128, 256), (128, 1), (64, 3)])
+def test_page_streaming_decode_matches_oracle(gpu_device, g, rep, dtype, tile, cu_count):
+    """The page-streaming decode (8 kv heads, block 128, head size 128): one
+    workgroup per piece streams whole pages for all heads.  Pieces on page
+    bounds (tile 128) and on 64-position bounds (items that start and end
+    mid-page), a single piece holding every item (the stage stream crosses
+    requests), folded (<= 8) and unfolded GQA groups up to 16, both 16-bit
+    dtypes, and NaN scales in every byte past the int4 histories, which the
+    masked positions of a page must not reach."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
+        DecodeSeq,
+        kivi_decode_attention,
+        plan_decode_pieces,
+    )
+
+    d, kvh, bs = 128, 8, 128
+    r_len = 2 * g if g <= 64 else g
+    lens = [r_len * 9 + 3, 1, 700, 0, r_len * 5 + 64, 77, 2 * bs + 1, 3 * bs]
+    cpu, table, ring_k, ring_v, seqs, wk, wv, _, _ = _ring_case(
+        gpu_device, d, kvh, g, bs, r_len, lens, seed=41, ring_dtype=dtype, stale=True
+    )
+    hq = kvh * rep
+    q = torch.randn(len(lens), hq, d, generator=torch.Generator().manual_seed(8)).to(dtype)
+    scale = d ** -0.5
+    dk, dv = ref.dequant_gather(*cpu, table, torch.tensor(lens), torch.float32, g)
+    dk = ref.overlay_residual(dk, lens, wk)
+    dv = ref.overlay_residual(dv, lens, wv)
+    want = ref.attention(q.float(), dk, dv, [1] * len(lens), lens, scale, causal=True)
+    dseqs = [DecodeSeq(n, hk, hv, row, ks_, vs_) for (n, hk, hv, row, ks_, vs_) in seqs]
+    meta, work, pieces = plan_decode_pieces(dseqs, kvh, cu_count, tile=tile)
+    print(f"page-streaming case g={g} rep={rep} {dtype} tile={tile} cu={cu_count}: "
+          f"{len(work)} items, {len(pieces) - 1} pieces", flush=True)
+    dev = gpu_device
+    got = kivi_decode_attention(
+        q.to(dev), to_dev(cpu, dev), table.to(dev), dseqs, ring_k.to(dev), ring_v.to(dev),
+        scale, g, plan=(torch.from_numpy(meta).to(dev), torch.from_numpy(work).to(dev),
+                        torch.from_numpy(pieces).to(dev)),
+    ).float().cpu()
+    assert torch.isfinite(got).all()
+    torch.testing.assert_close(got, want, atol=1e-2, rtol=1e-2)
 
 
 @pytest.mark.parametrize("d,kvh,g,bs", [(128, 8, 128, 128), (128, 8, 64, 128), (128, 4, 32, 64),

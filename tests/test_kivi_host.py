@@ -433,12 +433,15 @@ def test_one_launch_store_geometry_gate():
     assert not store_one_launch_supported(128, 128, torch.float32)
 
 
-@pytest.mark.parametrize("cu_count,kvh", [(256, 8), (3, 4), (1, 1), (256, 2)])
-def test_plan_decode_pieces_invariants(cu_count, kvh):
+@pytest.mark.parametrize("cu_count,kvh,tile",
+                         [(256, 8, 64), (3, 4, 64), (1, 1, 64), (256, 2, 64), (256, 8, 128),
+                          (3, 8, 128)])
+def test_plan_decode_pieces_invariants(cu_count, kvh, tile):
     """Equal-cost pieces: at most one wave slot per piece, items of a request
-    contiguous and covering it exactly (int4 items on 64-position starts,
+    contiguous and covering it exactly (int4 items on `tile`-position starts,
     both sides int4 over them), pieces covering the list in order, and piece
-    costs within one step of each other."""
+    costs within one step of each other.  Tile 128 (the page-streaming
+    decode's pages): no page is split between two pieces."""
     from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
         PIECE_MAX_COST,
         TAIL_POSITION_COST,
@@ -454,12 +457,12 @@ def test_plan_decode_pieces_invariants(cu_count, kvh):
         hk = ((n - 1) // r) * r if n else 0
         hv = max(0, n - r)
         seqs.append(DecodeSeq(n, hk, hv, i, 0, 0))
-    meta, work, pieces = plan_decode_pieces(seqs, kvh, cu_count)
+    meta, work, pieces = plan_decode_pieces(seqs, kvh, cu_count, tile=tile)
     slots = max(1, cu_count * 8 // kvh)
     total = 0.0
     for s in seqs:
         a = max(0, min(s.k_hist, s.v_hist, s.seq_len))
-        total += -(-a // 64) * 64 + (s.seq_len - a) * TAIL_POSITION_COST
+        total += -(-a // tile) * tile + (s.seq_len - a) * TAIL_POSITION_COST
     slots *= max(1, -(-int(total) // int(slots * PIECE_MAX_COST)))  # whole rounds
     assert 1 <= len(pieces) - 1 <= slots
     assert pieces[0] == 0 and pieces[-1] == len(work)
@@ -474,16 +477,47 @@ def test_plan_decode_pieces_invariants(cu_count, kvh):
             assert p == pos and e >= p
             pos = e
             if kind == 0:
-                assert p % 64 == 0 and e <= min(s.k_hist, s.v_hist) and e > p
+                assert p % tile == 0 and e <= min(s.k_hist, s.v_hist) and e > p
         assert pos == s.seq_len
     if len(pieces) - 1 == slots and slots > 1:
         cost = [
-            sum(-(-(e - p) // 64) * 64 if k == 0 else (e - p) * TAIL_POSITION_COST
+            sum(-(-(e - p) // tile) * tile if k == 0 else (e - p) * TAIL_POSITION_COST
                 for _, p, e, k in work[pieces[i] : pieces[i + 1]].tolist())
             for i in range(len(pieces) - 1)
         ]
         step = sum(cost) / slots
-        assert max(cost) <= step + 2 * 32 * TAIL_POSITION_COST + 64
+        assert max(cost) <= step + 2 * 32 * TAIL_POSITION_COST + tile
+
+
+def test_plan_pieces_rejects_other_tiles():
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import DecodeSeq, plan_decode_pieces
+
+    with pytest.raises(RuntimeError):
+        plan_decode_pieces([DecodeSeq(300, 256, 172, 0, 0, 0)], 8, 256, tile=96)
+
+
+def test_page_streaming_plan_covers_any_amount_of_work_in_pieces():
+    """With page streaming the default plan is pieces on page bounds, also for
+    work that takes many rounds (config 5's shape)."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
+        DecodeSeq,
+        page_streaming_applies,
+        plan_decode,
+    )
+
+    big = [DecodeSeq(32768, 32640, 32640, i, 0, 0) for i in range(256)]
+    _, work, pieces = plan_decode(big, 8, 256, page_streaming=True)
+    assert pieces is not None and pieces[0] == 0 and pieces[-1] == len(work)
+    # 32640 int4 positions + 128 tail positions at 6 each: 9 rounds of 256
+    assert len(pieces) - 1 == 256 * 9
+    int4 = work[work[:, 3] == 0]
+    assert (int4[:, 1] % 128 == 0).all()
+    assert page_streaming_applies(64, 8, 128, 128, 64, torch.bfloat16, torch.bfloat16)
+    assert page_streaming_applies(40, 8, 128, 128, 128, torch.float16, torch.float16)
+    assert not page_streaming_applies(40, 8, 128, 128, 128, torch.float16, torch.bfloat16)
+    assert not page_streaming_applies(32, 4, 128, 128, 128, torch.bfloat16, torch.bfloat16)
+    assert not page_streaming_applies(64, 8, 128, 64, 64, torch.bfloat16, torch.bfloat16)
+    assert not page_streaming_applies(136, 8, 128, 128, 64, torch.bfloat16, torch.bfloat16)
 
 
 def test_plan_decode_picks_pieces_for_one_round_and_splits_beyond():

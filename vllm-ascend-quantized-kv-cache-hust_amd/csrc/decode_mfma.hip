@@ -38,6 +38,7 @@
 // Online softmax in the log2 domain; each work item leaves (m, l, o) per head
 // for the log-sum-exp combine.
 #include "decode_tail.h"
+#include "decode_tr.h"
 #include "kvq_common.h"
 #include "kvq_decode.h"
 
@@ -735,12 +736,107 @@ __device__ __forceinline__ void store_partial(const tail::Partial& p, int wi, in
   }
 }
 
+// One int4 work item (kinds 0, 2, 3) of kv head h on the transposing-read
+// tile (CPG 8: 64-token tiles, key groups of 64 or more): the same walk as the
+// general loop of the kernel below -- windows of 64-position chunks, one
+// barrier per window, a double buffer per wave filled by LDS DMA -- with
+// decode_tr.h's tile layout and compute.
+template <typename TQ, int NVG, bool KSV, bool FOLD>
+__device__ __forceinline__ void tr_item(
+    const TQ* __restrict__ query, int hq, int kvh, int h, int rep, float qscale,
+    const uint32_t* __restrict__ kq, const float* __restrict__ ks, const float* __restrict__ km,
+    const uint32_t* __restrict__ vq, const float* __restrict__ vs, const float* __restrict__ vm,
+    int bs, int g, int64_t nb, const int32_t* __restrict__ block_table, int64_t maxb, int b,
+    int pb, int pe, int kind, int wi, char* my_lds, float* xfer, int half, int npair, int lane,
+    int n, int kg, int gpb, int ng, int wpd, bool pieces, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml) {
+  using T = tr::Tile<NVG, KSV>;
+  constexpr int D = T::D;
+  constexpr int GT = T::GT;
+  const tr::QLane<TQ> ql = tr::load_q<TQ>(query, b, hq, h, rep, n, kg, FOLD);
+  const tr::LaneDma ld = tr::lane_dma(lane, wpd, kvh, gpb, ng, KSV);
+  tr::Acc<NVG> acc;
+  acc.init();
+  const int bsh = __builtin_ctz(static_cast<unsigned>(bs));
+  const int gsh = __builtin_ctz(static_cast<unsigned>(g));
+  PageIds pages(block_table + static_cast<int64_t>(b) * maxb, maxb, nb, bsh, pb, pe, lane);
+  auto issue = [&](char* buf, int p, bool with_ks) {
+    const int64_t blk = pages.page(p);
+    const int off0 = p & (bs - 1);
+    const int64_t krow = (blk * kvh + h) * D;
+    const int64_t vtok = ((blk << bsh) + off0) * kvh + h;
+    tr::issue_tile<NVG, KSV>(buf, ld, kq + krow * wpd + (off0 >> 3), wpd,
+                             ks + krow * gpb + (off0 >> gsh), km + krow * gpb + (off0 >> gsh), gpb,
+                             vq + vtok * 16, kvh, vs + vtok * ng, vm + vtok * ng, with_ks);
+  };
+  const int hs = kind >= 2 ? kind - 2 : -1;
+  const int cb = hs < 0 ? (pb & ~(64 * npair - 1)) : pb + 64 * hs;
+  const int cs = 64 * npair * (hs < 0 ? 1 : 2);
+  const int nwin = (pe - cb + cs - 1) / cs;
+  int p_first = cb + (cs / npair) * half;
+  if (p_first < pb) p_first += cs;
+  auto next_tile = [&](int p) {
+    p += GT;
+    if ((p & 63) == 0) p += cs - 64;
+    return p;
+  };
+  tr::QGroup qg;
+  auto step = [&](const char* __restrict__ cur, char* __restrict__ nxt, int p0, bool new_group) {
+    const int p1 = next_tile(p0);
+    if (p1 < pe) {
+      if ((p1 >> gsh) != (p0 >> gsh)) {
+        issue(nxt, p1, true);
+        wait_vmcnt<T::NINST>();
+      } else {
+        issue(nxt, p1, false);
+        wait_vmcnt<T::NINST_CONT>();
+      }
+    } else {
+      wait_vmcnt<0>();
+    }
+    const uint32_t* W = reinterpret_cast<const uint32_t*>(cur);
+    if (new_group) tr::prepare_group<TQ, NVG, KSV, FOLD>(W, n, kg, ql, qscale, qg);
+    if (pieces) __builtin_amdgcn_s_setprio(1);
+    const uint32_t off = tr::lds_off(cur);
+    if (p0 + GT <= pe)
+      tr::compute_tile<NVG, KSV, FOLD, true>(W, off, p0, pe, n, kg, qg, qscale, acc);
+    else
+      tr::compute_tile<NVG, KSV, FOLD, false>(W, off, p0, pe, n, kg, qg, qscale, acc);
+    if (pieces) __builtin_amdgcn_s_setprio(0);
+  };
+  if (p_first < pe) issue(my_lds, p_first, true);  // prologue: tile 0 into buffer 0
+  int cur = 0;
+  int p = p_first;
+  int g_prev = -1;
+  for (int k = 0; k < nwin; ++k) {
+    __builtin_amdgcn_s_barrier();  // the workgroup's waves enter window k together
+    const int wend = cb + cs * (k + 1);
+    while (p < pe && p < wend) {
+      step(my_lds + cur * T::BYTES, my_lds + (cur ^ 1) * T::BYTES, p, (p >> gsh) != g_prev);
+      asm volatile("" ::: "memory");
+      cur ^= 1;
+      g_prev = p >> gsh;
+      p = next_tile(p);
+    }
+  }
+  tail::Partial part;
+  tr::finish<NVG>(acc, kg, part.o);
+  part.m = acc.m_run;
+  part.l = acc.l_run;
+  if (npair == 2) tail::merge_halves(part, xfer, half, lane);
+  if (half == 0) tr::store_partial(part.o, part.m, part.l, wi, hq, h, rep, n, kg, ws_o, ws_ml);
+}
+
 // LDS of one wave: its two tile buffers, or the tail path's staging.
+template <int CPG, bool VG1, bool KSV>
+__host__ __device__ constexpr int tile_bytes() {
+  return CPG == 8 ? tr::Tile<VG1 ? 1 : 2, KSV>::BYTES : Tile<CPG, VG1, KSV>::BYTES;
+}
 template <int CPG, bool VG1, bool KSV, bool TAIL>
 __host__ __device__ constexpr int wave_lds_bytes() {
-  return TAIL && tail::kLdsBytes > 2 * Tile<CPG, VG1, KSV>::BYTES
+  return TAIL && tail::kLdsBytes > 2 * tile_bytes<CPG, VG1, KSV>()
              ? tail::kLdsBytes
-             : 2 * Tile<CPG, VG1, KSV>::BYTES;
+             : 2 * tile_bytes<CPG, VG1, KSV>();
 }
 
 // A workgroup holds npair * hpw waves: kv heads q*hpw .. q*hpw + hpw - 1 of
@@ -836,6 +932,12 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, int hpw, 
   const int gpb = bs / g;
   const int ng = D / g;
   const int wpd = bs / 8;
+  if constexpr (CPG == 8) {
+    tr_item<TQ, VG1 ? 1 : 2, KSV, FOLD>(query, hq, kvh, h, rep, qscale, kq, ks, km, vq, vs, vm,
+                                        bs, g, nb, block_table, maxb, b, pb, pe, kind, wi,
+                                        my_lds, xfer, half, npair, lane, n, kg, gpb, ng, wpd,
+                                        pieces != nullptr, ws_o, ws_ml);
+  } else {
 
   const QRegs<TQ> qv = load_q<TQ, FOLD>(query, b, hq, h, rep, n, kg);
   const LaneNib<CPG> ln(n, kg);
@@ -934,6 +1036,7 @@ kivi_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, int hpw, 
   tail::Partial part = acc.finish(ln, kg);
   if (npair == 2) tail::merge_halves(part, xfer, half, lane);
   if (half == 0) store_partial<CPG>(part, wi, hq, h, rep, n, kg, ws_o, ws_ml);
+  }  // CPG 4
   }  // items
 }
 
@@ -1013,6 +1116,20 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
   const bool vg1 = cpg == 8 && g >= 128;
   // a key group per page: its scales are contiguous per head
   const bool ksv = vg1 && bs == g;
+  if (use_pieces) {
+    // whole pages for all kv heads per workgroup where the geometry allows
+    bool coop = false;
+    const int crc = launch_kivi_decode_coop(query, q_dtype, hq, kvh, d, qscale, kq, ks, km, vq,
+                                            vs, vm, bs, g, nb, block_table, maxb, seq_meta, work,
+                                            num_work, pieces, num_pieces, ring_k, ring_v,
+                                            ring_dtype, ring_len, ws_o, ws_ml, s, &coop);
+    if (crc != KVQ_OK) return crc;
+    if (coop) {
+      *launched = true;
+      *tail_done = true;
+      return KVQ_OK;
+    }
+  }
   const int64_t wave_lds = tail ? wave_lds_of<true>(cpg, vg1, ksv) : wave_lds_of<false>(cpg, vg1, ksv);
   int64_t lds_max = 0;  // LDS one workgroup may use on this device
   const int lrc = device_lds_max(&lds_max);

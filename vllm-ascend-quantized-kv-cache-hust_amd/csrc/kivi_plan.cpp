@@ -70,13 +70,13 @@ int64_t slots_for(int kvh, int cu_count) {
   return std::max<int64_t>(1, static_cast<int64_t>(cu_count) * kHeadSlotsPerCu / std::max(1, kvh));
 }
 
-// Cost of the whole batch in int4-position units: int4 ranges in 64-position
+// Cost of the whole batch in int4-position units: int4 ranges in `tile`-position
 // tiles, tail positions at `tail_cost` each.
-double total_cost(const Planner& pl, double tail_cost) {
+double total_cost(const Planner& pl, double tail_cost, int64_t tile = 64) {
   double total = 0;
   for (int64_t b = 0; b < pl.batch; ++b) {
     const int64_t end_a = pl.hist_both(b);
-    total += static_cast<double>(ceil_div(end_a, 64) * 64) +
+    total += static_cast<double>(ceil_div(end_a, tile) * tile) +
              static_cast<double>(pl.seqs[6 * b] - end_a) * tail_cost;
   }
   return total;
@@ -114,15 +114,17 @@ void plan_split(Planner& pl, int64_t split, bool paired) {
 }
 
 // Equal-cost pieces: every request's positions laid end to end (int4 in
-// 64-position tiles, tail in 32-position steps at `tail_cost` per position),
-// cut where the running cost crosses a multiple of total / slots.
-int64_t plan_pieces(Planner& pl, int kvh, int cu_count, double tail_cost, int32_t* pieces,
-                    int64_t cap_pieces) {
+// `tile`-position tiles -- 64, or 128 for the page-streaming kernel, whose
+// workgroups must not share a page -- tail in 32-position steps at `tail_cost`
+// per position), cut where the running cost crosses a multiple of total / slots.
+int64_t plan_pieces(Planner& pl, int kvh, int cu_count, double tail_cost, int64_t tile,
+                    int32_t* pieces, int64_t cap_pieces) {
   int64_t slots = slots_for(kvh, cu_count);
-  const double total = total_cost(pl, tail_cost);
+  const double total = total_cost(pl, tail_cost, tile);
   slots *= std::max<int64_t>(
       1, static_cast<int64_t>(std::ceil(total / (static_cast<double>(slots) * kPieceMaxCost))));
-  const double step = std::max(64.0, total / static_cast<double>(slots));
+  const double dtile = static_cast<double>(tile);
+  const double step = std::max(dtile, total / static_cast<double>(slots));
   int64_t np = 0;
   auto push = [&](int64_t v) {
     if (np >= cap_pieces + 1) {
@@ -146,12 +148,12 @@ int64_t plan_pieces(Planner& pl, int kvh, int cu_count, double tail_cost, int32_
     const int64_t end_a = pl.hist_both(b);
     for (int64_t p = 0; p < end_a;) {
       const int64_t tiles =
-          std::max<int64_t>(1, static_cast<int64_t>((cut - cum) / 64.0 + 0.5));
-      const int64_t e = std::min(end_a, p + 64 * tiles);
+          std::max<int64_t>(1, static_cast<int64_t>((cut - cum) / dtile + 0.5));
+      const int64_t e = std::min(end_a, p + tile * tiles);
       pl.add(b, p, e, 0);
-      cum += static_cast<double>(ceil_div(e - p, 64) * 64);
+      cum += static_cast<double>(ceil_div(e - p, tile) * tile);
       p = e;
-      after(64.0);
+      after(dtile);
     }
     const double unit = 32 * tail_cost;
     for (int64_t p = end_a; p < seq_len;) {
@@ -195,10 +197,13 @@ extern "C" int64_t kvq_plan_kivi_decode(const int32_t* seqs, int64_t batch, int 
     }
   }
   switch (mode) {
-    case KVQ_PLAN_PIECES:
-      if (!pieces || cap_pieces <= 0) return KVQ_ERR_INVALID;
-      *num_pieces = plan_pieces(pl, num_kv_heads, cu_count, tail_cost, pieces, cap_pieces);
+    case KVQ_PLAN_PIECES: {
+      // split_tokens, when given, is the int4 tile: 64 or 128 positions
+      const int64_t tile = split_tokens > 0 ? split_tokens : 64;
+      if (!pieces || cap_pieces <= 0 || (tile != 64 && tile != 128)) return KVQ_ERR_INVALID;
+      *num_pieces = plan_pieces(pl, num_kv_heads, cu_count, tail_cost, tile, pieces, cap_pieces);
       break;
+    }
     case KVQ_PLAN_SPLIT:
     case KVQ_PLAN_SPLIT_PAIRED:
       if (split_tokens <= 0) return KVQ_ERR_INVALID;

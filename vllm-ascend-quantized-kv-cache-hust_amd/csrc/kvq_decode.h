@@ -61,6 +61,22 @@ int launch_kivi_decode_mfma(const void* query, int q_dtype, int hq, int kvh, int
                             float* ws_o, float* ws_ml, hipStream_t s, bool* launched,
                             bool* tail_done);
 
+// The page-streaming decode (decode_coop.hip): given pieces, one workgroup of
+// kvh waves per piece streams whole pages of the piece's int4 items for all kv
+// heads, then runs its tail items.  Applies at kvh 8, head size 128, block
+// size 128, group 64 or 128, GQA groups of at most 16 heads, 16-bit query and
+// ring, a positive finite scale and a device with the ring's LDS; *launched
+// tells the caller whether it ran (every kind then done).
+bool coop_decode_applies(int q_dtype, int hq, int kvh, int d, int ring_dtype, int bs, int g);
+int launch_kivi_decode_coop(const void* query, int q_dtype, int hq, int kvh, int d, float qscale,
+                            const int32_t* kq, const float* ks, const float* km,
+                            const int32_t* vq, const float* vs, const float* vm, int bs, int g,
+                            int64_t nb, const int32_t* block_table, int64_t maxb,
+                            const int32_t* seq_meta, const int32_t* work, int64_t num_work,
+                            const int32_t* pieces, int64_t num_pieces, const void* ring_k,
+                            const void* ring_v, int ring_dtype, int ring_len, float* ws_o,
+                            float* ws_ml, hipStream_t s, bool* launched);
+
 // Standalone MFMA tail kernel for the kind-1 items, for geometries the int4
 // kernel does not cover.  *launched tells the caller whether kind-1 items still
 // need the generic kernel.

@@ -1103,7 +1103,8 @@ class AscendKiviInt4AttentionBackendMixin:
         """The decode step as two launches over one staged plan, or ``None``
         (nothing changed) when it needs the general path."""
         from ...ops.kivi_decode import _cu_count
-        from .decode_step import DecodeStepBuffers, KiviDecodeLauncher, eager_capacities
+        from .decode_step import (DecodeStepBuffers, KiviDecodeLauncher, eager_capacities,
+                                  step_plan_mode)
 
         from ...ops import _native
 
@@ -1127,8 +1128,9 @@ class AscendKiviInt4AttentionBackendMixin:
                                          num_heads=self.num_heads, head_size=self.head_size,
                                          work_cap=2 * work_cap, pieces_cap=2 * pieces_cap)
                 self._kivi_step_bufs = bufs
+            mode, tile = step_plan_mode(self, query, fixed=False)
             staged = bufs.stage(jobs, seqs, num_kv_heads=self.num_kv_heads, cu_count=cu,
-                                mode=_native.KVQ_PLAN_DEFAULT, fixed=False)
+                                mode=mode, fixed=False, tile=tile)
             launcher = KiviDecodeLauncher(self)
             q = query[:b].reshape(b, self.num_heads, self.head_size).contiguous()
             out = output[:b].view(b, self.num_heads, self.head_size)

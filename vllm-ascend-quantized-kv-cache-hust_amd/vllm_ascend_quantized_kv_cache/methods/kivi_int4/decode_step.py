@@ -28,7 +28,13 @@ import numpy as np
 import torch
 
 from ...ops import _native
-from ...ops.kivi_decode import WAVES_PER_CU, plan_into, work_capacity
+from ...ops.kivi_decode import (
+    PAGE_TILE,
+    WAVES_PER_CU,
+    page_streaming_applies,
+    plan_into,
+    work_capacity,
+)
 from .residual import StepJobs
 
 #: int64 words before the store job sections (the four counts)
@@ -111,8 +117,11 @@ class DecodeStepBuffers:
         self._used[i] = True
 
     def stage(self, jobs: StepJobs | None, seqs: np.ndarray, *, num_kv_heads: int,
-              cu_count: int, mode: int, fixed: bool) -> StagedPlan:
+              cu_count: int, mode: int, fixed: bool, tile: int = 0) -> StagedPlan:
         """Write a step's plan to pinned memory and queue its copy to ``plan``.
+
+        ``mode`` / ``tile``: the planner's mode and, for pieces, its int4 tile
+        (``step_plan_mode``).
 
         ``fixed``: the capacity layout, with the unused pieces filled with
         empty ranges, so a launch over all ``pieces_cap`` pieces (a captured
@@ -151,8 +160,8 @@ class DecodeStepBuffers:
             off += cap
         meta = h[meta_off:work_off].view(np.int32).reshape(b, 8)
         work = h[work_off:work_off + work_cap * 16].view(np.int32).reshape(work_cap, 4)
-        n, npc = plan_into(seqs, num_kv_heads, cu_count, mode, meta=meta, work=work,
-                           pieces=self._pieces)
+        n, npc = plan_into(seqs, num_kv_heads, cu_count, mode, split_tokens=tile, meta=meta,
+                           work=work, pieces=self._pieces)
         if fixed:
             if npc == 0:
                 raise RuntimeError("KIVI decode step: a fixed launch needs a plan in pieces.")
@@ -231,6 +240,17 @@ def step_geometry_ok(impl, query: torch.Tensor) -> bool:
     return (impl.head_size == 128 and impl.kivi_group_size in (64, 128)
             and query.dtype in (torch.bfloat16, torch.float16) and ring.dtype == query.dtype
             and impl.num_heads // impl.num_kv_heads <= 16 and bs & (bs - 1) == 0)
+
+
+def step_plan_mode(impl, query: torch.Tensor, *, fixed: bool) -> tuple[int, int]:
+    """``(mode, tile)`` of a decode step's plan: pieces on page bounds where the
+    page-streaming decode covers the layer; else pieces on 64-position tiles
+    for a fixed (captured) launch, the default plan for an eager one."""
+    if page_streaming_applies(impl.num_heads, impl.num_kv_heads, impl.head_size,
+                              impl._get_kivi_block_size(), impl.kivi_group_size, query.dtype,
+                              impl._kivi_ring.dtype):
+        return _native.KVQ_PLAN_PIECES, PAGE_TILE
+    return (_native.KVQ_PLAN_PIECES if fixed else _native.KVQ_PLAN_DEFAULT), 0
 
 
 def pieces_capacity(num_kv_heads: int, cu_count: int, rounds: int) -> int:
@@ -325,9 +345,9 @@ class KiviDecodeGraph:
                     "follow the block table; run it eagerly through forward."
                 )
             jobs, seqs, table_dev = plan
+            mode, tile = step_plan_mode(impl, key, fixed=True)
             staged = self.bufs.stage(jobs, seqs, num_kv_heads=impl.num_kv_heads,
-                                     cu_count=self.cu_count, mode=_native.KVQ_PLAN_PIECES,
-                                     fixed=True)
+                                     cu_count=self.cu_count, mode=mode, fixed=True, tile=tile)
             rows, cols = table_dev.shape
             self.table[:rows, :cols].copy_(table_dev, non_blocking=True)
         self.staged = staged

@@ -32,6 +32,22 @@ TAIL_POSITION_COST = 6.0
 #: largest piece, in int4 positions: more work than one piece per wave slot
 #: of this size runs as several rounds of pieces, dispatched as slots free
 PIECE_MAX_COST = 4096.0
+#: int4 tile of the pieces the page-streaming decode runs: whole pages, so no
+#: two workgroups stream the same page
+PAGE_TILE = 128
+
+
+def page_streaming_applies(num_heads: int, num_kv_heads: int, head_size: int, block_size: int,
+                           group_size: int, q_dtype: torch.dtype, ring_dtype: torch.dtype) -> bool:
+    """The geometry the page-streaming decode covers (``kvq_kivi_decode_attn``
+    given pieces: one workgroup per piece streams whole pages for all kv heads):
+    8 kv heads, head size 128, block size 128, group 64 or 128, at most 16
+    query heads per kv head, a 16-bit query shared with the ring.  Plans for
+    it cut int4 items on page bounds (``PAGE_TILE``)."""
+    return (num_kv_heads == 8 and head_size == 128 and block_size == 128
+            and group_size in (64, 128) and num_heads % num_kv_heads == 0
+            and num_heads // num_kv_heads <= 16
+            and q_dtype in (torch.bfloat16, torch.float16) and ring_dtype == q_dtype)
 
 
 @dataclass(frozen=True)
@@ -133,6 +149,7 @@ def plan_decode_pieces(
     num_kv_heads: int,
     cu_count: int = 256,
     tail_cost: float = TAIL_POSITION_COST,
+    tile: int = 64,
 ) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     """``(seq_meta, work, pieces)``: the work list cut into pieces of equal cost.
 
@@ -143,18 +160,25 @@ def plan_decode_pieces(
     needed to keep pieces under ``PIECE_MAX_COST``: one wave per (piece, kv
     head) then fills the chip a whole number of times and every wave of a
     round ends at about the same time.  A cut inside a request splits it into
-    items (int4 items start on multiples of 64); ``pieces[k]`` is the first
-    item of piece ``k``.  Planned natively (``kvq_plan_kivi_decode``).
+    items (int4 items start on multiples of ``tile``, 64 or ``PAGE_TILE``);
+    ``pieces[k]`` is the first item of piece ``k``.  Planned natively
+    (``kvq_plan_kivi_decode``).
     """
     meta, work, pieces = _plan(seqs, num_kv_heads, cu_count, _native.KVQ_PLAN_PIECES,
-                               tail_cost=tail_cost)
+                               split_tokens=tile, tail_cost=tail_cost)
     return meta, work, (pieces if pieces is not None else np.zeros(1, dtype=np.int32))
 
 
 def plan_decode(
-    seqs: list[DecodeSeq], num_kv_heads: int, cu_count: int = 256
+    seqs: list[DecodeSeq], num_kv_heads: int, cu_count: int = 256, *,
+    page_streaming: bool = False,
 ) -> tuple[np.ndarray, np.ndarray, np.ndarray | None]:
     """The default decode plan: ``(seq_meta, work, pieces or None)``.
+
+    ``page_streaming`` (the layer is one ``page_streaming_applies`` accepts):
+    pieces on page bounds, any amount of work -- a workgroup per piece streams
+    its pages at the memory's pace, and many rounds of equal pieces keep every
+    CU busy to the end.  Otherwise:
 
     Work that fills the chip's wave slots once (pieces of at most
     ``PIECE_MAX_COST``) is cut into equal-cost pieces (``plan_decode_pieces``):
@@ -165,6 +189,8 @@ def plan_decode(
     fill the last round's gaps (measured on 256 x 32K tokens: 2.53 ms, against
     2.60 ms for pairs of 4096-position half items).
     """
+    if page_streaming:
+        return _plan(seqs, num_kv_heads, cu_count, _native.KVQ_PLAN_PIECES, split_tokens=PAGE_TILE)
     return _plan(seqs, num_kv_heads, cu_count, _native.KVQ_PLAN_DEFAULT)
 
 
@@ -203,7 +229,10 @@ def kivi_decode_attention(
     pieces = None
     if plan is None:
         if split_tokens is None:
-            meta_np, work_np, pieces_np = plan_decode(seqs, kvh, _cu_count(query.device))
+            paged = page_streaming_applies(hq, kvh, d, pbs * 8, group_size, query.dtype,
+                                           ring_k.dtype)
+            meta_np, work_np, pieces_np = plan_decode(seqs, kvh, _cu_count(query.device),
+                                                      page_streaming=paged)
             if pieces_np is not None:
                 pieces = torch.from_numpy(pieces_np).to(query.device)
         else:
@@ -253,6 +282,7 @@ __all__ = [
     "DecodeSeq",
     "choose_split_tokens",
     "kivi_decode_attention",
+    "page_streaming_applies",
     "plan_decode",
     "plan_decode_pieces",
     "plan_decode_work",
