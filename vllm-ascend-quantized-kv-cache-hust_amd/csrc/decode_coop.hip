@@ -73,19 +73,28 @@ struct Ring {
   static constexpr int CODES = 32768;   // code bytes of a stage (both kinds)
   // scales + minima of a stage: keys 8 heads x 64 dims x GPB, values 64
   // tokens x 8 heads x NG (equal)
-  static constexpr int KS_HEAD = 2 * 64 * GPB * 4;      // bytes per head (K stage)
+  static constexpr int KS_ONE = 64 * GPB * 4;           // one head's scales (or minima), K stage
+  static constexpr int KS_HEAD = 2 * KS_ONE;            // bytes per head (K stage)
   static constexpr int SCALES = kHeads * KS_HEAD;       // 4 KiB (G 128) / 8 KiB (G 64)
+  static constexpr int KS_HALF = SCALES / 2;            // the minima follow all heads' scales
   static_assert(SCALES == 2 * 64 * kHeads * NG * 4, "key and value stages hold equal scales");
   static constexpr int SLOT = CODES + SCALES;
   static constexpr int BYTES = kSlots * SLOT;
   static constexpr int VS_LANES = SCALES / kHeads / 16;  // 16-byte DMA lanes per wave: 32 / 64
 };
 
-// One counted LDS DMA: 16 bytes per active lane from `g` to LDS byte address
-// m0 + 16 * lane (m0 uniform).  The s_nop covers the M0-write hazard.
-__device__ __forceinline__ void cdma16(const void* g, uint32_t m0) {
+// One counted LDS DMA: 16 bytes per active lane from base + voff + IMM (base
+// uniform, voff the lane's byte offset) to LDS byte address m0 + IMM + 16 *
+// lane (m0 uniform): the instruction offset moves both addresses.  The s_nop
+// covers the M0-write hazard.
+template <int IMM>
+__device__ __forceinline__ void cdma16(const char* base, uint32_t voff, uint32_t m0) {
+  static_assert(IMM >= 0 && IMM < 4096, "instruction offset range");
   m0 = __builtin_amdgcn_readfirstlane(m0);
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(m0) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 offset:%2"
+               :
+               : "v"(voff), "s"(base), "i"(IMM), "{m0}"(m0)
+               : "memory");
 }
 
 // 16-byte load into registers, not tracked by the compiler's wait counts.
@@ -179,13 +188,11 @@ struct KHalf {
 };
 
 template <int G, bool FOLD, int P>
-__device__ __forceinline__ void prepare_half(const char* scales_h, int grp, int n, int kg,
-                                             const tr::QLane<float>& ql, KHalf& kh) {
+__device__ __forceinline__ void prepare_half(const float* ksf, const float* kmf, int grp, int n,
+                                             int kg, const tr::QLane<float>& ql, KHalf& kh) {
 #pragma clang fp contract(fast)
   constexpr int GPB = Ring<G>::GPB;
-  // [scale: 64 dims x GPB][min: 64 dims x GPB] floats of this head and stage
-  const float* ksf = reinterpret_cast<const float*>(scales_h);
-  const float* kmf = ksf + 64 * GPB;
+  // ksf / kmf: [64 dims x GPB] scales / minima of this head and stage
   const float nsel = (FOLD && n >= 8) ? -1.0f : 0.0f;
   const h2 one2 = h2{1.0f16, 1.0f16};
   float kb_u[2], kb_p[2], off[2];
@@ -256,7 +263,9 @@ __device__ __forceinline__ void key_stage(const char* slot, int h, int n, int kg
 #pragma unroll
   for (int jm = 0; jm < 8; ++jm)
     rk[jm] = tr::read_tr4(base + (krel ^ (16u * (jm >> 1))) + 8u * (jm & 1));
-  const char* scales_h = slot + Ring<G>::CODES + Ring<G>::KS_HEAD * h;
+  // [scales: head x 64 dims x GPB][minima: same]
+  const float* ksf = reinterpret_cast<const float*>(slot + Ring<G>::CODES + Ring<G>::KS_ONE * h);
+  const float* kmf = ksf + Ring<G>::KS_HALF / 4;
   if (P == 0) {
 #pragma unroll
     for (int jm = 0; jm < 8; ++jm) st.sacc[jm] = f4{0.f, 0.f, 0.f, 0.f};
@@ -264,7 +273,7 @@ __device__ __forceinline__ void key_stage(const char* slot, int h, int n, int kg
 #pragma unroll
   for (int grp = 0; grp < GPB; ++grp) {
     KHalf kh;
-    prepare_half<G, FOLD, P>(scales_h, grp, n, kg, ql, kh);
+    prepare_half<G, FOLD, P>(ksf, kmf, grp, n, kg, ql, kh);
     st.kb[grp] = P == 0 ? kh.kb : st.kb[grp] + kh.kb;
     // the token blocks of key group grp: jm in [grp * 8 / GPB, (grp + 1) * 8 / GPB)
 #pragma unroll
@@ -519,52 +528,68 @@ kivi_decode_coop_kernel(const TQ* __restrict__ query, int hq, float qscale,
     return ln;
   };
 
-  // Stage DMAs of wave h.
+  // Stage DMAs of wave h: a uniform base plus the lane offsets below, fixed for
+  // the kernel (five registers), so a stage costs no vector arithmetic.
   //   K stage, instruction i (0..3): dim 16 i + (lane >> 2) of head h's run,
   //     chunk (lane & 3) ^ ((lane >> 3) & 3) of its 64-byte row;
+  //   K scales: waves 0..3 copy the scales of heads 2 w, 2 w + 1, waves 4..7
+  //     their minima (two runs of 64 GPB floats, 128 GPB floats apart);
   //   V stage, instruction i: token 8 h + 2 i + (lane >> 5) of the stage, chunk
-  //     (lane & 31) ^ psi(token); psi depends on the token's low two bits and bit 4;
-  //   scales: wave h's 16-byte slice of the stage's [scale | min] runs.
-  auto issue_stage = [&](const Cursor<true>& c, int slot, int lane) {
+  //     (lane & 31) ^ psi(token), psi(t) = (t & 3) | (((t >> 4) & 1) << 2),
+  //     which repeats for i and i + 2;
+  //   V scales: wave h's quarter of the stage's scale (h < 4) or minimum
+  //     (h >= 4) run.
+  constexpr int HALF = R::KS_ONE / 16;  // lanes per head run of K scales: 16 / 32
+  static_assert(2 * HALF <= 64 && R::VS_LANES <= 64, "one DMA instruction per scale run");
+  constexpr int VARR = 64 * kHeads * R::NG * 4;  // bytes per value scale (or minimum) run
+  static_assert(4 * 16 * R::VS_LANES == VARR, "four waves cover each value scale run");
+  const uint32_t k_lane = 64u * (lane0 >> 2) + 16u * ((lane0 & 3) ^ ((lane0 >> 3) & 3));
+  const uint32_t ks_lane =
+      16u * (lane0 % HALF) + (lane0 >= HALF ? static_cast<uint32_t>(2 * R::KS_ONE) : 0u);
+  uint32_t v_lane[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int t = 8 * h + 2 * i + (lane0 >> 5);  // token within the stage
+    const int psi = (t & 3) | (((t >> 4) & 1) << 2);
+    v_lane[i] = 512u * static_cast<uint32_t>(t) + 16u * static_cast<uint32_t>((lane0 & 31) ^ psi);
+  }
+  const uint32_t vs_lane = 16u * lane0;
+  const int hp = h & 3;  // K scales: the head pair 2 hp, 2 hp + 1; V scales: the quarter
+  const float* k_arr = h < 4 ? ks : km;
+  const float* v_arr = h < 4 ? vs : vm;
+  auto issue_stage = [&](const Cursor<true>& c, int slot) {
     const int64_t blk = c.blk;
     const uint32_t sbase = ring0 + static_cast<uint32_t>(slot * R::SLOT);
     if (c.stage < 2) {  // K0 / K1: head h's dims 64 P .. 64 P + 63
       const int P = c.stage;
       const int64_t row = (blk * kHeads + h) * kD + 64 * P;  // (page, head, dim) row
-      const uint32_t k_lane = 64u * (lane >> 2) + 16u * ((lane & 3) ^ ((lane >> 3) & 3));
-      const char* src = reinterpret_cast<const char*>(kq + row * wpd) + k_lane;
+      const char* src = reinterpret_cast<const char*>(kq + row * wpd);
       const uint32_t dst = sbase + 4096u * h;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) cdma16(src + 1024 * i, dst + 1024u * i);
-      // scales then minima of those dims: 64 * GPB floats each
-      const int64_t srow = row * R::GPB;
-      const uint32_t sdst = sbase + R::CODES + R::KS_HEAD * h;
-      constexpr int HALF = R::KS_HEAD / 2 / 16;  // lanes per array: 16 / 32
-      if (lane < 2 * HALF) {
-        const float* arr = lane < HALF ? ks : km;
-        cdma16(reinterpret_cast<const char*>(arr + srow) + 16 * (lane % HALF), sdst);
-      }
+      cdma16<0>(src, k_lane, dst);
+      cdma16<1024>(src, k_lane, dst);
+      cdma16<2048>(src, k_lane, dst);
+      cdma16<3072>(src, k_lane, dst);
+      // scales (or minima) of heads 2 hp, 2 hp + 1, dims 64 P .. 64 P + 63
+      const int64_t srow = ((blk * kHeads + 2 * hp) * kD + 64 * P) * R::GPB;
+      if (lane0 < 2 * HALF)
+        cdma16<0>(reinterpret_cast<const char*>(k_arr + srow), ks_lane,
+                  sbase + R::CODES + (h < 4 ? 0u : static_cast<uint32_t>(R::KS_HALF)) +
+                      static_cast<uint32_t>(2 * R::KS_ONE * hp));
     } else {  // V0 / V1: tokens 64 U .. 64 U + 63, waves take 8 tokens each
       const int U = c.stage - 2;
       const int64_t tok0 = blk * kPage + 64 * U;  // first token of the stage
-      const int t_hi = lane >> 5;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 8 * h + 2 * i + t_hi;  // token within the stage
-        const int psi = (t & 3) | (((t >> 4) & 1) << 2);
-        const uint32_t chunk = static_cast<uint32_t>((lane & 31) ^ psi);
-        const char* src = reinterpret_cast<const char*>(vq + (tok0 + t) * kHeads * 16) + 16 * chunk;
-        cdma16(src, sbase + 1024u * (4 * h + i));
-      }
-      // [scale: 64 tok x 8 heads x NG][min: same], wave h's slice of VS_LANES lanes
-      constexpr int ARR = 64 * kHeads * R::NG * 4;  // bytes per array
-      const int off = R::VS_LANES * 16 * h;         // byte offset of the slice in [scale | min]
-      if (lane < R::VS_LANES) {
-        const int o = off + 16 * lane;
-        const float* arr = o < ARR ? vs : vm;
-        cdma16(reinterpret_cast<const char*>(arr + tok0 * kHeads * R::NG) + (o % ARR),
-               sbase + R::CODES + static_cast<uint32_t>(off));
-      }
+      const char* src = reinterpret_cast<const char*>(vq + tok0 * kHeads * 16);
+      const uint32_t dst = sbase + 4096u * h;
+      // v_lane[1] already holds instruction 1's two tokens; i + 2 adds four
+      cdma16<0>(src, v_lane[0], dst);
+      cdma16<0>(src, v_lane[1], dst + 1024u);
+      cdma16<2048>(src, v_lane[0], dst);
+      cdma16<2048>(src, v_lane[1], dst + 1024u);
+      // [scale: 64 tok x 8 heads x NG][min: same]: wave h's quarter of one run
+      if (lane0 < R::VS_LANES)
+        cdma16<0>(reinterpret_cast<const char*>(v_arr + tok0 * kHeads * R::NG) +
+                      16 * R::VS_LANES * hp,
+                  vs_lane, sbase + R::CODES + static_cast<uint32_t>(16 * R::VS_LANES * h));
     }
   };
 
@@ -583,7 +608,7 @@ kivi_decode_coop_kernel(const TQ* __restrict__ query, int hq, float qscale,
     for (int j = 0; j < 3 && j < total; ++j) {
       if (j > 0 && ic.item_first())
         q_next = issue_q<TQ>(query, ic.b, hq, h, rep, lane0 & 15, lane0 >> 4, FOLD);
-      issue_stage(ic, j, lane0);
+      issue_stage(ic, j);
       ic.advance();
     }
     tr::QLane<float> ql;
@@ -602,7 +627,7 @@ kivi_decode_coop_kernel(const TQ* __restrict__ query, int hq, float qscale,
       const int ln = fresh_lane();
       if (i + 3 < total) {
         if (ic.item_first()) q_next = issue_q<TQ>(query, ic.b, hq, h, rep, ln & 15, ln >> 4, FOLD);
-        issue_stage(ic, (i + 3) & 3, ln);
+        issue_stage(ic, (i + 3) & 3);
         ic.advance();
       }
       return ln;
