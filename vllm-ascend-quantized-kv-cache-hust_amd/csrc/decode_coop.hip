@@ -58,7 +58,8 @@ using tr::h2;
 using tr::h8;
 using tr::v2i;
 
-constexpr int kHeads = 8;    // kv heads per workgroup, one wave each
+constexpr int kKvHeads = 8;  // kv heads of the layer
+constexpr int kWaves = 4;    // kv heads per workgroup, one wave each: two workgroups a piece
 constexpr int kPage = 128;   // positions per page (block size)
 constexpr int kD = 128;      // head size
 constexpr int kStages = 4;   // stages per page: K0, K1, V0, V1
@@ -70,17 +71,16 @@ template <int G>
 struct Ring {
   static constexpr int NG = kD / G;     // value groups per head row
   static constexpr int GPB = kPage / G; // key groups per page
-  static constexpr int CODES = 32768;   // code bytes of a stage (both kinds)
-  // scales + minima of a stage: keys 8 heads x 64 dims x GPB, values 64
-  // tokens x 8 heads x NG (equal)
+  static constexpr int CODES = 16384;   // code bytes of a stage (both kinds), 4 heads
+  // scales + minima of a stage: keys 4 heads x 64 dims x GPB, values 64
+  // tokens x 4 heads x NG (equal)
   static constexpr int KS_ONE = 64 * GPB * 4;           // one head's scales (or minima), K stage
-  static constexpr int KS_HEAD = 2 * KS_ONE;            // bytes per head (K stage)
-  static constexpr int SCALES = kHeads * KS_HEAD;       // 4 KiB (G 128) / 8 KiB (G 64)
-  static constexpr int KS_HALF = SCALES / 2;            // the minima follow all heads' scales
-  static_assert(SCALES == 2 * 64 * kHeads * NG * 4, "key and value stages hold equal scales");
+  static constexpr int KS_HALF = kWaves * KS_ONE;       // the minima follow all heads' scales
+  static constexpr int SCALES = 2 * KS_HALF;            // 2 KiB (G 128) / 4 KiB (G 64)
+  static_assert(SCALES == 2 * 64 * kWaves * NG * 4, "key and value stages hold equal scales");
   static constexpr int SLOT = CODES + SCALES;
-  static constexpr int BYTES = kSlots * SLOT;
-  static constexpr int VS_LANES = SCALES / kHeads / 16;  // 16-byte DMA lanes per wave: 32 / 64
+  static constexpr int BYTES = kSlots * SLOT;           // 72 / 80 KiB: two workgroups a CU
+  static constexpr int VS_LANES = SCALES / kWaves / 16;  // 16-byte DMA lanes per wave: 32 / 64
 };
 
 // One counted LDS DMA: 16 bytes per active lane from base + voff + IMM (base
@@ -250,21 +250,22 @@ struct WaveState {
 };
 
 template <int G, bool FOLD, int P>
-__device__ __forceinline__ void key_stage(const char* slot, int h, int n, int kg,
+__device__ __forceinline__ void key_stage(const char* slot, int w, int n, int kg,
                                           const tr::QLane<float>& ql, WaveState<G, FOLD>& st) {
 #pragma clang fp contract(fast)
   constexpr int GPB = Ring<G>::GPB;
   const tr::Consts cst;
   const uint32_t base = tr::lds_off(slot);
-  // keys of head h: [dim 0..63][64 B], 16-byte chunk c of dim d at c ^ ((d >> 1) & 3)
+  // keys of the workgroup's head w: [dim 0..63][64 B], 16-byte chunk c of dim d
+  // at c ^ ((d >> 1) & 3)
   const int d = 16 * kg + n;
-  const uint32_t krel = 4096u * h + 64u * d + 16u * ((d >> 1) & 3);
+  const uint32_t krel = 4096u * w + 64u * d + 16u * ((d >> 1) & 3);
   v2i rk[8];
 #pragma unroll
   for (int jm = 0; jm < 8; ++jm)
     rk[jm] = tr::read_tr4(base + (krel ^ (16u * (jm >> 1))) + 8u * (jm & 1));
   // [scales: head x 64 dims x GPB][minima: same]
-  const float* ksf = reinterpret_cast<const float*>(slot + Ring<G>::CODES + Ring<G>::KS_ONE * h);
+  const float* ksf = reinterpret_cast<const float*>(slot + Ring<G>::CODES + Ring<G>::KS_ONE * w);
   const float* kmf = ksf + Ring<G>::KS_HALF / 4;
   if (P == 0) {
 #pragma unroll
@@ -373,25 +374,25 @@ __device__ __forceinline__ void page_softmax(int page_pos, int pb, int pe, int k
 // PV over the stage's 64 tokens (U = 0: tokens 0..63 of the page, 1: 64..127).
 // FULL: all 64 positions are in [pb, pe).
 template <int G, bool FOLD, int U, bool FULL>
-__device__ __forceinline__ void value_stage(const char* slot, int h, int n, int kg, int page_pos,
+__device__ __forceinline__ void value_stage(const char* slot, int w, int n, int kg, int page_pos,
                                             int pb, int pe, WaveState<G, FOLD>& st) {
 #pragma clang fp contract(fast)
   constexpr int NG = Ring<G>::NG;
   const tr::Consts cst;
   const uint32_t base = tr::lds_off(slot);
-  // values: token t's 16-byte chunk q (= 4 head + dim block / 2) at q ^ psi(t),
-  // psi(t) = (t & 3) | (((t >> 4) & 1) << 2); lane (kg, n) names token tau(kg, n),
-  // whose psi is n & 7
+  // values: 256-byte token rows (the workgroup's 4 heads x 64 B); token t's
+  // 16-byte chunk q (= 4 head + dim block / 2) at q ^ psi(t), psi(t) = (t & 3) |
+  // (((t >> 4) & 3) << 2); lane (kg, n) names token tau(kg, n), whose psi is n,
+  // so a lane group's 16 reads land on 16 different chunks of a row
   const int t = tr::tau(kg, n);
-  const uint32_t lane_base = base + 512u * t;
-  const uint32_t psi16 = 16u * (n & 7);
+  const uint32_t lane_base = base + 256u * t;
   v2i rv[8];
 #pragma unroll
   for (int v = 0; v < 8; ++v)
-    rv[v] = tr::read_tr4(lane_base + ((64u * h + 16u * (v >> 1)) ^ psi16) + 8u * (v & 1));
-  // value scales / minima: [token 0..63][head 0..7][NG] floats
+    rv[v] = tr::read_tr4(lane_base + 16u * ((4u * w + (v >> 1)) ^ n) + 8u * (v & 1));
+  // value scales / minima: [token 0..63][head 0..3][NG] floats
   const float* vsf = reinterpret_cast<const float*>(slot + Ring<G>::CODES);
-  const float* vmf = vsf + 64 * kHeads * NG;
+  const float* vmf = vsf + 64 * kWaves * NG;
   const h8 ones_b = tr::as_h8(tr::kMagic, tr::kMagic, tr::kMagic, tr::kMagic);
   const h2 sixteenth = h2{0.0625f16, 0.0625f16};
 #pragma unroll
@@ -410,8 +411,8 @@ __device__ __forceinline__ void value_stage(const char* slot, int h, int n, int 
       for (int vg = 0; vg < NG; ++vg) {
         // past the item p = 0, but the bytes may be unwritten: select zeros so a
         // stale NaN cannot reach the sums
-        const float sv0 = vsf[(tt * kHeads + h) * NG + vg];
-        const float mv0 = vmf[(tt * kHeads + h) * NG + vg];
+        const float sv0 = vsf[(tt * kWaves + w) * NG + vg];
+        const float mv0 = vmf[(tt * kWaves + w) * NG + vg];
         const float sv = live ? sv0 : 0.0f;
         const float mv = live ? mv0 : 0.0f;
         pp[vg][i] = p * sv;
@@ -496,7 +497,7 @@ struct Cursor {
 };
 
 template <typename TQ, int G, bool FOLD>
-__global__ void __launch_bounds__(512, 1)
+__global__ void __launch_bounds__(64 * kWaves, 2)
 kivi_decode_coop_kernel(const TQ* __restrict__ query, int hq, float qscale,
                         const uint32_t* __restrict__ kq, const float* __restrict__ ks,
                         const float* __restrict__ km, const uint32_t* __restrict__ vq,
@@ -508,11 +509,18 @@ kivi_decode_coop_kernel(const TQ* __restrict__ query, int hq, float qscale,
                         int ring_len, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   using R = Ring<G>;
   extern __shared__ __align__(16) char lds_raw[];
-  const int k = blockIdx.x;
+  // Workgroup b runs half (b >> 3) & 1 of the kv heads of piece ((b >> 4) << 3)
+  // | (b & 7): the two halves of a piece get the same b % 8, which places them
+  // on one XCD, where the value scale lines they share meet in its L2.
+  const int bx = blockIdx.x;
+  const int half = (bx >> 3) & 1;
+  const int64_t k = (static_cast<int64_t>(bx >> 4) << 3) | (bx & 7);
   if (k >= num_pieces) return;  // workgroup-uniform
   const int lane0 = threadIdx.x & 63;
-  const int h = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // kv head = wave
-  const int rep = hq / kHeads;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the wave's head of the half
+  const int hb = kWaves * half;                                     // the half's first kv head
+  const int h = hb + w;                                             // the wave's kv head
+  const int rep = hq / kKvHeads;
   const int wpd = kPage / 8;           // key words per (page, head, dim) row
   cint32* cwork = as_const(work);
   cint32* ctable = as_const(block_table);
@@ -528,68 +536,73 @@ kivi_decode_coop_kernel(const TQ* __restrict__ query, int hq, float qscale,
     return ln;
   };
 
-  // Stage DMAs of wave h: a uniform base plus the lane offsets below, fixed for
-  // the kernel (five registers), so a stage costs no vector arithmetic.
+  // Stage DMAs of wave w (kv head h = hb + w): a uniform base plus lane offsets
+  // fixed for the kernel, so a stage costs no vector arithmetic.  The
+  // instruction offset moves the global and the LDS address alike.
   //   K stage, instruction i (0..3): dim 16 i + (lane >> 2) of head h's run,
   //     chunk (lane & 3) ^ ((lane >> 3) & 3) of its 64-byte row;
-  //   K scales: waves 0..3 copy the scales of heads 2 w, 2 w + 1, waves 4..7
-  //     their minima (two runs of 64 GPB floats, 128 GPB floats apart);
-  //   V stage, instruction i: token 8 h + 2 i + (lane >> 5) of the stage, chunk
-  //     (lane & 31) ^ psi(token), psi(t) = (t & 3) | (((t >> 4) & 1) << 2),
-  //     which repeats for i and i + 2;
-  //   V scales: wave h's quarter of the stage's scale (h < 4) or minimum
-  //     (h >= 4) run.
+  //   K scales: waves 0, 1 copy the scales of heads hb + 2 w', hb + 2 w' + 1
+  //     (w' = w & 1), waves 2, 3 their minima (two runs of 64 GPB floats, 128
+  //     GPB floats apart);
+  //   V stage, instruction i: token 16 w + 4 i + (lane >> 4) of the stage, the
+  //     half's 256 bytes of the token row, chunk (lane & 15) ^ psi(token), psi =
+  //     (lane >> 4) | (w << 2) for all four instructions;
+  //   V scales: waves 0, 1 copy the scales of tokens 32 w' .. 32 w' + 31 (the
+  //     half's 4 NG floats of each), waves 2, 3 their minima.
   constexpr int HALF = R::KS_ONE / 16;  // lanes per head run of K scales: 16 / 32
   static_assert(2 * HALF <= 64 && R::VS_LANES <= 64, "one DMA instruction per scale run");
-  constexpr int VARR = 64 * kHeads * R::NG * 4;  // bytes per value scale (or minimum) run
-  static_assert(4 * 16 * R::VS_LANES == VARR, "four waves cover each value scale run");
+  constexpr int VARR = 64 * kWaves * R::NG * 4;  // bytes per value scale (or minimum) run
+  static_assert(2 * 16 * R::VS_LANES == VARR, "two waves cover each value scale run");
   const uint32_t k_lane = 64u * (lane0 >> 2) + 16u * ((lane0 & 3) ^ ((lane0 >> 3) & 3));
   const uint32_t ks_lane =
       16u * (lane0 % HALF) + (lane0 >= HALF ? static_cast<uint32_t>(2 * R::KS_ONE) : 0u);
-  uint32_t v_lane[2];
+  uint32_t v_lane[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int t = 8 * h + 2 * i + (lane0 >> 5);  // token within the stage
-    const int psi = (t & 3) | (((t >> 4) & 1) << 2);
-    v_lane[i] = 512u * static_cast<uint32_t>(t) + 16u * static_cast<uint32_t>((lane0 & 31) ^ psi);
+  for (int i = 0; i < 4; ++i) {
+    const int t = 16 * w + 4 * i + (lane0 >> 4);  // token within the stage
+    const int psi = (t & 3) | (((t >> 4) & 3) << 2);
+    v_lane[i] = 512u * static_cast<uint32_t>(t) + 256u * static_cast<uint32_t>(half) +
+                16u * static_cast<uint32_t>((lane0 & 15) ^ psi);
   }
-  const uint32_t vs_lane = 16u * lane0;
-  const int hp = h & 3;  // K scales: the head pair 2 hp, 2 hp + 1; V scales: the quarter
-  const float* k_arr = h < 4 ? ks : km;
-  const float* v_arr = h < 4 ? vs : vm;
+  const int wp = w & 1;  // K scales: the head pair hb + 2 wp, + 1; V scales: the token half
+  // V scales: token 32 wp + lane / NG, its 16-byte part lane % NG
+  const uint32_t vs_lane = static_cast<uint32_t>(
+      32 * R::NG * (32 * wp + lane0 / R::NG) + 16 * (lane0 % R::NG));
+  const float* k_arr = w < 2 ? ks : km;
+  const float* v_arr = w < 2 ? vs : vm;
   auto issue_stage = [&](const Cursor<true>& c, int slot) {
     const int64_t blk = c.blk;
     const uint32_t sbase = ring0 + static_cast<uint32_t>(slot * R::SLOT);
     if (c.stage < 2) {  // K0 / K1: head h's dims 64 P .. 64 P + 63
       const int P = c.stage;
-      const int64_t row = (blk * kHeads + h) * kD + 64 * P;  // (page, head, dim) row
+      const int64_t row = (blk * kKvHeads + h) * kD + 64 * P;  // (page, head, dim) row
       const char* src = reinterpret_cast<const char*>(kq + row * wpd);
-      const uint32_t dst = sbase + 4096u * h;
+      const uint32_t dst = sbase + 4096u * w;
       cdma16<0>(src, k_lane, dst);
       cdma16<1024>(src, k_lane, dst);
       cdma16<2048>(src, k_lane, dst);
       cdma16<3072>(src, k_lane, dst);
-      // scales (or minima) of heads 2 hp, 2 hp + 1, dims 64 P .. 64 P + 63
-      const int64_t srow = ((blk * kHeads + 2 * hp) * kD + 64 * P) * R::GPB;
+      // scales (or minima) of heads hb + 2 wp, + 1, dims 64 P .. 64 P + 63
+      const int64_t srow = ((blk * kKvHeads + hb + 2 * wp) * kD + 64 * P) * R::GPB;
       if (lane0 < 2 * HALF)
         cdma16<0>(reinterpret_cast<const char*>(k_arr + srow), ks_lane,
-                  sbase + R::CODES + (h < 4 ? 0u : static_cast<uint32_t>(R::KS_HALF)) +
-                      static_cast<uint32_t>(2 * R::KS_ONE * hp));
-    } else {  // V0 / V1: tokens 64 U .. 64 U + 63, waves take 8 tokens each
+                  sbase + R::CODES + (w < 2 ? 0u : static_cast<uint32_t>(R::KS_HALF)) +
+                      static_cast<uint32_t>(2 * R::KS_ONE * wp));
+    } else {  // V0 / V1: tokens 64 U .. 64 U + 63, waves take 16 tokens each
       const int U = c.stage - 2;
       const int64_t tok0 = blk * kPage + 64 * U;  // first token of the stage
-      const char* src = reinterpret_cast<const char*>(vq + tok0 * kHeads * 16);
-      const uint32_t dst = sbase + 4096u * h;
-      // v_lane[1] already holds instruction 1's two tokens; i + 2 adds four
+      const char* src = reinterpret_cast<const char*>(vq + tok0 * kKvHeads * 16);
+      const uint32_t dst = sbase + 4096u * w;
       cdma16<0>(src, v_lane[0], dst);
       cdma16<0>(src, v_lane[1], dst + 1024u);
-      cdma16<2048>(src, v_lane[0], dst);
-      cdma16<2048>(src, v_lane[1], dst + 1024u);
-      // [scale: 64 tok x 8 heads x NG][min: same]: wave h's quarter of one run
+      cdma16<0>(src, v_lane[2], dst + 2048u);
+      cdma16<0>(src, v_lane[3], dst + 3072u);
+      // [scale: 64 tok x 4 heads x NG][min: same]: wave w's token half of one run
       if (lane0 < R::VS_LANES)
-        cdma16<0>(reinterpret_cast<const char*>(v_arr + tok0 * kHeads * R::NG) +
-                      16 * R::VS_LANES * hp,
-                  vs_lane, sbase + R::CODES + static_cast<uint32_t>(16 * R::VS_LANES * h));
+        cdma16<0>(reinterpret_cast<const char*>(v_arr + (tok0 * kKvHeads + hb) * R::NG),
+                  vs_lane,
+                  sbase + R::CODES + (w < 2 ? 0u : static_cast<uint32_t>(VARR)) +
+                      static_cast<uint32_t>(16 * R::VS_LANES * wp));
     }
   };
 
@@ -649,13 +662,13 @@ kivi_decode_coop_kernel(const TQ* __restrict__ query, int hq, float qscale,
         ql = unpack_q<TQ>(q_next, (FOLD ? (n & 7) : n) < rep);
         st.acc.init();
       }
-      key_stage<G, FOLD, 0>(lds_raw, h, n, kg, ql, st);
+      key_stage<G, FOLD, 0>(lds_raw, w, n, kg, ql, st);
       end_stage();
       // K1: dims 64..127, then the page's softmax
       ln = begin_stage(i0 + 1);
       n = ln & 15;
       kg = ln >> 4;
-      key_stage<G, FOLD, 1>(lds_raw + R::SLOT, h, n, kg, ql, st);
+      key_stage<G, FOLD, 1>(lds_raw + R::SLOT, w, n, kg, ql, st);
       if (page_pos >= pb && page_pos + kPage <= pe)  // uniform
         page_softmax<G, FOLD, true>(page_pos, pb, pe, kg, qscale, st);
       else
@@ -666,18 +679,18 @@ kivi_decode_coop_kernel(const TQ* __restrict__ query, int hq, float qscale,
       n = ln & 15;
       kg = ln >> 4;
       if (page_pos >= pb && page_pos + 64 <= pe)
-        value_stage<G, FOLD, 0, true>(lds_raw + 2 * R::SLOT, h, n, kg, page_pos, pb, pe, st);
+        value_stage<G, FOLD, 0, true>(lds_raw + 2 * R::SLOT, w, n, kg, page_pos, pb, pe, st);
       else
-        value_stage<G, FOLD, 0, false>(lds_raw + 2 * R::SLOT, h, n, kg, page_pos, pb, pe, st);
+        value_stage<G, FOLD, 0, false>(lds_raw + 2 * R::SLOT, w, n, kg, page_pos, pb, pe, st);
       end_stage();
       // V1: tokens 64..127
       ln = begin_stage(i0 + 3);
       n = ln & 15;
       kg = ln >> 4;
       if (page_pos + 64 >= pb && page_pos + kPage <= pe)
-        value_stage<G, FOLD, 1, true>(lds_raw + 3 * R::SLOT, h, n, kg, page_pos, pb, pe, st);
+        value_stage<G, FOLD, 1, true>(lds_raw + 3 * R::SLOT, w, n, kg, page_pos, pb, pe, st);
       else
-        value_stage<G, FOLD, 1, false>(lds_raw + 3 * R::SLOT, h, n, kg, page_pos, pb, pe, st);
+        value_stage<G, FOLD, 1, false>(lds_raw + 3 * R::SLOT, w, n, kg, page_pos, pb, pe, st);
       end_stage();
       if (cc.pg == cc.pg_end - 1) {  // the item's last page
         tr::Acc<Ring<G>::NG>& acc = st.acc;
@@ -691,11 +704,11 @@ kivi_decode_coop_kernel(const TQ* __restrict__ query, int hq, float qscale,
   }
 
   // ---- phase 2: the piece's tail items, one wave per kv head ----------------------
-  char* my_lds = lds_raw + h * tail::kLdsBytes;
+  char* my_lds = lds_raw + w * tail::kLdsBytes;
   for (int wi = it0; wi < it1; ++wi) {
     const int32_t* wk = work + 4 * static_cast<int64_t>(wi);
     if (wk[3] == 0 && wk[2] > wk[1]) continue;  // int4 items ran above
-    tail::Partial tp = tail::tail_item<TQ>(my_lds, query, hq, kHeads, qscale, kq, ks, km, vq,
+    tail::Partial tp = tail::tail_item<TQ>(my_lds, query, hq, kKvHeads, qscale, kq, ks, km, vq,
                                            vs, vm, kPage, G, nb, block_table, maxb, seq_meta,
                                            wk, wi, h, ring_k, ring_v, ring_len, 0, 1);
     tail::tail_store(tp, wi, hq, h, rep, lane0, ws_o, ws_ml);
@@ -707,7 +720,7 @@ kivi_decode_coop_kernel(const TQ* __restrict__ query, int hq, float qscale,
 namespace kvq {
 
 bool coop_decode_applies(int q_dtype, int hq, int kvh, int d, int ring_dtype, int bs, int g) {
-  return kvh == kHeads && d == kD && bs == kPage && (g == 64 || g == 128) &&
+  return kvh == kKvHeads && d == kD && bs == kPage && (g == 64 || g == 128) &&
          hq % kvh == 0 && hq / kvh <= 16 && tail_path_applies(q_dtype, hq, kvh, d, ring_dtype, bs);
 }
 
@@ -728,11 +741,12 @@ int launch_kivi_decode_coop(const void* query, int q_dtype, int hq, int kvh, int
   const int lrc = device_lds_max(&lds_max);
   if (lrc != KVQ_OK) return lrc;
   const int ring = g == 64 ? Ring<64>::BYTES : Ring<128>::BYTES;
-  static_assert(kHeads * tail::kLdsBytes <= Ring<128>::BYTES, "the tail items fit the ring");
+  static_assert(kWaves * tail::kLdsBytes <= Ring<128>::BYTES, "the tail items fit the ring");
   if (ring > lds_max) return KVQ_OK;  // not this device: the per-wave kernels run
-  if (num_pieces > 0x7fffffff) return KVQ_ERR_INVALID;
-  const dim3 grid(static_cast<unsigned>(num_pieces));
-  const dim3 block(64 * kHeads);
+  if (num_pieces > (int64_t{1} << 26)) return KVQ_ERR_INVALID;
+  // two workgroups (kv head halves) a piece, in groups of 8 pieces
+  const dim3 grid(static_cast<unsigned>(16 * ((num_pieces + 7) / 8)));
+  const dim3 block(64 * kWaves);
   const bool fold = hq / kvh <= 8;
   const uint32_t* kqu = reinterpret_cast<const uint32_t*>(kq);
   const uint32_t* vqu = reinterpret_cast<const uint32_t*>(vq);
