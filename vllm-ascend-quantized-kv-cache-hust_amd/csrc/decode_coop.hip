@@ -184,7 +184,7 @@ __device__ __forceinline__ tr::QLane<float> unpack_q(const QRaw& q, bool live) {
 // group's minima / offset term (summed over both K stages, then scaled).
 struct KHalf {
   h8 bq[2], bl[2];
-  float kb;  // sum_d q * mn - 1024 * sum_primed Q' over this stage's dims (unscaled)
+  float kb;  // sum_d q * mn - 1024 * sum_d Q' over this stage's dims (unscaled)
 };
 
 template <int G, bool FOLD, int P>
@@ -219,14 +219,12 @@ __device__ __forceinline__ void prepare_half(const float* ksf, const float* kmf,
       const uint32_t hi = tr::pack_h2(x0, x1);
       if (FOLD) {
         ph[p] = tr::pack_h2(tr::sub_half_sel<0>(x0, hi, nsel), tr::sub_half_sel<1>(x1, hi, nsel));
-        if (p & 1) off[e] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ph[p]), one2, off[e], false);
+        off[e] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ph[p]), one2, off[e], false);
       } else {
         ph[p] = hi;
         pl[p] = tr::pack_h2(tr::sub_half_sel<0>(x0, hi, -1.0f), tr::sub_half_sel<1>(x1, hi, -1.0f));
-        if (p & 1) {
-          off[e] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ph[p]), one2, off[e], false);
-          off[e] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pl[p]), one2, off[e], false);
-        }
+        off[e] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ph[p]), one2, off[e], false);
+        off[e] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pl[p]), one2, off[e], false);
       }
     }
     kh.bq[e] = tr::as_h8(ph[0], ph[1], ph[2], ph[3]);
@@ -234,6 +232,8 @@ __device__ __forceinline__ void prepare_half(const float* ksf, const float* kmf,
   }
   // primed q are q / 16: their minima term is 16 * kb_p
   const float kb = tr::sum_kg((kb_u[0] + kb_u[1]) + 16.0f * (kb_p[0] + kb_p[1]));
+  // every code slot holds 1024 + c (primed: 1024 + 16 c against Q' / 16): the
+  // MFMA sums carry 1024 * sum Q', removed here rather than per code
   float offs = tr::sum_kg(off[0] + off[1]);
   if (FOLD) offs = tr::add_ror8(offs);  // hi column + lo column of the head
   kh.kb = kb - 1024.0f * offs;
@@ -282,7 +282,7 @@ __device__ __forceinline__ void key_stage(const char* slot, int w, int n, int kg
 #pragma unroll
       for (int j = 0; j < 8 / GPB; ++j) {
         const int jm = grp * (8 / GPB) + j;
-        const h8 a = tr::key_codes(static_cast<uint32_t>(rk[jm][e]), cst);
+        const h8 a = tr::codes(static_cast<uint32_t>(rk[jm][e]), cst);
         st.sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, kh.bq[e], st.sacc[jm], 0, 0, 0);
         if (!FOLD)
           st.sacc[jm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, kh.bl[e], st.sacc[jm], 0, 0, 0);
