@@ -363,14 +363,19 @@ def bench_kivi_decode(torch, dev, *, b, hq, kvh, d, g, r, bs, lens, steps, warmu
     return res
 
 
-def bench_kivi_forward(torch, dev, *, lens, hq, kvh, d, g, r, bs, steps, warmup, seed):
-    """Config-3 decode steps through the KIVI mixin's ``forward()``, the way a
-    host calls it: the step's metadata (device ``slot_mapping`` and block
-    table, host ``seq_lens_list``) goes in, and the mixin plans on the host,
-    copies its plans to the device and launches the store, decode and
-    combine.  Timed by the host clock around ``steps`` back-to-back steps
-    (with one synchronisation at the end), so host planning and any device
-    synchronisation inside ``forward()`` are included."""
+def bench_kivi_forward(torch, dev, *, lens, hq, kvh, d, g, r, bs, steps, warmup, seed,
+                       layers=1, graph=False):
+    """Config-3 decode steps through the KIVI mixin, the way a host calls it,
+    over ``layers`` attention layers (each its own impl, caches and history;
+    one metadata object per engine step, shared by the layers as a vLLM
+    runner shares it).  The step's metadata (device ``slot_mapping`` and block
+    table, host ``seq_lens_list`` and copies) goes in, and the mixin plans on
+    the host, copies its plan to the device and launches the store, decode
+    and combine.  ``graph``: each layer's step is a captured HIP graph
+    (``kivi_decode_graph``), and the host calls ``prepare_kivi_graph_replay``
+    before each replay.  Timed by the host clock around ``steps`` engine
+    steps (one synchronisation at the end), so host planning and any device
+    synchronisation are included; reported per layer-step."""
     from types import SimpleNamespace
 
     from vllm_ascend_quantized_kv_cache.methods.kivi_int4 import attention_backend as ab
@@ -381,18 +386,9 @@ def bench_kivi_forward(torch, dev, *, lens, hq, kvh, d, g, r, bs, steps, warmup,
 
     b = len(lens)
     total = steps + warmup
-    impl = Impl()
-    impl.num_heads, impl.num_kv_heads, impl.head_size, impl.scale = hq, kvh, d, d ** -0.5
-    impl._init_kivi_state(None)
-    impl.enable_kivi = True
-    impl.kivi_group_size, impl.kivi_residual_length, impl.kivi_max_num_seqs = g, r, b
     nblk = [-(-(n + total) // bs) for n in lens]
     nb = sum(nblk) + 8
     layout = KiviByteCacheLayout(nb, bs, kvh, d, g)
-    kbuf = torch.zeros((nb, bs, kvh, layout.bytes_per_token_head), dtype=torch.uint8, device=dev)
-    vbuf = torch.zeros_like(kbuf)
-    kv_cache = (kbuf, vbuf)
-    impl._bind_kivi_cache(kv_cache)
     gen = torch.Generator().manual_seed(seed)
     perm = torch.randperm(nb, generator=gen)
     table = torch.zeros((b, max(nblk)), dtype=torch.int64)
@@ -408,10 +404,25 @@ def bench_kivi_forward(torch, dev, *, lens, hq, kvh, d, g, r, bs, steps, warmup,
     def slots(i, p0, p1):
         return table[i][pos[p0:p1] // bs] * bs + pos[p0:p1] % bs
 
-    for i, n in enumerate(lens):
-        k = (torch.randn((n, kvh, d), generator=gdev, device=dev) * key_scales).to(torch.bfloat16)
-        v = torch.randn((n, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
-        impl._write_kivi_cache(k, v, slots(i, 0, n).to(dev), [reqs[i]], [n])
+    impls, caches = [], []
+    for _ in range(layers):
+        impl = Impl()
+        impl.num_heads, impl.num_kv_heads, impl.head_size, impl.scale = hq, kvh, d, d ** -0.5
+        impl._init_kivi_state(None)
+        impl.enable_kivi = True
+        impl.kivi_group_size, impl.kivi_residual_length, impl.kivi_max_num_seqs = g, r, b
+        kbuf = torch.zeros((nb, bs, kvh, layout.bytes_per_token_head), dtype=torch.uint8,
+                           device=dev)
+        kv_cache = (kbuf, torch.zeros_like(kbuf))
+        impl._bind_kivi_cache(kv_cache)
+        for i, n in enumerate(lens):
+            k = (torch.randn((n, kvh, d), generator=gdev, device=dev) * key_scales).to(
+                torch.bfloat16)
+            v = torch.randn((n, kvh, d), generator=gdev, device=dev).to(torch.bfloat16)
+            # the lengths let the mirror record each window token's position
+            impl._write_kivi_cache(k, v, slots(i, 0, n).to(dev), [reqs[i]], [n], [n])
+        impls.append(impl)
+        caches.append(kv_cache)
     table_dev = table.to(dev)
     new_k = (torch.randn((total, b, kvh, d), generator=gdev, device=dev)
              * key_scales).to(torch.bfloat16)
@@ -429,24 +440,52 @@ def bench_kivi_forward(torch, dev, *, lens, hq, kvh, d, g, r, bs, steps, warmup,
                                    slot_mapping=sm.to(dev), block_tables=table_dev,
                                    slot_mapping_cpu=sm, block_tables_cpu=table, req_ids=reqs,
                                    num_actual_tokens=b))
+    graphs = [None] * layers
+    if graph:
+        for impl in impls:
+            impl.kivi_decode_graph(b, max_blocks=table.shape[1])
+        # static inputs the captured launches read: the host's layer inputs
+        q_s = torch.zeros((b, hq, d), dtype=torch.bfloat16, device=dev)
+        k_s = torch.zeros((b, kvh, d), dtype=torch.bfloat16, device=dev)
+        v_s = torch.zeros_like(k_s)
     torch.cuda.synchronize()
 
     def step(j):
-        impl.forward(None, qs[j], new_k[j], new_v[j], kv_cache, mds[j], out)
+        md = mds[j]
+        if not graph:
+            for impl, kv_cache in zip(impls, caches):
+                impl.forward(None, qs[j], new_k[j], new_v[j], kv_cache, md, out)
+            return
+        q_s.copy_(qs[j])
+        k_s.copy_(new_k[j])
+        v_s.copy_(new_v[j])
+        for li, impl in enumerate(impls):
+            impl.prepare_kivi_graph_replay(md, k_s, v_s)
+            if graphs[li] is None:
+                torch.cuda.synchronize()
+                graphs[li] = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graphs[li]):
+                    impl.forward(None, q_s, k_s, v_s, caches[li], md, out)
+            graphs[li].replay()
 
     for j in range(warmup):
         step(j)
     torch.cuda.synchronize()
-    reads0 = impl.kivi_host_reads
+    reads0 = sum(impl.kivi_host_reads for impl in impls)
     t0 = time.perf_counter()
     for j in range(warmup, total):
         step(j)
     torch.cuda.synchronize()
-    us = (time.perf_counter() - t0) / steps * 1e6
-    reads = impl.kivi_host_reads - reads0
-    del impl, kbuf, vbuf, new_k, new_v, qs
+    us = (time.perf_counter() - t0) / (steps * layers) * 1e6
+    reads = sum(impl.kivi_host_reads for impl in impls) - reads0
+    del impls, caches, new_k, new_v, qs, graphs
     torch.cuda.empty_cache()
-    return {"us_per_step": us, "host_reads_per_step": reads / steps}
+    return {"us_per_step": us, "host_reads_per_step": reads / (steps * layers), "layers": layers}
+
+
+#: layers of the forward legs: the attention layers of one engine step share
+#: its metadata object; eight of Qwen2.5-14B's 48 stand in for the model
+FORWARD_LAYERS = 8
 
 
 def cpu_info() -> dict:
@@ -1086,12 +1125,22 @@ def run_leg(torch, dev, leg: str, lens: list[int], args) -> dict:
     """One extra leg; returns its entries for the JSON line's ``extra``."""
     out = {}
     if leg == "forward":
-        fw = bench_kivi_forward(torch, dev, lens=lens, hq=40, kvh=8, d=128, g=128, r=128,
-                                bs=128, steps=args.steps, warmup=args.warmup, seed=11)
+        common = dict(lens=lens, hq=40, kvh=8, d=128, g=128, r=128, bs=128, steps=args.steps,
+                      warmup=args.warmup, seed=11)
+        fw1 = bench_kivi_forward(torch, dev, layers=1, **common)
+        fw = bench_kivi_forward(torch, dev, layers=FORWARD_LAYERS, **common)
         out["config3_forward"] = {"us_per_step": round(fw["us_per_step"], 1),
+                                  "layers": fw["layers"],
+                                  "us_per_step_one_layer": round(fw1["us_per_step"], 1),
                                   "host_reads_per_step": fw["host_reads_per_step"]}
-        log(f"config3: forward() {fw['us_per_step']:.1f} us per step (host clock, "
+        log(f"config3: forward() {fw['us_per_step']:.1f} us per layer-step over "
+            f"{fw['layers']} layers, {fw1['us_per_step']:.1f} us with one layer (host clock, "
             f"{fw['host_reads_per_step']:.0f} device reads per step)")
+        gr = bench_kivi_forward(torch, dev, layers=FORWARD_LAYERS, graph=True, **common)
+        out["config3_graph"] = {"us_per_step": round(gr["us_per_step"], 1), "layers": gr["layers"],
+                                "host_reads_per_step": gr["host_reads_per_step"]}
+        log(f"config3: graph prepare + replay {gr['us_per_step']:.1f} us per layer-step over "
+            f"{gr['layers']} layers (host clock)")
     elif leg == "config4":
         pg = bench_pack_gather(torch, dev)
         out["config4_pack"] = {"ms": round(pg["pack_ms"], 4), "gbs": round(pg["pack_gbs"], 1),

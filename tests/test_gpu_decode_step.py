@@ -53,7 +53,7 @@ class _Case:
     """Requests with int4 history and windows, identical on every impl built."""
 
     def __init__(self, device, *, b=6, hq=40, kvh=8, d=128, g=128, r=128, bs=128, steps=140,
-                 seed=0):
+                 seed=0, data_seed=None):
         gen = torch.Generator().manual_seed(seed)
         self.device, self.b, self.hq, self.kvh, self.d, self.g, self.r, self.bs = (
             device, b, hq, kvh, d, g, r, bs)
@@ -67,6 +67,8 @@ class _Case:
             self.table[i, :n] = perm[used:used + n]
             used += n
         self.table_dev = self.table.to(device)
+        if data_seed is not None:  # same geometry and slots, other keys, values, queries
+            gen = torch.Generator().manual_seed(data_seed)
         scales = torch.exp(torch.randn((kvh, d), generator=gen))
         self.keys = [(torch.randn(n + steps, kvh, d, generator=gen) * scales).to(torch.bfloat16)
                      for n in self.lens]
@@ -78,10 +80,13 @@ class _Case:
     def slot(self, i, p):
         return int(self.table[i, p // self.bs]) * self.bs + p % self.bs
 
-    def build(self, **kw):
+    def build(self, *, reverse=False, **kw):
+        """An impl holding the requests' history (``reverse``: registered last
+        to first, so each request gets another residual row)."""
         impl = _impl(self.device, hq=self.hq, kvh=self.kvh, d=self.d, g=self.g, r=self.r,
                      nb=self.nb, bs=self.bs, rows=self.b, **kw)
-        for i, n in enumerate(self.lens):
+        order = list(enumerate(self.lens))
+        for i, n in (order[::-1] if reverse else order):
             sl = torch.tensor([self.slot(i, p) for p in range(n)], device=self.device)
             impl._write_kivi_cache(self.keys[i][:n].to(self.device),
                                    self.values[i][:n].to(self.device), sl, [self.reqs[i]], [n],
@@ -146,6 +151,53 @@ def test_planned_decode_step_equals_general_path(gpu_device, g):
             case.oracle(fast, j, outs[0])
     assert fast._kivi_step_bufs is not None and general._kivi_step_bufs is None
     assert fast.kivi_host_reads == 0
+
+
+def test_layers_share_one_planned_step(gpu_device, monkeypatch):
+    """Layers called with one metadata object per engine step: the first
+    plans and stages the step, the others whose window mirror matches take
+    its plan and launch against their own caches.  Each layer has its own
+    keys, values and queries; its output equals, bit for bit, a lone twin's
+    that plans every step itself, over steps that flush key windows, and the
+    oracle's.  A layer whose requests sit in other residual rows (a mirror
+    that differs) plans on its own within the same steps."""
+    steps = 135
+    cases = [_Case(gpu_device, steps=steps, seed=5, data_seed=100 + i) for i in range(3)]
+    layers = [c.build() for c in cases[:2]] + [cases[2].build(reverse=True)]
+    twins = [c.build() for c in cases[:2]] + [cases[2].build(reverse=True)]
+    replayed = []
+    orig = ab.AscendKiviInt4AttentionBackendMixin._replay_shared_kivi_step
+
+    def counting(self, *a, **k):
+        replayed.append(self)
+        return orig(self, *a, **k)
+
+    monkeypatch.setattr(ab.AscendKiviInt4AttentionBackendMixin, "_replay_shared_kivi_step",
+                        counting)
+    for j in range(steps):
+        steps_j = [c.step(j) for c in cases]
+        md = steps_j[0][0]  # one metadata object for the engine step
+        outs, want = [], []
+        for impl, (_, q, k, v) in zip(layers, steps_j):
+            out = torch.zeros((cases[0].b, cases[0].hq, cases[0].d), dtype=torch.bfloat16,
+                              device=gpu_device)
+            impl.forward(None, q, k, v, None, md, out)
+            outs.append(out)
+        for twin, c in zip(twins, cases):
+            own_md, q, k, v = c.step(j)  # a metadata object of its own: plans alone
+            out = torch.zeros_like(outs[0])
+            twin.forward(None, q, k, v, None, own_md, out)
+            want.append(out)
+        torch.cuda.synchronize()
+        for li in range(3):
+            assert torch.equal(outs[li], want[li]), f"step {j} layer {li}"
+        if j % 45 == 0 or j == steps - 1:
+            for li in range(3):
+                _same_state(layers[li], twins[li])
+                cases[li].oracle(layers[li], j, outs[li])
+    # layer 1 reused layer 0's plan every step; layer 2 (other rows) never did
+    assert replayed == [layers[1]] * steps
+    assert layers[1]._kivi_step_bufs is None and layers[2]._kivi_step_bufs is not None
 
 
 def test_planned_decode_step_reads_nothing_back(gpu_device):

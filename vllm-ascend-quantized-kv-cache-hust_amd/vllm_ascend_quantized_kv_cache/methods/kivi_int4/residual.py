@@ -216,6 +216,29 @@ class KiviResidualRing:
             self.lane_slot[k][row] = ls
             self.lane_pos[k][row] = lp
 
+    def snapshot(self) -> tuple:
+        """Copies of the mirror arrays, per side: (start, length, lane_slot,
+        lane_pos)."""
+        return tuple((self.start[k].copy(), self.length[k].copy(), self.lane_slot[k].copy(),
+                      self.lane_pos[k].copy()) for k in _SIDES)
+
+    def matches(self, snap: tuple) -> bool:
+        """The mirror equals ``snap`` (a ``snapshot`` of a ring of this shape)."""
+        for k, (start, length, ls, lp) in zip(_SIDES, snap):
+            if not (np.array_equal(self.start[k], start) and np.array_equal(self.length[k], length)
+                    and np.array_equal(self.lane_slot[k], ls)
+                    and np.array_equal(self.lane_pos[k], lp)):
+                return False
+        return True
+
+    def load(self, snap: tuple) -> None:
+        """Set the mirror to ``snap`` (copied in; ``snap`` stays unchanged)."""
+        for k, (start, length, ls, lp) in zip(_SIDES, snap):
+            np.copyto(self.start[k], start)
+            np.copyto(self.length[k], length)
+            np.copyto(self.lane_slot[k], ls)
+            np.copyto(self.lane_pos[k], lp)
+
     def state(self) -> tuple:
         """The whole mirror as nested tuples of ints (for comparisons)."""
         return tuple(
