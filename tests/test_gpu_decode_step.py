@@ -200,6 +200,64 @@ def test_layers_share_one_planned_step(gpu_device, monkeypatch):
     assert layers[1]._kivi_step_bufs is None and layers[2]._kivi_step_bufs is not None
 
 
+def test_layer_graphs_share_one_planned_step(gpu_device, monkeypatch):
+    """Each layer's step captured once; per engine step every layer's
+    ``prepare`` sees the same metadata object.  The first layer plans and
+    stages, the next takes that plan with one copy (its mirror matches), a
+    layer whose requests sit in other rows plans on its own.  Every replay
+    equals an eager twin bit for bit, over steps that flush key windows."""
+    from vllm_ascend_quantized_kv_cache.methods.kivi_int4 import decode_step as dstep
+
+    steps = 131
+    cases = [_Case(gpu_device, steps=steps, seed=8, data_seed=200 + i) for i in range(3)]
+    layers = [c.build() for c in cases[:2]] + [cases[2].build(reverse=True)]
+    twins = [c.build() for c in cases[:2]] + [cases[2].build(reverse=True)]
+    copied = []
+    orig = dstep.DecodeStepBuffers.copy_staged_from
+
+    def counting(self, *a, **k):
+        copied.append(self)
+        return orig(self, *a, **k)
+
+    monkeypatch.setattr(dstep.DecodeStepBuffers, "copy_staged_from", counting)
+    c0 = cases[0]
+    gsteps = [impl.kivi_decode_graph(c0.b, max_blocks=c0.table.shape[1]) for impl in layers]
+    statics = [tuple(torch.zeros(shape, dtype=torch.bfloat16, device=gpu_device)
+                     for shape in ((c0.b, c0.hq, c0.d), (c0.b, c0.kvh, c0.d),
+                                   (c0.b, c0.kvh, c0.d), (c0.b, c0.hq, c0.d)))
+               for _ in layers]
+    graphs = [None] * 3
+    for j in range(steps):
+        steps_j = [c.step(j) for c in cases]
+        md = steps_j[0][0]
+        for li, impl in enumerate(layers):
+            q_s, k_s, v_s, out_s = statics[li]
+            _, q, k, v = steps_j[li]
+            q_s.copy_(q)
+            k_s.copy_(k)
+            v_s.copy_(v)
+            impl.prepare_kivi_graph_replay(md, k_s, v_s)
+            if graphs[li] is None:
+                torch.cuda.synchronize()
+                graphs[li] = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graphs[li]):
+                    impl.forward(None, q_s, k_s, v_s, None, md, out_s)
+            graphs[li].replay()
+        want = []
+        for twin, c in zip(twins, cases):
+            own_md, q, k, v = c.step(j)
+            out = torch.zeros_like(statics[0][0])
+            twin.forward(None, q, k, v, None, own_md, out)
+            want.append(out)
+        torch.cuda.synchronize()
+        for li in range(3):
+            assert torch.equal(statics[li][3], want[li]), f"replay {j} layer {li}"
+        if j in (0, 64, steps - 1):
+            for li in range(3):
+                _same_state(layers[li], twins[li])
+    assert copied == [gsteps[1].bufs] * steps
+
+
 def test_planned_decode_step_reads_nothing_back(gpu_device):
     case = _Case(gpu_device, steps=4, seed=3)
     impl = case.build()

@@ -97,6 +97,21 @@ class DecodeStepBuffers:
         self._used = [False] * self.STAGING
         self._next = 0
         self._pieces = np.zeros(pieces_cap + 1, dtype=np.int32)
+        self.last_host: tuple[int, int] | None = None  # (host buffer, bytes) of the last stage
+
+    def same_layout(self, other: "DecodeStepBuffers") -> bool:
+        """Fixed-layout plans of ``other`` read the same here (same capacities)."""
+        return (self.batch, self.cap_key_pack, self.cap_value, self.work_cap, self.pieces_cap,
+                self.nbytes) == (other.batch, other.cap_key_pack, other.cap_value,
+                                 other.work_cap, other.pieces_cap, other.nbytes)
+
+    def copy_staged_from(self, src: "DecodeStepBuffers", index: int, nbytes: int) -> None:
+        """Queue a copy of the plan ``src`` staged in its host buffer ``index``
+        into this device buffer; the copy is recorded on ``src``'s event for
+        that buffer, so ``src`` rewrites it only after the copy has read it."""
+        self.plan[:nbytes].copy_(src._host[index][:nbytes], non_blocking=True)
+        src._events[index].record()
+        src._used[index] = True
 
     def fits(self, batch: int, work_cap: int, pieces_cap: int) -> bool:
         return batch <= self.batch and work_cap <= self.work_cap and pieces_cap <= self.pieces_cap
@@ -178,6 +193,7 @@ class DecodeStepBuffers:
             h[pieces_off:pieces_off + 4 * (npc + 1)].view(np.int32)[:] = self._pieces[: npc + 1]
             nbytes = pieces_off + 4 * (npc + 1)
         self._upload(i, nbytes)
+        self.last_host = (i, nbytes)  # where this plan sits in host memory
         return StagedPlan(counts, jobs_off, meta_off, work_off, pieces_off, n, npc, fixed)
 
 
@@ -265,6 +281,18 @@ def eager_capacities(batch: int, num_kv_heads: int, cu_count: int, seqs: np.ndar
     return work, work
 
 
+class _SharedGraphStep:
+    """The last step a layer's ``KiviDecodeGraph.prepare`` planned, for the
+    other layers' graphs of the same engine step (the graph-path twin of the
+    eager path's shared step): the metadata object, the layer signature, the
+    window mirror before and after, and where the staged plan sits in the
+    planning graph's host memory."""
+
+    __slots__ = ("md", "sig", "before", "after", "bufs", "host", "staged")
+
+    last: "_SharedGraphStep | None" = None
+
+
 class KiviDecodeGraph:
     """A decode step of one layer captured in a HIP graph and replayed per step.
 
@@ -337,6 +365,28 @@ class KiviDecodeGraph:
                 "16-bit activations shared with the ring, at most 16 query heads per kv head, "
                 "a power-of-two block size); run it eagerly through forward."
             )
+        # another layer's graph planned this engine step from the same mirror:
+        # take its plan (one host-to-device copy) instead of planning again
+        sig = (impl.num_heads, impl.num_kv_heads, impl.head_size, impl.kivi_group_size,
+               impl._get_kivi_block_size(), impl.kivi_residual_length, ring.rows, ring.dtype,
+               key.dtype, key.device, int(impl.k_quant_cache.shape[0]), self.cu_count,
+               torch.cuda.current_stream(key.device).cuda_stream)
+        shared = _SharedGraphStep.last
+        if (shared is not None and shared.md is attn_metadata and shared.sig == sig
+                and shared.bufs is not self.bufs and shared.bufs.same_layout(self.bufs)
+                and impl._kivi_mirror_matches(shared.before)):
+            impl._kivi_mirror_load(shared.after)
+            try:
+                self.bufs.copy_staged_from(shared.bufs, *shared.host)
+                table_dev = attn_metadata.block_tables[:b]
+                rows, cols = table_dev.shape
+                self.table[:rows, :cols].copy_(table_dev, non_blocking=True)
+            except BaseException:
+                impl._kivi_mirror_load(shared.before)
+                raise
+            self.staged = shared.staged
+            return
+        before = impl._kivi_mirror_snapshot()
         with impl._kivi_planning():
             plan = impl._plan_kivi_decode_step(attn_metadata, key, value, allow_compaction=False)
             if plan is None:
@@ -351,6 +401,10 @@ class KiviDecodeGraph:
             rows, cols = table_dev.shape
             self.table[:rows, :cols].copy_(table_dev, non_blocking=True)
         self.staged = staged
+        rec = _SharedGraphStep()
+        rec.md, rec.sig, rec.before, rec.after = attn_metadata, sig, before, impl._kivi_mirror_snapshot()
+        rec.bufs, rec.host, rec.staged = self.bufs, self.bufs.last_host, staged
+        _SharedGraphStep.last = rec
 
     def launch(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                output: torch.Tensor) -> torch.Tensor:
