@@ -158,8 +158,12 @@ class AscendKiviInt4AttentionBackendMixin:
             raise RuntimeError("KIVI cache tensors are not bound.")
 
     def _get_kivi_block_size(self) -> int:
+        kq = self.k_quant_cache
+        if kq is not None and kq is getattr(self, "_kivi_bs_of", None):
+            return self._kivi_bs  # the bound key codes' page geometry, as last read
         self._check_kivi_cache_bound()
-        return self.k_quant_cache.shape[-1] * 8
+        self._kivi_bs, self._kivi_bs_of = kq.shape[-1] * 8, kq
+        return self._kivi_bs
 
     # ------------------------------------------------------------------
     # cache binding (ab.py:135-175)
@@ -176,7 +180,19 @@ class AscendKiviInt4AttentionBackendMixin:
             )
         if len(kv_cache) == 0:
             return
+        last = getattr(self, "_kivi_bound_objs", None)
+        if (last is not None and len(kv_cache) == 2 and kv_cache[0] is last[0]
+                and kv_cache[1] is last[1] and kv_cache[0].data_ptr() == last[2]
+                and kv_cache[1].data_ptr() == last[3] and kv_cache[0].shape == last[4]
+                and kv_cache[1].shape == last[5]
+                and (self.num_kv_heads, self.head_size, self.kivi_group_size) == last[6]
+                and self._kivi_ring is not None):
+            return  # the very buffer objects bound last time, unchanged
+        self._kivi_bound_objs = None
         if len(kv_cache) == 2:
+            objs = (kv_cache[0], kv_cache[1], kv_cache[0].data_ptr(), kv_cache[1].data_ptr(),
+                    kv_cache[0].shape, kv_cache[1].shape,
+                    (self.num_kv_heads, self.head_size, self.kivi_group_size))
             # the same two buffers as the last call: the six views are still
             # bound (they hold the buffers' storage, so no other allocation
             # can have taken these addresses)
@@ -185,6 +201,7 @@ class AscendKiviInt4AttentionBackendMixin:
                      self.num_kv_heads, self.head_size, self.kivi_group_size)
             if (bound == getattr(self, "_kivi_bound_buffers", None) and self._kivi_ring is not None
                     and all(t is not None for t in self._kivi_caches())):
+                self._kivi_bound_objs = objs
                 return
             layout = kivi_byte_cache_layout(
                 kv_cache[0],
@@ -196,6 +213,7 @@ class AscendKiviInt4AttentionBackendMixin:
             kv_cache = kivi_caches_from_byte_tensors(kv_cache[0], kv_cache[1], layout)
             self._kivi_bound_buffers = bound
         else:
+            objs = None
             self._kivi_bound_buffers = None
         if len(kv_cache) != 6:
             raise RuntimeError(
@@ -211,6 +229,7 @@ class AscendKiviInt4AttentionBackendMixin:
             self.v_mn_cache,
         ) = kv_cache
         self._ensure_kivi_residual_buffers()
+        self._kivi_bound_objs = objs
 
     # ------------------------------------------------------------------
     # residual rows (ab.py:181-259)

@@ -139,10 +139,24 @@ class KiviResidualRing:
         self.key = torch.zeros((rows, ring_len, num_kv_heads, head_size), dtype=dtype, device=device)
         self.value = torch.zeros_like(self.key)
         self.written = False
-        self.start = {s: np.zeros(rows, dtype=np.int64) for s in _SIDES}
-        self.length = {s: np.zeros(rows, dtype=np.int64) for s in _SIDES}
-        self.lane_slot = {s: np.full((rows, ring_len), -1, dtype=np.int64) for s in _SIDES}
-        self.lane_pos = {s: np.full((rows, ring_len), -1, dtype=np.int64) for s in _SIDES}
+        # the whole mirror is one int64 block; the per-side arrays are views
+        # into it, so a snapshot, a comparison or a restore is one operation
+        per_side = 2 * rows + 2 * rows * ring_len
+        self._mirror = np.empty(2 * per_side, dtype=np.int64)
+        self.start, self.length, self.lane_slot, self.lane_pos = {}, {}, {}, {}
+        off = 0
+        for s in _SIDES:
+            self.start[s] = self._mirror[off:off + rows]
+            self.length[s] = self._mirror[off + rows:off + 2 * rows]
+            off += 2 * rows
+            self.lane_slot[s] = self._mirror[off:off + rows * ring_len].reshape(rows, ring_len)
+            off += rows * ring_len
+            self.lane_pos[s] = self._mirror[off:off + rows * ring_len].reshape(rows, ring_len)
+            off += rows * ring_len
+            self.start[s][:] = 0
+            self.length[s][:] = 0
+            self.lane_slot[s][:] = -1
+            self.lane_pos[s][:] = -1
         self._saved: dict[int, tuple] | None = None
         # vectorized snapshots of whole batches of rows: (rows, per-side arrays)
         self._saved_batches: list[tuple[np.ndarray, tuple]] = []
@@ -216,28 +230,18 @@ class KiviResidualRing:
             self.lane_slot[k][row] = ls
             self.lane_pos[k][row] = lp
 
-    def snapshot(self) -> tuple:
-        """Copies of the mirror arrays, per side: (start, length, lane_slot,
-        lane_pos)."""
-        return tuple((self.start[k].copy(), self.length[k].copy(), self.lane_slot[k].copy(),
-                      self.lane_pos[k].copy()) for k in _SIDES)
+    def snapshot(self) -> np.ndarray:
+        """A copy of the whole mirror (start, length, lane_slot, lane_pos of
+        both sides)."""
+        return self._mirror.copy()
 
-    def matches(self, snap: tuple) -> bool:
+    def matches(self, snap: np.ndarray) -> bool:
         """The mirror equals ``snap`` (a ``snapshot`` of a ring of this shape)."""
-        for k, (start, length, ls, lp) in zip(_SIDES, snap):
-            if not (np.array_equal(self.start[k], start) and np.array_equal(self.length[k], length)
-                    and np.array_equal(self.lane_slot[k], ls)
-                    and np.array_equal(self.lane_pos[k], lp)):
-                return False
-        return True
+        return snap.shape == self._mirror.shape and bool((self._mirror == snap).all())
 
-    def load(self, snap: tuple) -> None:
+    def load(self, snap: np.ndarray) -> None:
         """Set the mirror to ``snap`` (copied in; ``snap`` stays unchanged)."""
-        for k, (start, length, ls, lp) in zip(_SIDES, snap):
-            np.copyto(self.start[k], start)
-            np.copyto(self.length[k], length)
-            np.copyto(self.lane_slot[k], ls)
-            np.copyto(self.lane_pos[k], lp)
+        np.copyto(self._mirror, snap)
 
     def state(self) -> tuple:
         """The whole mirror as nested tuples of ints (for comparisons)."""

@@ -136,12 +136,19 @@ def lib() -> ctypes.CDLL:
     return _LIB
 
 
+_DTYPE_CODES: dict = {}
+
+
 def dtype_code(dtype) -> int:
+    code = _DTYPE_CODES.get(dtype)
+    if code is not None:
+        return code
     import torch
 
     codes = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
     if dtype not in codes:
         raise RuntimeError(f"unsupported floating dtype for the HIP kernels: {dtype}")
+    _DTYPE_CODES[dtype] = codes[dtype]
     return codes[dtype]
 
 
