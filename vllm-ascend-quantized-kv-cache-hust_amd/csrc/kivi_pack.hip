@@ -1002,6 +1002,70 @@ int launch_store_lds(const void* key_input, const void* value_input, void* ring_
                                          vr_dst, c2, c3, s);
 }
 
+// One side of a pack on the LDS-staged kernel (the other side empty, no ring
+// rows): the per-side entry points' path where the kernel applies, so every
+// pack writes its scales and minima as consecutive runs (a per-row scale
+// written alone covers a 4-byte piece of a line, which the memory side turns
+// into a read of the line).
+template <typename T, typename I>
+int pack_side_lds(bool key, const void* src_a, int64_t n_a, const void* src_b,
+                  const int64_t* src_index, const void* slot_mapping, int64_t num_tokens,
+                  int kvh, int g, int bs, int32_t* quant, float* scale, float* mn,
+                  hipStream_t s) {
+  const lp::Side<T, I> side{static_cast<const T*>(src_a), n_a, static_cast<const T*>(src_b),
+                            src_index, static_cast<const I*>(slot_mapping), num_tokens};
+  const lp::Side<T, I> none{nullptr, 0, nullptr, nullptr, nullptr, 0};
+  lp::Ctx<T, I> c{};
+  c.k = key ? side : none;
+  c.v = key ? none : side;
+  c.kvh = kvh;
+  c.bs = bs;
+  c.kdiv = FastDiv::make(static_cast<uint32_t>(kvh));
+  c.kq = key ? quant : nullptr;
+  c.ks = key ? scale : nullptr;
+  c.km = key ? mn : nullptr;
+  c.vq = key ? nullptr : quant;
+  c.vs = key ? nullptr : scale;
+  c.vm = key ? nullptr : mn;
+  if (g == 128)
+    return launch_pack_lds<T, I, 128>(c, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                      nullptr, nullptr, nullptr, 0, 0, s);
+  return launch_pack_lds<T, I, 64>(c, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                   nullptr, nullptr, nullptr, 0, 0, s);
+}
+
+bool pack_lds_applies(int src_dtype, int head_size, int group_size, int64_t num_tokens,
+                      int kvh) {
+  return head_size == 128 && (group_size == 64 || group_size == 128) &&
+         (src_dtype == KVQ_DTYPE_BF16 || src_dtype == KVQ_DTYPE_F16) &&
+         num_tokens * kvh < 0x7fffffff;  // source rows are int32 in the kernel
+}
+
+template <typename I>
+int pack_side_lds_dispatch(bool key, int src_dtype, const void* src_a, int64_t n_a,
+                           const void* src_b, const int64_t* src_index, const void* slot_mapping,
+                           int64_t num_tokens, int kvh, int g, int bs, int32_t* quant,
+                           float* scale, float* mn, hipStream_t s) {
+  if (src_dtype == KVQ_DTYPE_BF16)
+    return pack_side_lds<bf16, I>(key, src_a, n_a, src_b, src_index, slot_mapping, num_tokens,
+                                  kvh, g, bs, quant, scale, mn, s);
+  return pack_side_lds<f16, I>(key, src_a, n_a, src_b, src_index, slot_mapping, num_tokens, kvh,
+                               g, bs, quant, scale, mn, s);
+}
+
+int pack_side(bool key, int src_dtype, const void* src_a, int64_t n_a, const void* src_b,
+              const int64_t* src_index, const void* slot_mapping, int slot_index_type,
+              int64_t num_tokens, int kvh, int g, int bs, int32_t* quant, float* scale,
+              float* mn, hipStream_t s) {
+  if (slot_index_type == KVQ_INDEX_I64)
+    return pack_side_lds_dispatch<int64_t>(key, src_dtype, src_a, n_a, src_b, src_index,
+                                           slot_mapping, num_tokens, kvh, g, bs, quant, scale,
+                                           mn, s);
+  return pack_side_lds_dispatch<int32_t>(key, src_dtype, src_a, n_a, src_b, src_index,
+                                         slot_mapping, num_tokens, kvh, g, bs, quant, scale, mn,
+                                         s);
+}
+
 bool kivi_geometry_ok(int kvh, int d, int g, int bs) {
   return kvh > 0 && d > 0 && g > 0 && bs > 0 && g % 8 == 0 && d % 8 == 0 && d % g == 0 &&
          bs % g == 0;
@@ -1025,6 +1089,11 @@ extern "C" int kvq_kivi_pack_key(const void* src_a, int64_t n_a, const void* src
   if (num_tokens % group_size) return KVQ_ERR_INVALID;
   if (!src_index && n_a < num_tokens) return KVQ_ERR_INVALID;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pack_lds_applies(src_dtype, head_size, group_size, num_tokens, num_kv_heads) &&
+      (slot_index_type == KVQ_INDEX_I32 || slot_index_type == KVQ_INDEX_I64))
+    return pack_side(true, src_dtype, src_a, n_a, src_b, src_index, slot_mapping,
+                     slot_index_type, num_tokens, num_kv_heads, group_size, block_size, k_quant,
+                     k_scale, k_mn, s);
   if (head_size == 128 && (group_size == 64 || group_size == 128) &&
       (src_dtype == KVQ_DTYPE_BF16 || src_dtype == KVQ_DTYPE_F16)) {
     // register form: one wave per (token group, head, part of the dims):
@@ -1078,6 +1147,11 @@ extern "C" int kvq_kivi_pack_value(const void* src_a, int64_t n_a, const void* s
     return KVQ_ERR_GEOMETRY;
   if (!src_index && n_a < num_tokens) return KVQ_ERR_INVALID;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pack_lds_applies(src_dtype, head_size, group_size, num_tokens, num_kv_heads) &&
+      (slot_index_type == KVQ_INDEX_I32 || slot_index_type == KVQ_INDEX_I64))
+    return pack_side(false, src_dtype, src_a, n_a, src_b, src_index, slot_mapping,
+                     slot_index_type, num_tokens, num_kv_heads, group_size, block_size, v_quant,
+                     v_scale, v_mn, s);
   const int wpr = head_size / 8;
   const int gw = group_size / 8;
   const int64_t rows = num_tokens * num_kv_heads;
