@@ -1,6 +1,12 @@
 // SPDX-License-Identifier: Apache-2.0
 // KIVI INT4 pack kernels for MI355X (gfx950).
 //
+// Head size 128 with G in {64, 128} and 16-bit input, both per-side entry
+// points (kvq_kivi_pack_key / kvq_kivi_pack_value) run on the one-launch
+// store's LDS-staged kernel (below) with the other side empty.  The forms
+// described next serve the other geometries, and inputs past that kernel's
+// int32 source-row range.
+//
 // Key pack  (reference: pkg/ops/triton/kivi_pack.py:134-226)
 //   Head size 128 with G in {64, 128} and 16-bit input: the register form
 //   below (kivi_pack_key_wave_kernel), one wave per group, head and quarter
