@@ -238,6 +238,62 @@ def test_gather_with_residual_overlay(gpu_device, d, kvh, g, bs):
     assert torch.equal(want_v, got_v.cpu())
 
 
+@pytest.mark.parametrize("g,bs,kvh,index_dtype", [(64, 128, 8, torch.int32),
+                                                   (128, 128, 8, torch.int64),
+                                                   (64, 64, 4, torch.int32)])
+def test_gather_of_many_pages_matches_oracle(gpu_device, g, bs, kvh, index_dtype):
+    """Thousands of (page, head) units of the d = 128 gather: more workgroups
+    than the device holds at once, units past a request's end (a ragged batch
+    over a wide table), and requests whose tails come from the rings (none,
+    part of a page, more than a page, the whole request).  Pages hold random
+    codes, scales and minima."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_gather import gather_dequant_with_residual
+
+    d = 128
+    lens = [20000, 7001, 15000, 129]
+    tails = [(128, 5), (0, 0), (77, 128), (1, 129)]  # (k_tail, v_tail) rows from the rings
+    r_len = 256
+    gen = torch.Generator().manual_seed(17)
+    nblk = [-(-n // bs) for n in lens]
+    nb = sum(nblk) + 3
+    maxb = max(nblk)
+    table = torch.full((len(lens), maxb), -1, dtype=index_dtype)
+    perm = torch.randperm(nb, generator=gen)
+    used = 0
+    for r, n in enumerate(nblk):
+        table[r, :n] = perm[used : used + n].to(index_dtype)
+        used += n
+    kq = torch.randint(-2**31, 2**31, (nb, kvh, d, bs // 8), generator=gen, dtype=torch.int64)
+    vq = torch.randint(-2**31, 2**31, (nb, bs, kvh, d // 8), generator=gen, dtype=torch.int64)
+    kq, vq = kq.to(torch.int32), vq.to(torch.int32)
+    ks = torch.rand((nb, kvh, d, bs // g), generator=gen) + 0.01
+    km = torch.randn((nb, kvh, d, bs // g), generator=gen)
+    vs = torch.rand((nb, bs, kvh, d // g), generator=gen) + 0.01
+    vm = torch.randn((nb, bs, kvh, d // g), generator=gen)
+    cpu = (kq, ks, km, vq, vs, vm)
+    ring_k = torch.randn((len(lens), r_len, kvh, d), generator=gen).to(torch.bfloat16)
+    ring_v = torch.randn((len(lens), r_len, kvh, d), generator=gen).to(torch.bfloat16)
+    meta, wk, wv = [], [], []
+    for b, (kt, vt) in enumerate(tails):
+        row = len(lens) - 1 - b
+        kf, vf = (37 * b + 11) % r_len, (53 * b + 200) % r_len
+        meta.append([row, kf, kt, vf, vt])
+        wk.append(ring_k[row, [(kf + i) % r_len for i in range(kt)]])
+        wv.append(ring_v[row, [(vf + i) % r_len for i in range(vt)]])
+    meta = torch.tensor(meta, dtype=torch.int32)
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int64)
+    for out_dtype in (torch.bfloat16, torch.float32):
+        want_k, want_v = ref.dequant_gather(*cpu, table, torch.tensor(lens), out_dtype, g)
+        want_k = ref.overlay_residual(want_k, lens, wk)
+        want_v = ref.overlay_residual(want_v, lens, wv)
+        got_k, got_v = gather_dequant_with_residual(
+            to_dev(cpu, gpu_device), table.to(gpu_device), cu.to(gpu_device), sum(lens),
+            out_dtype, g, meta.to(gpu_device), ring_k.to(gpu_device), ring_v.to(gpu_device),
+        )
+        assert torch.equal(want_k, got_k.cpu()), out_dtype
+        assert torch.equal(want_v, got_v.cpu()), out_dtype
+
+
 @pytest.mark.parametrize("d,kvh,g,bs", GEOMS)
 @pytest.mark.parametrize("rep", [1, 5])
 def test_decode_attention_matches_oracle(gpu_device, d, kvh, g, bs, rep):
