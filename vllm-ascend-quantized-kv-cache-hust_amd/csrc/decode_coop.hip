@@ -1,7 +1,8 @@
 // SPDX-License-Identifier: Apache-2.0
-// Page-streaming KIVI INT4 decode for MI355X (gfx950): one workgroup of eight
-// waves (one per kv head) per piece of the decode plan, streaming whole pages
-// for all heads through a four-slot LDS ring.
+// Page-streaming KIVI INT4 decode for MI355X (gfx950): two workgroups of four
+// waves per piece of the decode plan, one per half of the 8 kv heads (a wave
+// per kv head), each streaming whole pages for its heads through a four-slot
+// LDS ring.
 //
 // Why: an int4 page of one request holds, per side, all kv heads' codes and
 // scales in a few contiguous runs -- keys [head][dim][128 tokens] (64 KiB),
@@ -11,19 +12,21 @@
 // and 4 bytes of every 32- or 64-byte value scale row.  Those lines are
 // requested again by other waves later, after the XCD's L2 may have dropped
 // them (config 3 fetched 1.23x, config 5 1.48x the algorithmic bytes), and
-// each wave issues about twice the line requests its bytes need.  Here the
-// workgroup streams each page once, every line whole, in four stages:
-//   K0  key codes of dims 0..63 (8 heads x 64 dims x 64 B = 32 KiB, a
+// each wave issues about twice the line requests its bytes need.  Here a
+// workgroup streams its half of each page once, every line whole, in four
+// stages:
+//   K0  key codes of dims 0..63 (4 heads x 64 dims x 64 B = 16 KiB, a
 //       contiguous 4 KiB run per head) + their scales / minima;
 //   K1  dims 64..127;
-//   V0  value codes of tokens 0..63 (64 tokens x 8 heads x 64 B = 32 KiB,
-//       contiguous) + their scales / minima;
+//   V0  value codes of tokens 0..63 (64 tokens x 4 heads x 64 B = 16 KiB, a
+//       256-byte run of each 512-byte token row) + their scales / minima;
 //   V1  tokens 64..127.
 // Each wave issues 5 LDS-DMA instructions per stage (16-byte lanes; its head's
-// key run, or 8 tokens of the value run, plus a slice of the scales), so a
-// stage is 40 instructions of whole lines.  The ring keeps three stages in
-// flight while one is computed; one barrier per stage both publishes the
-// stage and frees the slot the next DMA refills.
+// key run, or 16 tokens of the value runs, plus a slice of the scales), 20 a
+// stage per workgroup.  Both workgroups of a piece run on one XCD, where the
+// two halves of a value line or a value scale line meet in its L2.  The ring
+// keeps three stages in flight while one is computed; one barrier per stage
+// both publishes the stage and frees the slot the next DMA refills.
 //
 // Compute per wave (its kv head h, the GQA group's query heads as MFMA
 // columns) uses the transposing-read operands of decode_tr.h: scores for the
