@@ -340,8 +340,7 @@ __device__ __forceinline__ void page_softmax(int page_pos, int pb, int pe, int k
                                fmaxf(st.sacc[jm][2], st.sacc[jm][3])));
     }
   }
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  tmax = max_rows4(tmax);
   tr::Acc<NG>& acc = st.acc;
   const float m_new = fmaxf(acc.m_run, tmax);
   // m_new is finite: every page of an item holds at least one of its positions

@@ -117,9 +117,7 @@ __device__ __forceinline__ float sum_kg(float v) {  // over the 4 lane groups of
   return v;
 }
 __device__ __forceinline__ float max_kg(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
+  return max_rows4(v);
 }
 
 // ---- tile layout -------------------------------------------------------------

@@ -203,8 +203,7 @@ __device__ __forceinline__ void compute_tile(const TileRegs& t, int p, int pb, i
       s[j][r] = v;
       mx = fmaxf(mx, v);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  mx = max_rows4(mx);
   const float m_new = fmaxf(st.m, mx);
   // a fully masked prefix keeps m = -inf: nothing to rescale, p = 0
   const float m_use = m_new == -INFINITY ? 0.0f : m_new;

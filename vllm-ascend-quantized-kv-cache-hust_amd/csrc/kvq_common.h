@@ -235,6 +235,21 @@ __device__ __forceinline__ float kivi_dequant(uint32_t q, float scale, float mn)
   return __fadd_rn(__fmul_rn(static_cast<float>(q), scale), mn);
 }
 
+// Maximum over lanes l, l ^ 16, l ^ 32 and l ^ 48 (one value from each of
+// the wave's four 16-lane rows), with gfx950's row-swap permutes: VALU only.
+// (__shfl_xor goes through ds_bpermute: an LDS round trip plus address
+// arithmetic per step.)  permlane32_swap(u, u) returns [lo, lo] and [hi, hi]
+// (the wave's 32-lane halves), permlane16_swap(v, v) rows [0, 0, 2, 2] and
+// [1, 1, 3, 3]; the max of each pair covers the lanes the next step needs.
+__device__ __forceinline__ float max_rows4(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));  // lanes l, l ^ 32
+  const uint32_t v = __float_as_uint(m);
+  const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));           // and l ^ 16
+}
+
 __device__ __forceinline__ float fmin_ordered(float a, float b) { return b < a ? b : a; }
 __device__ __forceinline__ float fmax_ordered(float a, float b) { return b > a ? b : a; }
 

@@ -506,8 +506,7 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
         float tmax = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sacc[e / 4][g2][e % 4]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = max_rows4(tmax);
         // lazy offset: the row's exponent offset moves only when its max grows
         // past it by more than 8 (log2 units), so p <= 2^8 and most blocks
         // leave o and l unscaled; the normalisation by l makes the result the
