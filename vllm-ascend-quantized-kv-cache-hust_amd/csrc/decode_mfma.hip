@@ -111,11 +111,7 @@ __device__ __forceinline__ uint32_t code_pair_exact(uint32_t lo, uint32_t hi, ui
   return __builtin_bit_cast(uint32_t, v);
 }
 
-__device__ __forceinline__ float sum_kg(float v) {  // over the 4 lane groups of 16
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
-}
+__device__ __forceinline__ float sum_kg(float v) { return sum_rows4(v); }  // over the 4 lane groups of 16
 __device__ __forceinline__ float max_kg(float v) {
   return max_rows4(v);
 }

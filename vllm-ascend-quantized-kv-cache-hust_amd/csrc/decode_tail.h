@@ -79,16 +79,8 @@ __device__ __forceinline__ float half_f32<f16>(uint32_t w, int hi) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(hi ? w >> 16 : w)));
 }
 
-__device__ __forceinline__ float sum_kg(float v) {  // over the 4 lane groups of 16
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
-}
-__device__ __forceinline__ float max_kg(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
-}
+__device__ __forceinline__ float sum_kg(float v) { return sum_rows4(v); }  // over the 4 lane groups of 16
+__device__ __forceinline__ float max_kg(float v) { return max_rows4(v); }
 
 __device__ __forceinline__ int64_t clamp_page(const int32_t* __restrict__ bt, int p, int bsh,
                                               int64_t nb) {

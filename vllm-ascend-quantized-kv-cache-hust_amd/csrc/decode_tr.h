@@ -300,11 +300,7 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{lo, hi}), h2));
 }
 
-__device__ __forceinline__ float sum_kg(float v) {  // over the 4 lane groups of 16
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
-}
+__device__ __forceinline__ float sum_kg(float v) { return sum_rows4(v); }  // over the 4 lane groups of 16
 
 // x + (x of lane n ^ 8 in the same 16-lane row): v_add_f32 with a DPP
 // row_ror:8 operand.
@@ -474,8 +470,7 @@ __device__ __forceinline__ void compute_tile(const uint32_t* W, uint32_t buf_off
     tm[jm] = fmaxf(fmaxf(sacc[jm][0], sacc[jm][1]), fmaxf(sacc[jm][2], sacc[jm][3]));
   }
   float tmax = fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3]));
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  tmax = max_rows4(tmax);
   const float m_new = fmaxf(acc.m_run, tmax);
   const float alpha = acc.m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(acc.m_run - m_new);
   float ps[4];

@@ -316,8 +316,7 @@ int8_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, int hpw, 
       amax = fmaxf(amax, fabsf(qf[i]));
     }
   }
-  amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+  amax = max_rows4(amax);
   int ex = 0;
   if (amax > 0.0f) (void)frexpf(amax, &ex);
   const int e = amax > 0.0f ? 15 - ex : 0;  // max |Q' * 2^e| in [2^14, 2^15)
@@ -396,8 +395,7 @@ int8_decode_mfma_kernel(const TQ* __restrict__ query, int hq, int kvh, int hpw, 
 
   // ---- epilogue ----
   float l = st.l;
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
+  l = sum_rows4(l);
   float va[8];
 #pragma unroll
   for (int tt = 0; tt < 8; ++tt) va[tt] = to_f32(v_aq[static_cast<int64_t>(h) * kD + 8 * n + tt]);

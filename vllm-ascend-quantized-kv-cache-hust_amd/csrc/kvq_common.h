@@ -250,6 +250,18 @@ __device__ __forceinline__ float max_rows4(float x) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));           // and l ^ 16
 }
 
+// Sum over the same four lanes, rows paired first (l ^ 16), then halves
+// (l ^ 32): lane for lane the additions of v += shfl_xor(v, 16); v +=
+// shfl_xor(v, 32), so the result is bit-identical to that form.
+__device__ __forceinline__ float sum_rows4(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);  // lanes l, l ^ 16
+  const uint32_t v = __float_as_uint(s);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);          // and l ^ 32
+}
+
 __device__ __forceinline__ float fmin_ordered(float a, float b) { return b < a ? b : a; }
 __device__ __forceinline__ float fmax_ordered(float a, float b) { return b > a ? b : a; }
 

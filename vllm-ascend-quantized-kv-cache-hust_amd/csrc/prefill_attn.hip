@@ -201,8 +201,7 @@ prefill_attn_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
       sc[4 + r] = ok1 ? s1[r] * qscale : -INFINITY;
       tmax = fmaxf(tmax, fmaxf(sc[r], sc[4 + r]));
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = max_rows4(tmax);
     const float m_new = fmaxf(m_run, tmax);
     const float alpha = m_run == -INFINITY ? (m_new == -INFINITY ? 1.0f : 0.0f)
                                            : exp2f(m_run - m_new);
@@ -215,8 +214,7 @@ prefill_attn_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
       // normalise by the probabilities the MFMA actually sees
       psum += op_to_f32(pop[i], O{});
     }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
+    psum = sum_rows4(psum);
     l_run = l_run * alpha + psum;
     m_run = m_new;
     // PV: A = V^T rows (dims), 8 tokens {4*kg + r, 16 + 4*kg + r}
