@@ -32,16 +32,8 @@ using namespace kvq;
 constexpr int kMaxRep = 16;   // query heads per kv head handled by the generic kernel
 constexpr int kMaxDpl = 4;    // dims per lane (head_size <= 256)
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return max_wave64(v); }
+__device__ __forceinline__ float wave_sum(float v) { return sum_wave64(v); }
 
 // Staging of the K or V rows of positions [p0, p0 + n) (n <= 64) of one kv
 // head into LDS as fp32 [64][d + 1].  Positions below `hist` come from the
@@ -357,8 +349,7 @@ decode_combine_kernel(int hq, int d, const int32_t* __restrict__ seq_meta, int m
     const int s = s0 + lane;
     if (s < nw) mx = fmaxf(mx, ws_ml[2 * (static_cast<int64_t>(fw + s) * hq + hh)]);
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  mx = max_wave64(mx);
   float acc[KD];
 #pragma unroll
   for (int k = 0; k < KD; ++k) acc[k] = 0.0f;
@@ -402,8 +393,7 @@ decode_combine_kernel(int hq, int d, const int32_t* __restrict__ seq_meta, int m
       }
     }
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) wsum += __shfl_xor(wsum, o, 64);
+  wsum = sum_wave64(wsum);
   const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
 #pragma unroll
   for (int k = 0; k < KD; ++k) {

@@ -262,6 +262,33 @@ __device__ __forceinline__ float sum_rows4(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);          // and l ^ 32
 }
 
+// Whole-wave reductions without LDS: DPP inside each 16-lane row (quad
+// swaps, then the half-row and row mirrors, which pair the quads and halves
+// already reduced), then the row swaps above.  Every lane ends with the same
+// value (each step adds or maxes equal operand pairs in either order).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+__device__ __forceinline__ float max_wave64(float x) {
+  x = fmaxf(x, dpp_f32<kDppQuadXor1>(x));
+  x = fmaxf(x, dpp_f32<kDppQuadXor2>(x));
+  x = fmaxf(x, dpp_f32<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp_f32<kDppRowMirror>(x));
+  return max_rows4(x);
+}
+__device__ __forceinline__ float sum_wave64(float x) {
+  x += dpp_f32<kDppQuadXor1>(x);
+  x += dpp_f32<kDppQuadXor2>(x);
+  x += dpp_f32<kDppHalfMirror>(x);
+  x += dpp_f32<kDppRowMirror>(x);
+  return sum_rows4(x);
+}
+
 __device__ __forceinline__ float fmin_ordered(float a, float b) { return b < a ? b : a; }
 __device__ __forceinline__ float fmax_ordered(float a, float b) { return b > a ? b : a; }
 
