@@ -274,6 +274,24 @@ constexpr int kFaBlock = 64;  // keys per block
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s* lds_v4s_ptr;
 
+// LDS DMA of 16 bytes per lane from base + voff (base uniform, in SGPRs;
+// voff the lane's 32-bit byte offset) to LDS bytes m0 + 16 * lane (m0
+// uniform), so no 64-bit address is formed per lane.  The s_nop covers the
+// M0-write hazard.  Inline asm, outside the compiler's wait counting: the
+// kernel waits for every block's DMA explicitly (wait_vmcnt<0> before the
+// barrier that publishes it).
+__device__ __forceinline__ void dma16_so(const char* base, uint32_t voff, uint32_t m0) {
+  m0 = __builtin_amdgcn_readfirstlane(m0);
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(base), "{m0}"(m0)
+               : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(p)));
+}
+
 template <int D>
 struct FaLds {
   static constexpr int K_BYTES = kFaBlock * D * 2;
@@ -389,7 +407,7 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
     const char* gb = reinterpret_cast<const char*>(base + static_cast<int64_t>(kb) * row_stride);
     if (kb + kFaBlock <= lk) {  // uniform: only the last block clamps
 #pragma unroll
-      for (int i = 0; i < KINST; ++i) dma16(gb + off[i], dst + 1024 * (wave * KINST + i));
+      for (int i = 0; i < KINST; ++i) dma16_so(gb, off[i], lds_addr(dst + 1024 * (wave * KINST + i)));
     } else {
 #pragma unroll
       for (int i = 0; i < KINST; ++i) {
@@ -609,9 +627,17 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
     }
     if (i + 1 < nblk) wait_vmcnt<0>();  // block i + 2's keys and i + 1's values landed
   };
-  for (int i = 0; i < nblk; ++i) {
-    const int odd = i & 1;
-    step(odd ? kbuf0 : kbuf1, odd ? vbuf1 : vbuf0, odd ? kbuf1 : kbuf0, odd ? vbuf0 : vbuf1, i);
+  // two steps per iteration, so that each step's buffers are compile-time
+  // LDS offsets (folded into the reads' immediates instead of per-read adds)
+  int i = 0;
+  for (; i + 1 < nblk; i += 2) {
+    step(kbuf1, vbuf0, kbuf0, vbuf1, i);
+    __syncthreads();
+    step(kbuf0, vbuf1, kbuf1, vbuf0, i + 1);
+    __syncthreads();
+  }
+  if (i < nblk) {
+    step(kbuf1, vbuf0, kbuf0, vbuf1, i);
     __syncthreads();
   }
 
