@@ -329,6 +329,7 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   // 16-lane groups of one LDS cycle read
   auto vswz = [](int r) { return 2 * (r % 4) + (PPR >= 16 ? 8 * ((r / 4) % 2) : 0); };
   extern __shared__ __align__(16) char lds[];
+  const uint32_t lds0 = lds_addr(lds);  // LDS byte address of the buffers (DMA M0)
 
   // Workgroup ids go to the XCDs round-robin.  The rep * qblocks workgroups
   // that stream one (request, kv head)'s K/V run on one XCD, one such pair
@@ -407,7 +408,8 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
     const char* gb = reinterpret_cast<const char*>(base + static_cast<int64_t>(kb) * row_stride);
     if (kb + kFaBlock <= lk) {  // uniform: only the last block clamps
 #pragma unroll
-      for (int i = 0; i < KINST; ++i) dma16_so(gb, off[i], lds_addr(dst + 1024 * (wave * KINST + i)));
+      for (int i = 0; i < KINST; ++i)
+        dma16_so(gb, off[i], lds0 + static_cast<uint32_t>(dst - lds) + 1024u * (wave * KINST + i));
     } else {
 #pragma unroll
       for (int i = 0; i < KINST; ++i) {
