@@ -540,6 +540,41 @@ def test_mfma_lane_layout(gpu_device):
     assert torch.equal(d.cpu(), a.float() @ b.float())
 
 
+def test_lane_reductions(gpu_device):
+    """The permlane / DPP reductions the kernels use: the four-row max and sum
+    (the sum in the shuffle form's order, bit for bit) and the whole-wave max
+    and sum (every lane the same value)."""
+    from vllm_ascend_quantized_kv_cache.ops import _native
+
+    g = torch.Generator().manual_seed(6)
+    x = (torch.rand(16, 64, generator=g, dtype=torch.float64) - 0.5) * 2.0 ** torch.randint(
+        -20, 20, (16, 64), generator=g, dtype=torch.int64).double()
+    x = x.float()
+    x[3, 17] = float("-inf")  # a masked score
+    dx = x.to(gpu_device).contiguous()
+    out = torch.empty(16, 64, 4, dtype=torch.float32, device=gpu_device)
+    rc = _native.lib().kvq_selftest_lane_reductions(dx.data_ptr(), out.data_ptr(),
+                                                    _native.stream_of(out))
+    _native.check(rc, "kvq_selftest_lane_reductions")
+    out = out.cpu()
+    lanes = torch.arange(64)
+    for t in range(16):
+        v = x[t]
+        m4 = torch.maximum(torch.maximum(v, v[lanes ^ 16]), torch.maximum(v[lanes ^ 32], v[lanes ^ 48]))
+        s1 = v + v[lanes ^ 16]  # float32 adds, the shuffle form's order
+        s4 = s1 + s1[lanes ^ 32]
+        assert torch.equal(out[t, :, 0], m4), t
+        assert torch.equal(out[t, :, 1], s4), t
+        assert torch.equal(out[t, :, 2], torch.full((64,), float(v.max()))), t
+        ws = out[t, :, 3]
+        assert torch.equal(ws, ws[:1].expand(64)), t
+        exact = float(v.double().sum())
+        if torch.isfinite(v).all():
+            assert abs(float(ws[0]) - exact) <= 1e-5 * float(v.double().abs().sum()), t
+        else:
+            assert float(ws[0]) == exact, t
+
+
 def test_lds_dma_lane_layout(gpu_device):
     """global_load_lds writes lane i's bytes at LDS base + size * i (16 B and 4 B lanes)."""
     from vllm_ascend_quantized_kv_cache.ops import _native

@@ -1048,6 +1048,21 @@ __global__ void lds_dma_probe_kernel(const uint32_t* __restrict__ src, uint32_t*
   for (int i = 0; i < 5; ++i) dst[64 * i + lane] = l[64 * i + lane];
 }
 
+// The cross-lane reductions the kernels use (kvq_common.h), on 16 rounds of
+// 64 values: dst[4 (64 t + l) + {0, 1, 2, 3}] = max_rows4, sum_rows4,
+// max_wave64, sum_wave64 of lane l's value src[64 t + l].
+__global__ void lane_reduction_probe_kernel(const float* __restrict__ src, float* __restrict__ dst) {
+  const int lane = threadIdx.x;
+  for (int t = 0; t < 16; ++t) {
+    const float x = src[64 * t + lane];
+    float* o = dst + 4 * (64 * t + lane);
+    o[0] = max_rows4(x);
+    o[1] = sum_rows4(x);
+    o[2] = max_wave64(x);
+    o[3] = sum_wave64(x);
+  }
+}
+
 // 16x32 (A) times 32x16 (B) through the same intrinsic and operand mapping the
 // decode kernels rely on: lane l holds A[l%16][8*(l/16)+i] and B[8*(l/16)+i][l%16];
 // the result lands as D[4*(l/16)+r][l%16].
@@ -1185,6 +1200,14 @@ extern "C" int kvq_selftest_mfma_f16(const void* a, const void* b, float* d, voi
   hipLaunchKernelGGL(mfma_layout_probe_kernel, dim3(1), dim3(64), 0,
                      static_cast<hipStream_t>(stream), static_cast<const _Float16*>(a),
                      static_cast<const _Float16*>(b), d);
+  KVQ_LAUNCH_CHECK();
+  return KVQ_OK;
+}
+
+extern "C" int kvq_selftest_lane_reductions(const float* src, float* dst, void* stream) {
+  if (!src || !dst) return KVQ_ERR_INVALID;
+  hipLaunchKernelGGL(lane_reduction_probe_kernel, dim3(1), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), src, dst);
   KVQ_LAUNCH_CHECK();
   return KVQ_OK;
 }

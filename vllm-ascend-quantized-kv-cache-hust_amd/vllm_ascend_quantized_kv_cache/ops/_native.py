@@ -84,6 +84,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "kvq_selftest_mfma_f16": (_I, [_P, _P, _P, _P]),
     "kvq_selftest_lds_dma": (_I, [_P, _P, _P]),
+    "kvq_selftest_lane_reductions": (_I, [_P, _P, _P]),
     "kvq_int8_decode_workspace_bytes": (_I64, [_I64, _I, _I]),
     "kvq_int8_decode_attn": (
         _I,
