@@ -413,9 +413,11 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
     } else {
 #pragma unroll
       for (int i = 0; i < KINST; ++i) {
-        const int back = kb + krow[i] >= lk ? kb + krow[i] - (lk - 1) : 0;  // rows to step back
-        dma16(gb + off[i] - static_cast<int64_t>(back) * row_stride * 2,
-              dst + 1024 * (wave * KINST + i));
+        // rows past the end step back to row lk - 1 - kb of the block (>= 0),
+        // so the offset from the block's first row stays non-negative
+        const int back = kb + krow[i] >= lk ? kb + krow[i] - (lk - 1) : 0;
+        dma16_so(gb, off[i] - static_cast<uint32_t>(back) * static_cast<uint32_t>(row_stride * 2),
+                 lds0 + static_cast<uint32_t>(dst - lds) + 1024u * (wave * KINST + i));
       }
     }
   };
