@@ -244,10 +244,15 @@ __device__ __forceinline__ float kivi_dequant(uint32_t q, float scale, float mn)
 __device__ __forceinline__ float max_rows4(float x) {
   const uint32_t u = __float_as_uint(x);
   const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));  // lanes l, l ^ 32
-  const uint32_t v = __float_as_uint(m);
+  // med3(a, b, FLT_MAX) is max(a, b) for every a, b <= FLT_MAX (-inf
+  // included), without the canonicalizing moves fmaxf puts in front of
+  // values the compiler cannot vouch for (with +inf as the third operand the
+  // compiler turns it back into fmaxf)
+  constexpr float kBig = 0x1.fffffep127f;
+  const float m = __builtin_amdgcn_fmed3f(__uint_as_float(a[0]), __uint_as_float(a[1]), kBig);
+  const uint32_t v = __float_as_uint(m);  // lanes l, l ^ 32
   const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));           // and l ^ 16
+  return __builtin_amdgcn_fmed3f(__uint_as_float(b[0]), __uint_as_float(b[1]), kBig);  // and l ^ 16
 }
 
 // Sum over the same four lanes, rows paired first (l ^ 16), then halves

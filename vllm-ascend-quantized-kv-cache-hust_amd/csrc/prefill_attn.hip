@@ -520,24 +520,35 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
             sacc[e / 4][g2][e % 4] = 16 * (e / 4) + e % 4 <= rel ? sacc[e / 4][g2][e % 4] : -INFINITY;
         }
       }
-      float m_off[NG], alpha[NG];
+      float m_off[NG], alpha[NG], tmax[NG];
+      // row maxima: two chains per column group, the groups side by side,
+      // then the cross-row steps of both groups together
 #pragma unroll
       for (int g2 = 0; g2 < NG; ++g2) {
-        float tmax = -INFINITY;
+        float ta = -INFINITY, tb = -INFINITY;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sacc[e / 4][g2][e % 4]);
-        tmax = max_rows4(tmax);
+        for (int e = 0; e < 8; ++e) {
+          ta = fmaxf(ta, sacc[e / 4][g2][e % 4]);
+          tb = fmaxf(tb, sacc[2 + e / 4][g2][e % 4]);
+        }
+        tmax[g2] = fmaxf(ta, tb);
+      }
+#pragma unroll
+      for (int g2 = 0; g2 < NG; ++g2) tmax[g2] = max_rows4(tmax[g2]);
+#pragma unroll
+      for (int g2 = 0; g2 < NG; ++g2) {
         // lazy offset: the row's exponent offset moves only when its max grows
         // past it by more than 8 (log2 units), so p <= 2^8 and most blocks
         // leave o and l unscaled; the normalisation by l makes the result the
         // same softmax whatever offset the row settled on
-        const bool grow = tmax > m_run[g2] + lazy_thr;  // raw-score units
-        const float m_new = grow ? tmax : m_run[g2];
+        const bool grow = tmax[g2] > m_run[g2] + lazy_thr;  // raw-score units
+        const float m_new = grow ? tmax[g2] : m_run[g2];
         m_off[g2] = m_new == -INFINITY ? 0.0f : -qscale * m_new;
-        alpha[g2] = !grow ? 1.0f
-                          : (m_run[g2] == -INFINITY
-                                 ? 0.0f
-                                 : __builtin_amdgcn_exp2f(__builtin_fmaf(qscale, m_run[g2], m_off[g2])));
+        // computed on every lane (a select, not a branch); used only when the
+        // offset grows from a finite one
+        const float e = __builtin_amdgcn_exp2f(
+            __builtin_fmaf(qscale, m_run[g2] == -INFINITY ? 0.0f : m_run[g2], m_off[g2]));
+        alpha[g2] = !grow ? 1.0f : (m_run[g2] == -INFINITY ? 0.0f : e);
         m_run[g2] = m_new;
       }
       bool rescale = false;
