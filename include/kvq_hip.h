@@ -397,10 +397,12 @@ int kvq_selftest_lds_dma(const void* src, void* dst, void* stream);
 
 /* One wave applies the cross-lane reductions the kernels use to 16 rounds of
  * 64 floats src[64 t + l] and writes, for lane l of round t,
- * dst[4 (64 t + l) + 0..3] = the max over lanes l, l^16, l^32, l^48
- * (permlane row swaps), their sum as (x_l + x_l^16) + (x_l^32 + x_l^48), and
- * the max and the sum over all 64 lanes (DPP steps plus the row swaps).  No
- * counterpart in the reference; it pins the gfx950 lane semantics. */
+ * dst[6 (64 t + l) + 0..5] = the max over lanes l, l^16, l^32, l^48
+ * (permlane row swaps), their sum as (x_l + x_l^16) + (x_l^32 + x_l^48), the
+ * max and the sum over all 64 lanes (DPP steps plus the row swaps), and the
+ * four-row maxima of round t and of round (t + 1) % 16 taken together (the
+ * paired form).  No counterpart in the reference; it pins the gfx950 lane
+ * semantics. */
 int kvq_selftest_lane_reductions(const float* src, float* dst, void* stream);
 
 #ifdef __cplusplus

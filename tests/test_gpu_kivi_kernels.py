@@ -542,8 +542,8 @@ def test_mfma_lane_layout(gpu_device):
 
 def test_lane_reductions(gpu_device):
     """The permlane / DPP reductions the kernels use: the four-row max and sum
-    (the sum in the shuffle form's order, bit for bit) and the whole-wave max
-    and sum (every lane the same value)."""
+    (the sum in the shuffle form's order, bit for bit), the whole-wave max and
+    sum (every lane the same value), and the paired four-row max."""
     from vllm_ascend_quantized_kv_cache.ops import _native
 
     g = torch.Generator().manual_seed(6)
@@ -552,18 +552,25 @@ def test_lane_reductions(gpu_device):
     x = x.float()
     x[3, 17] = float("-inf")  # a masked score
     dx = x.to(gpu_device).contiguous()
-    out = torch.empty(16, 64, 4, dtype=torch.float32, device=gpu_device)
+    out = torch.empty(16, 64, 6, dtype=torch.float32, device=gpu_device)
     rc = _native.lib().kvq_selftest_lane_reductions(dx.data_ptr(), out.data_ptr(),
                                                     _native.stream_of(out))
     _native.check(rc, "kvq_selftest_lane_reductions")
     out = out.cpu()
     lanes = torch.arange(64)
+
+    def max4(v):
+        return torch.maximum(torch.maximum(v, v[lanes ^ 16]), torch.maximum(v[lanes ^ 32], v[lanes ^ 48]))
+
     for t in range(16):
         v = x[t]
-        m4 = torch.maximum(torch.maximum(v, v[lanes ^ 16]), torch.maximum(v[lanes ^ 32], v[lanes ^ 48]))
+        m4 = max4(v)
         s1 = v + v[lanes ^ 16]  # float32 adds, the shuffle form's order
         s4 = s1 + s1[lanes ^ 32]
         assert torch.equal(out[t, :, 0], m4), t
+        # the paired form: each value gets its own four-row max, not the other's
+        assert torch.equal(out[t, :, 4], m4), t
+        assert torch.equal(out[t, :, 5], max4(x[(t + 1) % 16])), t
         assert torch.equal(out[t, :, 1], s4), t
         assert torch.equal(out[t, :, 2], torch.full((64,), float(v.max()))), t
         ws = out[t, :, 3]

@@ -1055,11 +1055,15 @@ __global__ void lane_reduction_probe_kernel(const float* __restrict__ src, float
   const int lane = threadIdx.x;
   for (int t = 0; t < 16; ++t) {
     const float x = src[64 * t + lane];
-    float* o = dst + 4 * (64 * t + lane);
+    float* o = dst + 6 * (64 * t + lane);
     o[0] = max_rows4(x);
     o[1] = sum_rows4(x);
     o[2] = max_wave64(x);
     o[3] = sum_wave64(x);
+    float px = x, py = src[64 * ((t + 1) % 16) + lane];
+    max_rows4_pair(px, py);
+    o[4] = px;
+    o[5] = py;
   }
 }
 

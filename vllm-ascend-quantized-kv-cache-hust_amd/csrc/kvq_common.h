@@ -255,6 +255,24 @@ __device__ __forceinline__ float max_rows4(float x) {
   return __builtin_amdgcn_fmed3f(__uint_as_float(b[0]), __uint_as_float(b[1]), kBig);  // and l ^ 16
 }
 
+// max_rows4 of two values in three swaps instead of four: the first swap
+// trades x's lanes 32-63 for y's lanes 0-31, so one register carries x's
+// reduction in lanes 0-31 and y's in lanes 32-63 until the last swap hands
+// each half to every lane.
+__device__ __forceinline__ void max_rows4_pair(float& x, float& y) {
+  constexpr float kBig = 0x1.fffffep127f;
+  // a[0] = (x lanes 0-31, y lanes 0-31), a[1] = (x lanes 32-63, y lanes 32-63)
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  const uint32_t z = __float_as_uint(
+      __builtin_amdgcn_fmed3f(__uint_as_float(a[0]), __uint_as_float(a[1]), kBig));
+  const auto b = __builtin_amdgcn_permlane16_swap(z, z, false, false);
+  const uint32_t w = __float_as_uint(
+      __builtin_amdgcn_fmed3f(__uint_as_float(b[0]), __uint_as_float(b[1]), kBig));
+  const auto c = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  x = __uint_as_float(c[0]);
+  y = __uint_as_float(c[1]);
+}
+
 // Sum over the same four lanes, rows paired first (l ^ 16), then halves
 // (l ^ 32): lane for lane the additions of v += shfl_xor(v, 16); v +=
 // shfl_xor(v, 32), so the result is bit-identical to that form.

@@ -267,6 +267,9 @@ prefill_attn_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
 //                  address, k = 0..3).
 // The rescale needs no shuffles: S^T and O^T both put the lane's query in
 // its column.
+// The common step's softmax is the row maxima, one compare per column, and an
+// fma and exp2 per score; the offset bookkeeping (new offset, rescale factor)
+// sits in the branch that the lazy offset rarely takes.
 
 constexpr int kFaGroupRows = 128;  // query rows per workgroup
 constexpr int kFaXcds = 8;         // XCDs workgroup ids are dealt over
@@ -367,6 +370,7 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   const int wave_last_pos = lk - lq + wave_last;
 
   // Q^T operands: group g2, k-step s: query row wrow0 + 16*g2 + n, dims 32s + 8kg + i
+  // (unscaled: exact in the operand type)
   u8v qop[NG][KS];
   int my_pos[NG];
   bool live[NG];
@@ -428,10 +432,18 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
   const int tr_chunk = (lane % 4) / 2;  // + 2j
   const int tr_half = 8 * (lane % 2);   // byte offset inside the 16-byte column
 
-  float m_run[NG];
-#pragma unroll
-  for (int g2 = 0; g2 < NG; ++g2) m_run[g2] = -INFINITY;
+  // Per query column: m_run, the raw score the exponent offset stands for
+  // (-inf before the first finite score); m_off = -qscale * m_run (0 while
+  // m_run is -inf), so p = 2^(qscale * s + m_off); m_thr = m_run + 8 / qscale,
+  // the raw score past which the offset moves (lazy offset, below).
   const float lazy_thr = 8.0f / qscale;  // qscale > 0
+  float m_run[NG], m_off[NG], m_thr[NG];
+#pragma unroll
+  for (int g2 = 0; g2 < NG; ++g2) {
+    m_run[g2] = -INFINITY;
+    m_off[g2] = 0.0f;
+    m_thr[g2] = -INFINITY;
+  }
   // l_acc[g2]: every row holds the running sum of the (rounded) P of query
   // column n, accumulated by an MFMA with an all-ones A, so it is the exact sum
   // of what the PV MFMAs saw and rescales together with o
@@ -508,7 +520,7 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
     if (active(i)) {
       // ---- online softmax of block i per query column ----
       // the max runs over raw scores (qscale > 0), the exponent is one fma:
-      // p = 2^(qscale * s - qscale * m)
+      // p = 2^(qscale * s + m_off)
       const bool full = kb + kFaBlock <= lk && (!causal || kb + kFaBlock - 1 <= lk - lq + wrow0);
       if (!full) {  // uniform: one branch, then a compare per score
 #pragma unroll
@@ -520,46 +532,55 @@ prefill_attn_fa_kernel(const T* __restrict__ q, const T* __restrict__ k,
             sacc[e / 4][g2][e % 4] = 16 * (e / 4) + e % 4 <= rel ? sacc[e / 4][g2][e % 4] : -INFINITY;
         }
       }
-      float m_off[NG], alpha[NG], tmax[NG];
+      float tmax[NG];
       // row maxima: two chains per column group, the groups side by side,
       // then the cross-row steps of both groups together
 #pragma unroll
       for (int g2 = 0; g2 < NG; ++g2) {
-        float ta = -INFINITY, tb = -INFINITY;
+        // med3(a, b, FLT_MAX) = max(a, b) for scores (never +inf or NaN),
+        // without the canonicalizing moves a two-operand fmaxf gets
+        constexpr float kBig = 0x1.fffffep127f;
+        float ta = __builtin_amdgcn_fmed3f(sacc[0][g2][0], sacc[0][g2][1], kBig);
+        float tb = __builtin_amdgcn_fmed3f(sacc[2][g2][0], sacc[2][g2][1], kBig);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
+        for (int e = 2; e < 8; ++e) {
           ta = fmaxf(ta, sacc[e / 4][g2][e % 4]);
           tb = fmaxf(tb, sacc[2 + e / 4][g2][e % 4]);
         }
         tmax[g2] = fmaxf(ta, tb);
       }
+      if constexpr (NG == 2) {
+        max_rows4_pair(tmax[0], tmax[1]);
+      } else {
 #pragma unroll
-      for (int g2 = 0; g2 < NG; ++g2) tmax[g2] = max_rows4(tmax[g2]);
+        for (int g2 = 0; g2 < NG; ++g2) tmax[g2] = max_rows4(tmax[g2]);
+      }
+      // lazy offset: a column's offset moves only when its max grows past
+      // m_run by more than 8 (log2 units), so p <= 2^8 and most blocks skip
+      // the branch (o, l and the offsets stay); the normalisation by l makes
+      // the result the same softmax whatever offset the column settled on
+      bool grow[NG], rescale = false;
 #pragma unroll
       for (int g2 = 0; g2 < NG; ++g2) {
-        // lazy offset: the row's exponent offset moves only when its max grows
-        // past it by more than 8 (log2 units), so p <= 2^8 and most blocks
-        // leave o and l unscaled; the normalisation by l makes the result the
-        // same softmax whatever offset the row settled on
-        const bool grow = tmax[g2] > m_run[g2] + lazy_thr;  // raw-score units
-        const float m_new = grow ? tmax[g2] : m_run[g2];
-        m_off[g2] = m_new == -INFINITY ? 0.0f : -qscale * m_new;
-        // computed on every lane (a select, not a branch); used only when the
-        // offset grows from a finite one
-        const float e = __builtin_amdgcn_exp2f(
-            __builtin_fmaf(qscale, m_run[g2] == -INFINITY ? 0.0f : m_run[g2], m_off[g2]));
-        alpha[g2] = !grow ? 1.0f : (m_run[g2] == -INFINITY ? 0.0f : e);
-        m_run[g2] = m_new;
+        grow[g2] = tmax[g2] > m_thr[g2];
+        rescale = rescale || grow[g2];
       }
-      bool rescale = false;
-#pragma unroll
-      for (int g2 = 0; g2 < NG; ++g2) rescale = rescale || alpha[g2] != 1.0f;
       if (__any(rescale)) {
 #pragma unroll
         for (int g2 = 0; g2 < NG; ++g2) {
-          l_acc[g2] *= alpha[g2];
+          const float m_new = grow[g2] ? tmax[g2] : m_run[g2];
+          // the first finite max finds o and l still zero
+          const float alpha =
+              !grow[g2] ? 1.0f
+                        : (m_run[g2] == -INFINITY
+                               ? 0.0f
+                               : __builtin_amdgcn_exp2f(qscale * (m_run[g2] - m_new)));
+          l_acc[g2] *= alpha;
 #pragma unroll
-          for (int j = 0; j < DB; ++j) o[j][g2] *= alpha[g2];
+          for (int j = 0; j < DB; ++j) o[j][g2] *= alpha;
+          m_run[g2] = m_new;
+          m_off[g2] = m_new == -INFINITY ? 0.0f : -qscale * m_new;
+          m_thr[g2] = m_new + lazy_thr;
         }
       }
       // raised wave priority from here to the end of the PV MFMAs: the SIMD's
