@@ -489,6 +489,46 @@ def test_plan_decode_pieces_invariants(cu_count, kvh, tile):
         assert max(cost) <= step + 2 * 32 * TAIL_POSITION_COST + tile
 
 
+def test_page_streaming_one_round_plan_weights_the_first_dispatched_pieces():
+    """Config 3's shape (32 requests of 2048-16384 positions, 8 KV heads, 256
+    CUs, page tiles): one round of 256 pieces whose first half (the first
+    workgroup on each CU) carries 1.4 times the cost of the second half, each
+    piece within a step of its share, the requests covered exactly."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
+        PAGE_TILE,
+        TAIL_POSITION_COST,
+        DecodeSeq,
+        plan_decode_pieces,
+    )
+
+    rng = random.Random(3)
+    seqs = []
+    for i in range(32):
+        n = rng.randrange(2048, 16385)
+        seqs.append(DecodeSeq(n, ((n - 1) // 128) * 128, n - 128, i, 0, 0))
+    meta, work, pieces = plan_decode_pieces(seqs, 8, 256, tile=PAGE_TILE)
+    assert len(pieces) - 1 == 256
+    cost = [
+        sum(-(-(e - p) // PAGE_TILE) * PAGE_TILE if k == 0 else (e - p) * TAIL_POSITION_COST
+            for _, p, e, k in work[pieces[i] : pieces[i + 1]].tolist())
+        for i in range(256)
+    ]
+    unit = sum(cost) / (1.4 * 128 + 128)
+    margin = PAGE_TILE + 2 * 32 * TAIL_POSITION_COST
+    for i, c in enumerate(cost):
+        share = 1.4 * unit if i < 128 else unit
+        assert abs(c - share) <= margin, (i, c, share)
+    ratio = (sum(cost[:128]) / 128) / (sum(cost[128:]) / 128)
+    assert 1.3 < ratio < 1.5
+    for b, s in enumerate(seqs):
+        first, count = int(meta[b, 6]), int(meta[b, 7])
+        pos = 0
+        for _, p, e, _ in work[first : first + count].tolist():
+            assert p == pos
+            pos = e
+        assert pos == s.seq_len
+
+
 def test_plan_pieces_rejects_other_tiles():
     from vllm_ascend_quantized_kv_cache.ops.kivi_decode import DecodeSeq, plan_decode_pieces
 

@@ -30,6 +30,14 @@ namespace {
 constexpr int kHeadSlotsPerCu = 8;
 constexpr double kPieceMaxCost = 4096;  // int4 positions per piece before a second round
 constexpr int kTailItemTokens = 64;     // positions per tail item in split plans
+// One-round page-streaming plans run two workgroups per CU, and the first
+// half of the pieces are the first workgroup dispatched to each CU.  While
+// both run, the SIMD arbiter issues the older workgroup's waves first, so
+// those pieces stream faster (config 3 on MI355X: 5.2 against 7.3 us per
+// page); they get this much more cost per piece, so that both workgroups of a
+// CU finish together instead of the younger one streaming alone, at half the
+// CU's requests in flight, at the end.
+constexpr double kFirstWaveShare = 1.4;
 
 struct Planner {
   const int32_t* seqs;
@@ -116,7 +124,8 @@ void plan_split(Planner& pl, int64_t split, bool paired) {
 // Equal-cost pieces: every request's positions laid end to end (int4 in
 // `tile`-position tiles -- 64, or 128 for the page-streaming kernel, whose
 // workgroups must not share a page -- tail in 32-position steps at `tail_cost`
-// per position), cut where the running cost crosses a multiple of total / slots.
+// per position), cut where the running cost crosses a multiple of total / slots
+// (one-round page-streaming plans: kFirstWaveShare times that for the first half).
 int64_t plan_pieces(Planner& pl, int kvh, int cu_count, double tail_cost, int64_t tile,
                     int32_t* pieces, int64_t cap_pieces) {
   int64_t slots = slots_for(kvh, cu_count);
@@ -125,6 +134,20 @@ int64_t plan_pieces(Planner& pl, int kvh, int cu_count, double tail_cost, int64_
       1, static_cast<int64_t>(std::ceil(total / (static_cast<double>(slots) * kPieceMaxCost))));
   const double dtile = static_cast<double>(tile);
   const double step = std::max(dtile, total / static_cast<double>(slots));
+  // the page-streaming kernel's single round: pieces [0, slots / 2) are the
+  // first workgroups on their CUs (two per CU, slots == CUs)
+  const bool skew = tile == 128 && slots == cu_count && slots >= 2 &&
+                    total / static_cast<double>(slots) >= 4 * dtile;
+  const int64_t first = slots / 2;
+  const double share_unit =
+      total / (kFirstWaveShare * static_cast<double>(first) + static_cast<double>(slots - first));
+  // cumulative cost at the end of piece j
+  auto target = [&](int64_t j) -> double {
+    if (!skew) return step * static_cast<double>(j + 1);
+    return j < first ? share_unit * kFirstWaveShare * static_cast<double>(j + 1)
+                     : share_unit * (kFirstWaveShare * static_cast<double>(first) +
+                                     static_cast<double>(j + 1 - first));
+  };
   int64_t np = 0;
   auto push = [&](int64_t v) {
     if (np >= cap_pieces + 1) {
@@ -134,12 +157,13 @@ int64_t plan_pieces(Planner& pl, int kvh, int cu_count, double tail_cost, int64_
     pieces[np++] = static_cast<int32_t>(v);
   };
   push(0);
-  double cum = 0.0, cut = step;
+  int64_t cut_j = 0;
+  double cum = 0.0, cut = target(0);
   // close the piece once the running cost reaches the cut
   auto after = [&](double unit) {
     if (cum >= cut - unit / 2 && np < slots && pl.n > pieces[np - 1]) {
       push(pl.n);
-      while (cut - unit / 2 <= cum) cut += step;
+      while (cut - unit / 2 <= cum) cut = target(++cut_j);
     }
   };
   for (int64_t b = 0; b < pl.batch && !pl.overflow; ++b) {

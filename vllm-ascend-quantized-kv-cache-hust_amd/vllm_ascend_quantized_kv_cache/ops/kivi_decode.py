@@ -159,7 +159,11 @@ def plan_decode_pieces(
     is ``slots = cu_count * WAVES_PER_CU / num_kv_heads`` times the rounds
     needed to keep pieces under ``PIECE_MAX_COST``: one wave per (piece, kv
     head) then fills the chip a whole number of times and every wave of a
-    round ends at about the same time.  A cut inside a request splits it into
+    round ends at about the same time (in a one-round plan with ``tile`` =
+    ``PAGE_TILE`` and one piece per CU, the first half of the pieces, which the
+    hardware dispatches first on their CUs and whose waves the arbiter then
+    favours, carry 1.4 times the cost of the second half, so that the two
+    workgroups sharing a CU finish together).  A cut inside a request splits it into
     items (int4 items start on multiples of ``tile``, 64 or ``PAGE_TILE``);
     ``pieces[k]`` is the first item of piece ``k``.  Planned natively
     (``kvq_plan_kivi_decode``).
