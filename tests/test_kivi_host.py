@@ -463,7 +463,11 @@ def test_plan_decode_pieces_invariants(cu_count, kvh, tile):
     for s in seqs:
         a = max(0, min(s.k_hist, s.v_hist, s.seq_len))
         total += -(-a // tile) * tile + (s.seq_len - a) * TAIL_POSITION_COST
-    slots *= max(1, -(-int(total) // int(slots * PIECE_MAX_COST)))  # whole rounds
+    per_round = slots
+    rounds = max(1, -(-int(total) // int(slots * PIECE_MAX_COST)))  # whole rounds
+    slots *= rounds
+    if tile == 128 and rounds >= 2 and total / slots >= 8 * tile:
+        slots += per_round  # the last round in pieces of half the cost
     assert 1 <= len(pieces) - 1 <= slots
     assert pieces[0] == 0 and pieces[-1] == len(work)
     assert all(a < b for a, b in zip(pieces[:-1], pieces[1:]))
@@ -479,7 +483,7 @@ def test_plan_decode_pieces_invariants(cu_count, kvh, tile):
             if kind == 0:
                 assert p % tile == 0 and e <= min(s.k_hist, s.v_hist) and e > p
         assert pos == s.seq_len
-    if len(pieces) - 1 == slots and slots > 1:
+    if len(pieces) - 1 == slots and slots > 1 and rounds == 1 and not (tile == 128 and slots == cu_count):
         cost = [
             sum(-(-(e - p) // tile) * tile if k == 0 else (e - p) * TAIL_POSITION_COST
                 for _, p, e, k in work[pieces[i] : pieces[i + 1]].tolist())
@@ -548,8 +552,17 @@ def test_page_streaming_plan_covers_any_amount_of_work_in_pieces():
     big = [DecodeSeq(32768, 32640, 32640, i, 0, 0) for i in range(256)]
     _, work, pieces = plan_decode(big, 8, 256, page_streaming=True)
     assert pieces is not None and pieces[0] == 0 and pieces[-1] == len(work)
-    # 32640 int4 positions + 128 tail positions at 6 each: 9 rounds of 256
-    assert len(pieces) - 1 == 256 * 9
+    # 32640 int4 positions + 128 tail positions at 6 each: 9 rounds of 256,
+    # the last of them cut into 512 pieces of half the cost
+    assert len(pieces) - 1 == 256 * 8 + 512
+    cost = [
+        sum(-(-(e - p) // 128) * 128 if k == 0 else (e - p) * 6.0
+            for _, p, e, k in work[pieces[i] : pieces[i + 1]].tolist())
+        for i in range(len(pieces) - 1)
+    ]
+    step = sum(cost) / (256 * 9)
+    assert all(abs(c - step) <= 128 + 2 * 32 * 6.0 for c in cost[:2048])
+    assert all(abs(c - step / 2) <= 128 + 2 * 32 * 6.0 for c in cost[2048:])
     int4 = work[work[:, 3] == 0]
     assert (int4[:, 1] % 128 == 0).all()
     assert page_streaming_applies(64, 8, 128, 128, 64, torch.bfloat16, torch.bfloat16)

@@ -125,15 +125,24 @@ void plan_split(Planner& pl, int64_t split, bool paired) {
 // `tile`-position tiles -- 64, or 128 for the page-streaming kernel, whose
 // workgroups must not share a page -- tail in 32-position steps at `tail_cost`
 // per position), cut where the running cost crosses a multiple of total / slots
-// (one-round page-streaming plans: kFirstWaveShare times that for the first half).
+// (one-round page-streaming plans: kFirstWaveShare times that for the first
+// half; several rounds: the last round in pieces of half that).
 int64_t plan_pieces(Planner& pl, int kvh, int cu_count, double tail_cost, int64_t tile,
                     int32_t* pieces, int64_t cap_pieces) {
-  int64_t slots = slots_for(kvh, cu_count);
+  const int64_t per_round = slots_for(kvh, cu_count);
   const double total = total_cost(pl, tail_cost, tile);
-  slots *= std::max<int64_t>(
-      1, static_cast<int64_t>(std::ceil(total / (static_cast<double>(slots) * kPieceMaxCost))));
+  const int64_t rounds = std::max<int64_t>(
+      1, static_cast<int64_t>(std::ceil(total / (static_cast<double>(per_round) * kPieceMaxCost))));
+  int64_t slots = per_round * rounds;
   const double dtile = static_cast<double>(tile);
   const double step = std::max(dtile, total / static_cast<double>(slots));
+  // Page-streaming plans of several rounds: the hardware hands the pieces to
+  // CUs as earlier ones finish, so the last pieces to start set the end; the
+  // last round is cut into twice as many pieces of half the cost, which halves
+  // the spread of those last starts and ends.
+  const bool split_last = tile == 128 && rounds >= 2 && step >= 8 * dtile;
+  const int64_t full = split_last ? per_round * (rounds - 1) : slots;
+  if (split_last) slots = full + 2 * per_round;
   // the page-streaming kernel's single round: pieces [0, slots / 2) are the
   // first workgroups on their CUs (two per CU, slots == CUs)
   const bool skew = tile == 128 && slots == cu_count && slots >= 2 &&
@@ -143,6 +152,8 @@ int64_t plan_pieces(Planner& pl, int kvh, int cu_count, double tail_cost, int64_
       total / (kFirstWaveShare * static_cast<double>(first) + static_cast<double>(slots - first));
   // cumulative cost at the end of piece j
   auto target = [&](int64_t j) -> double {
+    if (split_last && j >= full)
+      return step * static_cast<double>(full) + 0.5 * step * static_cast<double>(j + 1 - full);
     if (!skew) return step * static_cast<double>(j + 1);
     return j < first ? share_unit * kFirstWaveShare * static_cast<double>(j + 1)
                      : share_unit * (kFirstWaveShare * static_cast<double>(first) +

@@ -270,7 +270,9 @@ def step_plan_mode(impl, query: torch.Tensor, *, fixed: bool) -> tuple[int, int]
 
 
 def pieces_capacity(num_kv_heads: int, cu_count: int, rounds: int) -> int:
-    return max(1, cu_count * WAVES_PER_CU // max(1, num_kv_heads)) * max(1, rounds)
+    # plans of two or more rounds cut the last round into twice as many pieces
+    rounds = max(1, rounds)
+    return max(1, cu_count * WAVES_PER_CU // max(1, num_kv_heads)) * (rounds + (rounds > 1))
 
 
 def eager_capacities(batch: int, num_kv_heads: int, cu_count: int, seqs: np.ndarray
