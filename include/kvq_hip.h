@@ -53,7 +53,7 @@ enum {
 /* Decode work plans (kvq_plan_kivi_decode). */
 enum {
   KVQ_PLAN_DEFAULT = 0,       /* pieces when the work fills the chip once, else paired splits */
-  KVQ_PLAN_PIECES = 1,        /* equal-cost pieces (one or more rounds) */
+  KVQ_PLAN_PIECES = 1,        /* cost-balanced pieces (one or more rounds) */
   KVQ_PLAN_SPLIT = 2,         /* int4 ranges every split_tokens positions */
   KVQ_PLAN_SPLIT_PAIRED = 3,  /* as SPLIT, each range as an even/odd-chunk pair */
 };
@@ -170,9 +170,9 @@ int kvq_kivi_gather_dequant(const int32_t* k_quant, const float* k_scale, const 
  *   pieces      int32 [num_pieces + 1] or NULL: piece k is work items
  *               [pieces[k], pieces[k+1]).  At num_kv_heads 8, D 128,
  *               block_size 128, group_size 64 or 128, at most 16 query
- *               heads per kv head and 16-bit query and ring, one workgroup
- *               per piece streams the piece's kind-0 items page by page for
- *               all kv heads, then runs its tail items (plan with
+ *               heads per kv head and 16-bit query and ring, two workgroups
+ *               per piece (one per half of the kv heads) stream the piece's
+ *               kind-0 items page by page, then run its tail items (plan with
  *               split_tokens 128 so that no two pieces share a page).
  *               Elsewhere, where the MFMA kernel runs both kinds, one wave
  *               per (piece, kv head) runs its piece's items in order in a

@@ -151,7 +151,7 @@ def plan_decode_pieces(
     tail_cost: float = TAIL_POSITION_COST,
     tile: int = 64,
 ) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
-    """``(seq_meta, work, pieces)``: the work list cut into pieces of equal cost.
+    """``(seq_meta, work, pieces)``: the work list cut into cost-balanced pieces.
 
     Every request's positions, int4 part (in 64-position tiles) then tail
     (``tail_cost`` per position, in 32-position steps), are laid end to end
