@@ -145,7 +145,7 @@ int64_t plan_pieces(Planner& pl, int kvh, int cu_count, double tail_cost, int64_
   if (split_last) slots = full + 2 * per_round;
   // the page-streaming kernel's single round: pieces [0, slots / 2) are the
   // first workgroups on their CUs (two per CU, slots == CUs)
-  const bool skew = tile == 128 && slots == cu_count && slots >= 2 &&
+  const bool skew = tile == 128 && rounds == 1 && slots == cu_count && slots >= 2 &&
                     total / static_cast<double>(slots) >= 4 * dtile;
   const int64_t first = slots / 2;
   const double share_unit =
