@@ -33,8 +33,8 @@ constexpr int kTailItemTokens = 64;     // positions per tail item in split plan
 // One-round page-streaming plans run two workgroups per CU, and the first
 // half of the pieces are the first workgroup dispatched to each CU.  While
 // both run, the SIMD arbiter issues the older workgroup's waves first, so
-// those pieces stream faster (config 3 on MI355X: 5.2 against 7.3 us per
-// page); they get this much more cost per piece, so that both workgroups of a
+// those pieces stream faster (config 3 on MI355X with equal pieces: about 5.3
+// against 6.8 us per page); they get this much more cost per piece, so that both workgroups of a
 // CU finish together instead of the younger one streaming alone, at half the
 // CU's requests in flight, at the end.
 constexpr double kFirstWaveShare = 1.4;
@@ -121,7 +121,7 @@ void plan_split(Planner& pl, int64_t split, bool paired) {
   }
 }
 
-// Equal-cost pieces: every request's positions laid end to end (int4 in
+// Cost-balanced pieces: every request's positions laid end to end (int4 in
 // `tile`-position tiles -- 64, or 128 for the page-streaming kernel, whose
 // workgroups must not share a page -- tail in 32-position steps at `tail_cost`
 // per position), cut where the running cost crosses a multiple of total / slots
