@@ -239,14 +239,18 @@ def test_config3_decode_step_full_batch(gpu_device):
 
 def test_config5_decode_step_full_batch(gpu_device):
     """Config 5: 256 x 32768 tokens, Hq 64, G 64 (S = 80 B), 65,800 shuffled
-    pages (10.8 GB, past 2^31 bytes per side); the whole batch runs on the GPU
-    with the multi-round paired plan, requests 0, 85, 170 and 255 are compared
-    with the oracle."""
+    pages (10.8 GB, past 2^31 bytes per side); the whole batch runs through
+    forward() on the page-streaming decode (eight rounds of pieces, then the
+    last round in pieces of half the cost), and requests 0, 85, 170 and 255
+    (the last pieces) are compared with the oracle."""
     from vllm_ascend_quantized_kv_cache.ops.kivi_decode import DecodeSeq, plan_decode
 
     b, n = 256, 32768
-    # the plan at this size: split items in paired rounds, not one round of pieces
-    assert plan_decode([DecodeSeq(n + 1, *_incremental(n + 1, 128))] * b, 8)[2] is None
+    seqs = [DecodeSeq(n + 1, *_incremental(n + 1, 128))] * b
+    # without page streaming the plan at this size is split items, no pieces
+    assert plan_decode(seqs, 8)[2] is None
+    pieces = plan_decode(seqs, 8, page_streaming=True)[2]
+    assert pieces is not None and len(pieces) - 1 == 256 * 8 + 512
     kbuf = _kivi_decode_step(gpu_device, b=b, hq=64, kvh=8, d=128, g=64, r=128, bs=128,
                              lens=[n] * b, check={0, 85, 170, 255}, seed=5)
     assert kbuf.numel() > 2 ** 31
