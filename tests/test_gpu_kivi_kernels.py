@@ -162,13 +162,14 @@ def test_gather_bit_exact(gpu_device, d, kvh, g, bs):
 
 
 def _ring_case(dev, d, kvh, g, bs, r_len, lens, seed, ring_dtype=torch.float32, split=None,
-               stale=False):
+               stale=False, make=None):
     """Packed history for several requests plus residual rings (FIFO, wrapped).
 
     ``split(n) -> (hist_k, hist_v)``: the int4 history of each side (default:
     the incremental rule, ``ref.incremental_split``).  ``stale``: the bytes no
     pack writes hold NaN scales and minima and nonzero codes, as a reused
-    page would, so a read past a request's int4 history shows."""
+    page would, so a read past a request's int4 history shows.  ``make(n, kvh,
+    d, seed) -> (key, value)``: the request's K/V (default ``make_kv``)."""
     nb = sum(-(-n // bs) for n in lens) + 2
     maxb = max(-(-n // bs) for n in lens)
     table = torch.full((len(lens), maxb), -1, dtype=torch.int32)
@@ -189,7 +190,8 @@ def _ring_case(dev, d, kvh, g, bs, r_len, lens, seed, ring_dtype=torch.float32, 
     seqs, windows_k, windows_v, keys, values = [], [], [], [], []
     gen = torch.Generator().manual_seed(seed + 1)
     for b, n in enumerate(lens):
-        key, value = make_kv(n, kvh, d, seed=seed * 31 + b)
+        key, value = (make or (lambda n_, h_, d_, sd: make_kv(n_, h_, d_, seed=sd)))(
+            n, kvh, d, seed * 31 + b)
         keys.append(key)
         values.append(value)
         hk, hv = split(n) if split else ref.incremental_split(n, r_len)
@@ -594,3 +596,56 @@ def test_lds_dma_lane_layout(gpu_device):
                                             _native.stream_of(dst))
     _native.check(rc, "kvq_selftest_lds_dma")
     assert torch.equal(dst.cpu(), src)
+
+
+@pytest.mark.parametrize("kvh,g,bs,rep,dtype",
+                         [(8, 128, 128, 5, torch.bfloat16), (8, 64, 128, 8, torch.float16),
+                          (4, 32, 64, 4, torch.bfloat16)])
+def test_decode_with_row_maxima_growing_every_page(gpu_device, kvh, g, bs, rep, dtype):
+    """Keys along one direction per kv head with a magnitude that grows with
+    the position (even heads) or shrinks (odd heads), queries along it: every
+    page and tail tile raises the even heads' running maximum, so the softmax
+    rescales at each one, in the page-streaming decode (8 kv heads) and the
+    per-wave one (4), int4 pages and tails alike."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
+        DecodeSeq,
+        kivi_decode_attention,
+        page_streaming_applies,
+    )
+
+    d = 128
+    r_len = 2 * g if g <= 64 else g
+    lens = [r_len * 7 + 3, r_len * 2 + 64, 700]
+    u = torch.randn(kvh, d, generator=torch.Generator().manual_seed(17))
+    u = u / u.norm(dim=1, keepdim=True)
+    sign = torch.tensor([1.0 if h % 2 == 0 else -1.0 for h in range(kvh)])
+
+    def make(n, h_, d_, sd):
+        gen = torch.Generator().manual_seed(sd)
+        pos = torch.arange(n, dtype=torch.float32)
+        key = u[None] * (sign[None, :, None] * 0.05 * pos[:, None, None]) + 0.05 * torch.randn(
+            n, h_, d_, generator=gen)
+        value = torch.randn(n, h_, d_, generator=gen)
+        return key.to(dtype), value.to(dtype)
+
+    cpu, table, ring_k, ring_v, seqs, wk, wv, _, _ = _ring_case(
+        gpu_device, d, kvh, g, bs, r_len, lens, seed=51, ring_dtype=dtype, make=make
+    )
+    hq = kvh * rep
+    q = (8.0 * u.repeat_interleave(rep, dim=0)[None].expand(len(lens), hq, d)
+         + 0.05 * torch.randn(len(lens), hq, d, generator=torch.Generator().manual_seed(9)))
+    q = q.to(dtype)
+    scale = d ** -0.5
+    dk, dv = ref.dequant_gather(*cpu, table, torch.tensor(lens), torch.float32, g)
+    dk = ref.overlay_residual(dk, lens, wk)
+    dv = ref.overlay_residual(dv, lens, wv)
+    want = ref.attention(q, dk, dv, [1] * len(lens), lens, scale, causal=True)
+    dseqs = [DecodeSeq(n, hk, hv, row, ks_, vs_) for (n, hk, hv, row, ks_, vs_) in seqs]
+    assert page_streaming_applies(hq, kvh, d, bs, g, dtype, dtype) == (kvh == 8)
+    dev = gpu_device
+    # the default plan: pieces on page bounds for the page-streaming decode
+    got = kivi_decode_attention(
+        q.to(dev), to_dev(cpu, dev), table.to(dev), dseqs, ring_k.to(dev), ring_v.to(dev),
+        scale, g,
+    )
+    torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
