@@ -136,3 +136,56 @@ def test_int8_decode_empty_request_is_zero(gpu_device):
                                     k_inv, v_inv)
     want = ref.attention(q[live], dk, dv, [1, 1], [lens[i] for i in live], scale, causal=True)
     torch.testing.assert_close(got[live], want, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("kvh,d,bs,rep", [(8, 128, 128, 4), (4, 64, 32, 2)])
+def test_int8_decode_with_row_maxima_growing_every_block(gpu_device, kvh, d, bs, rep):
+    """Keys along one direction per kv head with a magnitude that grows with
+    the position (even heads) or shrinks (odd heads), queries along it: the
+    even heads' running maximum rises on every block of every item, so the
+    online softmax rescales each time; split items too."""
+    from vllm_ascend_quantized_kv_cache.ops.int8_ops import int8_decode_attention
+
+    dtype = torch.bfloat16
+    lens = [513, 1000, 129]
+    u = torch.randn(kvh, d, generator=torch.Generator().manual_seed(23))
+    u = u / u.norm(dim=1, keepdim=True)
+    sign = torch.tensor([1.0 if h % 2 == 0 else -1.0 for h in range(kvh)])
+
+    def make(n, seed):
+        gen = torch.Generator().manual_seed(seed)
+        pos = torch.arange(n, dtype=torch.float32)
+        key = u[None] * (sign[None, :, None] * 0.05 * pos[:, None, None]) + 0.05 * torch.randn(
+            n, kvh, d, generator=gen)
+        return key.to(dtype), torch.randn(n, kvh, d, generator=gen).to(dtype)
+
+    nblk = [-(-n // bs) for n in lens]
+    nb = sum(nblk) + 3
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(7))
+    table = torch.zeros(len(lens), max(nblk), dtype=torch.int32)
+    used = 0
+    for i, n in enumerate(nblk):
+        table[i, :n] = perm[used : used + n]
+        used += n
+    kc = torch.zeros(nb, bs, kvh, d, dtype=torch.int8)
+    vc = torch.zeros_like(kc)
+    # scales from the longest ramp, so no request's keys clip
+    first_k, first_v = make(max(lens), 99)
+    k_inv, v_inv, k_aq, v_aq = ref.int8_calc_scales(first_k, first_v)
+    for i, n in enumerate(lens):
+        key, value = make(n, 100 + i)
+        ref.int8_reshape_and_cache(key, value, k_inv, v_inv, slots_for(table[i], range(n), bs),
+                                   kc, vc)
+    hq = kvh * rep
+    q = (8.0 * u.repeat_interleave(rep, dim=0)[None].expand(len(lens), hq, d)
+         + 0.05 * torch.randn(len(lens), hq, d, generator=torch.Generator().manual_seed(3)))
+    q = q.to(dtype)
+    scale = d ** -0.5
+    dk, dv = ref.int8_paged_dequant(kc, vc, table, lens, torch.float32, k_inv, v_inv)
+    want = ref.attention(q, dk, dv, [1] * len(lens), lens, scale, causal=True)
+    for split in (None, 256):
+        got = int8_decode_attention(
+            q.to(gpu_device), kc.to(gpu_device), vc.to(gpu_device), k_aq.to(gpu_device),
+            v_aq.to(gpu_device), table.to(gpu_device), lens, scale, split_tokens=split,
+        )
+        torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
