@@ -649,3 +649,39 @@ def test_decode_with_row_maxima_growing_every_page(gpu_device, kvh, g, bs, rep, 
         scale, g,
     )
     torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
+
+
+def test_decode_combine_of_many_items_per_request(gpu_device):
+    """Split plans of 128 positions: one request in 158 items (the
+    combine's (m, l) pass and weighted sum run in three 64-item chunks), one
+    in 17 (one past the rows the combine preloads), one in 16, and a short
+    one, against the oracle."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
+        DecodeSeq,
+        kivi_decode_attention,
+        plan_decode_work,
+    )
+
+    d, kvh, g, bs, rep = 128, 8, 128, 128, 5
+    r_len = g
+    # int4 items of 128 up to min(k_hist, v_hist), then two 64-position tail items
+    lens = [20005, 15 * 128 + 10, 14 * 128 + 8, 70]
+    cpu, table, ring_k, ring_v, seqs, wk, wv, _, _ = _ring_case(
+        gpu_device, d, kvh, g, bs, r_len, lens, seed=61, ring_dtype=torch.bfloat16
+    )
+    dseqs = [DecodeSeq(n, hk, hv, row, ks_, vs_) for (n, hk, hv, row, ks_, vs_) in seqs]
+    meta, _ = plan_decode_work(dseqs, 128)
+    items = meta[:, 7].tolist()
+    assert items[0] > 128 and items[1] == 17 and items[2] == 16, items
+    hq = kvh * rep
+    q = torch.randn(len(lens), hq, d, generator=torch.Generator().manual_seed(12)).to(torch.bfloat16)
+    scale = d ** -0.5
+    dk, dv = ref.dequant_gather(*cpu, table, torch.tensor(lens), torch.float32, g)
+    dk = ref.overlay_residual(dk, lens, wk)
+    dv = ref.overlay_residual(dv, lens, wv)
+    want = ref.attention(q, dk, dv, [1] * len(lens), lens, scale, causal=True)
+    got = kivi_decode_attention(
+        q.to(gpu_device), to_dev(cpu, gpu_device), table.to(gpu_device), dseqs,
+        ring_k.to(gpu_device), ring_v.to(gpu_device), scale, g, split_tokens=128,
+    )
+    torch.testing.assert_close(got.float().cpu(), want, atol=1e-2, rtol=1e-2)
