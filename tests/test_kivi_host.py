@@ -1271,3 +1271,32 @@ def test_plan_decode_step_rolls_back_when_a_later_stage_raises():
             assert ring.state() != before
             raise RuntimeError("staging failed")
     assert ring.state() == before
+
+
+def test_page_tile_plan_of_two_rounds_at_16_kv_heads():
+    """16 KV heads on 256 CUs (128 pieces a round): a plan of about 1.5
+    rounds of cost has 128 pieces of the full step, then the last round as 256
+    pieces of half of it; no first-half weighting (that is for one-round
+    plans), so each group is within a step of its share."""
+    from vllm_ascend_quantized_kv_cache.ops.kivi_decode import (
+        PAGE_TILE,
+        PIECE_MAX_COST,
+        TAIL_POSITION_COST,
+        DecodeSeq,
+        plan_decode_pieces,
+    )
+
+    per_round = 256 * 8 // 16
+    n = int(per_round * PIECE_MAX_COST * 1.5) // 64  # 1.5 rounds of cost over 64 requests
+    seqs = [DecodeSeq(n, ((n - 1) // 128) * 128, n - 128, i, 0, 0) for i in range(64)]
+    meta, work, pieces = plan_decode_pieces(seqs, 16, 256, tile=PAGE_TILE)
+    assert len(pieces) - 1 == per_round + 2 * per_round
+    cost = [
+        sum(-(-(e - p) // PAGE_TILE) * PAGE_TILE if k == 0 else (e - p) * TAIL_POSITION_COST
+            for _, p, e, k in work[pieces[i] : pieces[i + 1]].tolist())
+        for i in range(len(pieces) - 1)
+    ]
+    step = sum(cost) / (2 * per_round)
+    margin = PAGE_TILE + 2 * 32 * TAIL_POSITION_COST
+    assert all(abs(c - step) <= margin for c in cost[:per_round])
+    assert all(abs(c - step / 2) <= margin for c in cost[per_round:])
